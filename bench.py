@@ -1,0 +1,275 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV hot path: decode attention + KV append at Qwen3-1.7B shape.
+
+Workload (the metric's configuration): 28 layers, 16 query heads over 8 kv
+heads, head_dim 128; 32 sequences with contexts uniform in [256, 4096] (after the step's append), one
+new token each per step; f16 K/V in 16-token pages scattered by a seeded permutation of an 8,192-page
+pool (131,072 tokens: the "28k-token pool" of the config cannot hold the ~69.6k tokens the batch
+needs); q/k/v activations N(0, 1), resident in HBM before timing.
+
+A step is what a serving step does on this path: the host plans it (page allocation through the
+BlockManager, packing, one upload), then for each of the 28 layers the fused QK-norm + RoPE + KV
+append and the paged decode attention (+ split merge) run on the GPU. Contexts grow by one token per
+step, as in decoding.
+
+Prints one JSON line (the driver's contract); a human summary goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+N_LAYERS, H, KVH, D = 28, 16, 8, 128
+BATCH, CTX_LO, CTX_HI = 32, 256, 4096
+POOL_PAGES = 8192
+PAGE = 16
+SEED = 20261005
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+KV_BYTES_PER_TOKEN = 2 * KVH * D * 2  # f16 K + V of one token, one layer: 4096 B
+# Per new token per layer: qkv in 8 KiB + q out 4 KiB + KV append 4 KiB + q in 4 KiB + attention out 4 KiB.
+TOKEN_BYTES = 8192 + 4096 + 4096 + 4096 + 4096
+METRIC = "paged decode-attn+append tokens/s and % HBM peak (Qwen3-1.7B shape, batch 32)"
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Workload:
+    """Config 2 on the GPU path."""
+
+    def __init__(self, total_steps: int):
+        import torch
+
+        from ember_amd import BlockManager
+        from ember_amd.paged_kv import PagedKv
+
+        self.torch = torch
+        rng = np.random.default_rng(SEED)
+        self.ctx_after = rng.integers(CTX_LO, CTX_HI + 1, BATCH)  # context after the first step's append
+        self.ctx = self.ctx_after - 1                             # cached before the first step
+        max_ctx = int(self.ctx_after.max()) + total_steps + PAGE
+        self.max_blocks = (max_ctx + PAGE - 1) // PAGE
+        # Pages scattered over the pool: take every block, give them back in a seeded random order,
+        # so the allocator's free stack hands them out permuted.
+        self.bm = BlockManager(POOL_PAGES, False)
+        every = [self.bm.allocate() for _ in range(POOL_PAGES)]
+        self.bm.release_all([every[i] for i in rng.permutation(POOL_PAGES)])
+        self.blocks = [[] for _ in range(BATCH)]
+        for s in range(BATCH):
+            self._ensure(s, int(self.ctx[s]))
+        self.stream = torch.cuda.Stream()
+        self.kv = PagedKv(n_layers=N_LAYERS, n_heads=H, n_kv_heads=KVH, rms_eps=1e-6, rope_theta=1e6,
+                          max_position=self.max_blocks * PAGE, num_blocks=POOL_PAGES, max_batch_tokens=BATCH,
+                          max_seqs=BATCH, dtype=torch.float16, stream=self.stream)
+        g = torch.Generator(device="cuda").manual_seed(SEED)
+        with torch.cuda.stream(self.stream):
+            for layer in range(N_LAYERS):  # cached K/V: random f16 in every page (the values do not matter)
+                self.kv.pool_view(layer, "k").normal_(generator=g)
+                self.kv.pool_view(layer, "v").normal_(generator=g)
+            self.qkv = torch.randn((N_LAYERS, BATCH, (H + 2 * KVH) * D), generator=g, device="cuda",
+                                   dtype=torch.float16)
+            self.qn = 1 + 0.1 * torch.randn((N_LAYERS, D), generator=g, device="cuda")
+            self.kn = 1 + 0.1 * torch.randn((N_LAYERS, D), generator=g, device="cuda")
+            self.out = torch.empty((BATCH, H, D), device="cuda", dtype=torch.float16)
+        self.stream.synchronize()
+        self.sum_ctx_timed = 0
+        self.alloc_s = 0.0
+
+    def _ensure(self, s: int, upto: int) -> None:
+        need = (upto + PAGE - 1) // PAGE
+        while len(self.blocks[s]) < need:
+            b = self.bm.allocate()
+            if b < 0:
+                raise RuntimeError("the page pool is exhausted")
+            self.blocks[s].append(b)
+
+    def step(self) -> int:
+        from ember_amd.paged_kv import StepBatch
+
+        t0 = time.perf_counter()
+        for s in range(BATCH):
+            self._ensure(s, int(self.ctx[s]) + 1)
+        self.alloc_s += time.perf_counter() - t0
+        tables = np.zeros((BATCH, self.max_blocks), np.int32)
+        for s in range(BATCH):
+            tables[s, :len(self.blocks[s])] = self.blocks[s]
+        pos = self.ctx.astype(np.int32)
+        b = StepBatch(tokens=[0] * BATCH, positions=pos.tolist(), query_start=list(range(BATCH + 1)),
+                      context_len=(pos + 1).tolist(), block_tables=tables.reshape(-1).tolist(),
+                      max_blocks=self.max_blocks)
+        self.kv.plan(b)
+        for layer in range(N_LAYERS):
+            self.kv.layer(layer, self.qkv[layer], self.out, q_norm=self.qn[layer], k_norm=self.kn[layer])
+        self.ctx += 1
+        return int(pos.sum() + BATCH)  # sum of contexts after this step's append
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The oracle (the reference's f32 CPU path, restated) on one layer of the same batch, threads = the
+    host's CPU share. Reported as tokens/s for 28 layers (per-layer time x 28)."""
+    import oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    rng = np.random.default_rng(SEED)
+    ctx_after = rng.integers(CTX_LO, CTX_HI + 1, BATCH)
+    perm = rng.permutation(POOL_PAGES).astype(np.int32)
+    pages = (ctx_after + PAGE - 1) // PAGE
+    mb = int(pages.max()) + 1
+    tables = np.zeros((BATCH, mb), np.int32)
+    at = 0
+    for s in range(BATCH):
+        tables[s, :pages[s]] = perm[at:at + pages[s]]
+        at += pages[s]
+    k = rng.standard_normal((POOL_PAGES, KVH, PAGE, D), dtype=np.float32)
+    v = rng.standard_normal((POOL_PAGES, KVH, PAGE, D), dtype=np.float32)
+    qkv = rng.standard_normal((BATCH, (H + 2 * KVH) * D), dtype=np.float32)
+    inv = oracle.inv_freq(1e6, D)
+    ones = np.ones(D, np.float32)
+    pos = (ctx_after - 1).astype(np.int32)
+    qs = np.arange(BATCH + 1, dtype=np.int32)
+
+    def one_step():
+        q = oracle.append_layer(qkv, pos, qs, tables, k, v, n_heads=H, n_kv=KVH, inv_freq_=inv, q_norm=ones,
+                                k_norm=ones, num_blocks=POOL_PAGES, kv_f16=False)
+        oracle.attention_layer(q, pos, qs, tables, k, v, n_heads=H, n_kv=KVH, num_blocks=POOL_PAGES, kv_f16=False,
+                               threads=threads)
+
+    one_step()  # warm up (threads, pages)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+    per_layer = float(np.median(times))
+    cpu_model = ""
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                cpu_model = ln.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": BATCH / (per_layer * N_LAYERS),
+        "unit": "tokens/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"1 of {N_LAYERS} layers of the same 32-sequence batch (sum of contexts {int(ctx_after.sum())}), "
+                   f"f32 KV, median of {len(times)} steps ({per_layer * 1e3:.1f} ms/layer) x {N_LAYERS} layers; "
+                   f"{cpu_model or platform.processor()}"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this path has no multi-GPU "
+              "part to measure; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from ember_amd import lib
+
+    lib()  # fails loudly when the HIP library is not built
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    log(f"[bench] setting up config 2 ({N_LAYERS} layers, batch {BATCH}, {POOL_PAGES}-page pool)")
+    w = Workload(args.steps + args.warmup)
+    for _ in range(args.warmup):
+        w.step()
+    w.stream.synchronize()
+    w.kv.set_timing(True)
+    w.kv.timing()  # start from zero
+    w.alloc_s = 0.0
+    sum_ctx = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sum_ctx += w.step()
+    w.stream.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launches, kernel_ms = w.kv.timing()
+    w.kv.set_timing(False)
+
+    ms_per_step = wall * 1e3 / args.steps
+    tokens_s = BATCH * args.steps / wall
+    step_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + TOKEN_BYTES * BATCH)
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
+    # Decode kernel roofline: algorithmic bytes per launch = K+V of every context token + the queries.
+    kernel_bytes = KV_BYTES_PER_TOKEN * sum_ctx + 4096 * BATCH * args.steps  # over all timed launches / 28
+    kernel_bytes *= N_LAYERS
+    kernel_gbs = kernel_bytes / (kernel_ms * 1e-3) / 1e9 if kernel_ms > 0 else 0.0
+    log(f"[bench] {args.steps} steps in {wall:.3f} s: {ms_per_step:.3f} ms/step, {tokens_s:.0f} tokens/s, "
+        f"step {step_gbs:.0f} GB/s ({step_gbs / HBM_PEAK_GBS:.1%} of peak)")
+    log(f"[bench] paged_decode_kernel: {launches} launches, avg {kernel_ms / max(launches, 1) * 1e3:.1f} us, "
+        f"{kernel_gbs:.0f} GB/s ({kernel_gbs / HBM_PEAK_GBS:.1%}); host BlockManager {w.alloc_s / args.steps * 1e6:.1f} us/step")
+
+    cpu = None
+    if args.cpu_seconds > 0:
+        log("[bench] timing the CPU baseline (oracle, f32 KV)")
+        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu['value']:.1f} tokens/s on {cpu['cores']} threads")
+
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: N(0,1) q/k/v activations and random f16 K/V pages, seeded",
+        "config": {
+            "workload": "BASELINE configs[1]: batched paged decode, Qwen3-1.7B KV shape, 28 layers, "
+                        "16 q / 8 kv heads, d=128, 32 sequences, context U[256,4096], 1 new token each per step, "
+                        "f16 KV in 16-token pages scattered over an 8192-page pool",
+            "global_batch": BATCH,
+            "layers": N_LAYERS,
+            "accumulate": "f32",
+            "step_gb": round(step_bytes / 1e9, 4),
+            "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+            "host_blockmanager_us_per_step": round(w.alloc_s / args.steps * 1e6, 2),
+        },
+        "roofline": {
+            "kernel": "paged_decode_kernel",
+            "bound": "hbm",
+            "achieved": round(kernel_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+            "bytes_per_launch": round(kernel_bytes / max(launches, 1)),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

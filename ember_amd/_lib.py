@@ -1,0 +1,164 @@
+"""ctypes binding of include/ember_hip.h.
+
+The shared library is built in-tree by ember_amd.build (``__graft_entry__.build()``).
+There is no fallback: if the library is missing, loading raises, so nothing can
+silently run on another code path.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int32, c_int64, c_uint8, c_uint64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
+
+# Constants of include/ember_hip.h.
+ABI_VERSION = 1
+BLOCK_SIZE = 16
+PREFILL_TILE = 64
+MAX_RUN = 8
+OK = 0
+ERR_INVALID = -1
+DTYPE_F16 = 0
+DTYPE_F32 = 1
+
+
+class EmberError(RuntimeError):
+    """A failure reported through the C ABI (the reference's ember::Error)."""
+
+
+class QkvArgs(ctypes.Structure):
+    _fields_ = [
+        ("qkv", c_void_p), ("q_out", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("q_norm", c_void_p), ("k_norm", c_void_p), ("bias", c_void_p), ("inv_freq", c_void_p),
+        ("positions", c_void_p), ("token_seq", c_void_p), ("block_tables", c_void_p),
+        ("max_blocks", c_int32), ("T", c_int32), ("n_heads", c_int32), ("n_kv", c_int32), ("head_dim", c_int32),
+        ("eps", c_float), ("num_blocks", c_int32), ("dtype", c_int32),
+    ]
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("token_index", c_void_p), ("q", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("positions", c_void_p), ("token_seq", c_void_p), ("block_tables", c_void_p),
+        ("max_blocks", c_int32), ("T", c_int32), ("n_heads", c_int32), ("n_kv", c_int32), ("head_dim", c_int32),
+        ("scale", c_float), ("out", c_void_p), ("num_splits", c_int32), ("split_len", c_int32),
+        ("part_acc", c_void_p), ("part_ml", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
+        ("run_first", c_void_p), ("run_count", c_void_p), ("num_runs", c_int32), ("max_run", c_int32),
+    ]
+
+
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("tile_start", c_void_p), ("tile_end", c_void_p), ("tile_seq", c_void_p),
+        ("positions", c_void_p), ("block_tables", c_void_p),
+        ("num_tiles", c_int32), ("max_blocks", c_int32), ("n_heads", c_int32), ("n_kv", c_int32), ("head_dim", c_int32),
+        ("scale", c_float), ("out", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
+    ]
+
+
+class CopyArgs(ctypes.Structure):
+    _fields_ = [
+        ("k_cache", c_void_p), ("v_cache", c_void_p), ("src_blocks", c_void_p), ("dst_blocks", c_void_p),
+        ("n", c_int32), ("n_layers", c_int32), ("layer_stride", c_int64),
+        ("n_kv", c_int32), ("head_dim", c_int32), ("num_blocks", c_int32), ("dtype", c_int32),
+    ]
+
+
+class KvConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", c_int32), ("n_heads", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32),
+        ("rms_eps", c_float), ("rope_theta", c_double), ("max_position", c_int32), ("num_blocks", c_int32),
+        ("max_batch_tokens", c_int32), ("max_seqs", c_int32), ("dtype", c_int32), ("qk_norm", c_int32),
+        ("split_len", c_int32),
+    ]
+
+
+class StepBatchC(ctypes.Structure):
+    _fields_ = [
+        ("tokens", c_void_p), ("positions", c_void_p), ("query_start", c_void_p), ("context_len", c_void_p),
+        ("block_tables", c_void_p), ("num_tokens", c_int32), ("num_seqs", c_int32), ("max_blocks", c_int32),
+    ]
+
+
+STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC]
+
+# name -> (restype, argtypes); every extern "C" symbol of include/ember_hip.h.
+PROTOTYPES = {
+    "ember_hip_kv_append": (c_int32, [POINTER(QkvArgs), c_void_p]),
+    "ember_hip_paged_decode": (c_int32, [POINTER(AttnArgs), c_void_p]),
+    "ember_hip_prefill_attn": (c_int32, [POINTER(PrefillArgs), c_void_p]),
+    "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
+    "ember_hip_last_error": (c_char_p, []),
+    "ember_hip_abi_version": (c_int32, []),
+    "ember_hip_sizeof": (c_int32, [c_int32]),
+    "ember_bm_create": (c_void_p, [c_int32, c_int32]),
+    "ember_bm_destroy": (None, [c_void_p]),
+    "ember_bm_num_blocks": (c_int32, [c_void_p]),
+    "ember_bm_available": (c_int32, [c_void_p]),
+    "ember_bm_used": (c_int32, [c_void_p]),
+    "ember_bm_cached": (c_int32, [c_void_p]),
+    "ember_bm_allocate": (c_int32, [c_void_p]),
+    "ember_bm_release": (c_int32, [c_void_p, c_int32]),
+    "ember_bm_release_all": (c_int32, [c_void_p, POINTER(c_int32), c_int32]),
+    "ember_bm_block_hash": (c_uint64, [c_uint64, POINTER(c_int32), c_int32]),
+    "ember_bm_match_prefix": (c_int32, [c_void_p, POINTER(c_int32), c_int32, POINTER(c_int32)]),
+    "ember_bm_seal": (c_uint64, [c_void_p, c_int32, c_uint64, POINTER(c_int32), c_int32]),
+    "ember_bm_prefix_caching": (c_int32, [c_void_p]),
+    "ember_bm_refcount": (c_int32, [c_void_p, c_int32]),
+    "ember_bm_hit_tokens": (c_uint64, [c_void_p]),
+    "ember_bm_lookup_tokens": (c_uint64, [c_void_p]),
+    "ember_bm_check": (c_int32, [c_void_p, c_char_p, c_int32]),
+    "ember_bm_states": (None, [c_void_p, POINTER(c_uint8)]),
+    "ember_bm_share": (c_int32, [c_void_p, POINTER(c_int32), c_int32]),
+    "ember_bm_copy_on_write": (c_int32, [c_void_p, c_int32]),
+    "ember_kv_create": (c_void_p, [POINTER(KvConfig), c_void_p]),
+    "ember_kv_destroy": (None, [c_void_p]),
+    "ember_kv_plan": (c_int32, [c_void_p, POINTER(StepBatchC)]),
+    "ember_kv_layer": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ember_kv_copy_blocks": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), c_int32]),
+    "ember_kv_k_pool": (c_void_p, [c_void_p, c_int32]),
+    "ember_kv_v_pool": (c_void_p, [c_void_p, c_int32]),
+    "ember_kv_layer_stride": (c_int64, [c_void_p]),
+    "ember_kv_spare_block": (c_int32, [c_void_p]),
+    "ember_kv_plan_info": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "ember_kv_set_timing": (c_int32, [c_void_p, c_int32]),
+    "ember_kv_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
+}
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded libember_hip.so with every prototype set; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` first"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in PROTOTYPES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.ember_hip_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH} has ABI {handle.ember_hip_abi_version()}, expected {ABI_VERSION}")
+        for i, st in enumerate(STRUCTS):
+            if handle.ember_hip_sizeof(i) != ctypes.sizeof(st):
+                raise ImportError(f"struct layout mismatch for {st.__name__}")
+        _lib = handle
+    return _lib
+
+
+def last_error() -> str:
+    msg = lib().ember_hip_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(code: int, what: str = "") -> int:
+    """Raises EmberError for a negative or hipError_t return code."""
+    if code != OK:
+        raise EmberError(f"{what or 'ember'} failed ({code}): {last_error()}")
+    return code

@@ -1,0 +1,165 @@
+// C ABI of the kernel launchers (include/ember_hip.h, part 1): argument
+// validation, instance selection, error reporting. Nothing here throws; every
+// failure is a return code plus a per-thread message.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "capi_errors.hpp"
+#include "device.hpp"
+#include "ember_hip.h"
+#include "kernels.hpp"
+
+namespace ember::hip {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return EMBER_OK;
+    return set_error(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+}
+
+namespace {
+
+bool valid_dtype(int d) { return d == EMBER_DTYPE_F16 || d == EMBER_DTYPE_F32; }
+
+int check_heads(const char *who, int head_dim, int n_heads, int n_kv) {
+    if (head_dim != kHeadDim) return set_error(EMBER_ERR_INVALID, "%s: head_dim %d is not supported (128)", who, head_dim);
+    if (n_kv <= 0 || n_heads <= 0 || n_heads % n_kv != 0)
+        return set_error(EMBER_ERR_INVALID, "%s: %d query heads do not group over %d kv heads", who, n_heads, n_kv);
+    return EMBER_OK;
+}
+
+}  // namespace
+}  // namespace ember::hip
+
+using namespace ember::hip;
+
+extern "C" {
+
+const char *ember_hip_last_error(void) { return g_last_error.c_str(); }
+
+int ember_hip_abi_version(void) { return EMBER_ABI_VERSION; }
+
+int32_t ember_hip_sizeof(int32_t which) {
+    switch (which) {
+        case 0: return sizeof(EmberQkvArgs);
+        case 1: return sizeof(EmberAttnArgs);
+        case 2: return sizeof(EmberPrefillArgs);
+        case 3: return sizeof(EmberCopyArgs);
+        case 4: return sizeof(EmberKvConfig);
+        case 5: return sizeof(EmberStepBatch);
+        default: return -1;
+    }
+}
+
+int ember_hip_kv_append(const EmberQkvArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "kv_append: null arguments");
+    if (int e = check_heads("kv_append", a->head_dim, a->n_heads, a->n_kv)) return e;
+    if (a->n_heads > 64 || a->n_kv > 64)
+        return set_error(EMBER_ERR_INVALID, "kv_append: at most 64 query and 64 kv heads (got %d, %d)", a->n_heads, a->n_kv);
+    if (!valid_dtype(a->dtype)) return set_error(EMBER_ERR_INVALID, "kv_append: unknown dtype %d", a->dtype);
+    if (a->T < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
+        return set_error(EMBER_ERR_INVALID, "kv_append: bad sizes (T %d, max_blocks %d, num_blocks %d)", a->T, a->max_blocks,
+                         a->num_blocks);
+    if (a->T == 0) return EMBER_OK;
+    if (!a->qkv || !a->q_out || !a->k_cache || !a->v_cache || !a->inv_freq || !a->positions || !a->token_seq ||
+        !a->block_tables)
+        return set_error(EMBER_ERR_INVALID, "kv_append: a required pointer is null");
+    if ((a->q_norm == nullptr) != (a->k_norm == nullptr))
+        return set_error(EMBER_ERR_INVALID, "kv_append: q_norm and k_norm go together");
+    return hip_status(launch_kv_append(*a, static_cast<hipStream_t>(stream)), "kv_append");
+}
+
+int ember_hip_paged_decode(const EmberAttnArgs *a, void *stream) {
+    return paged_decode(a, static_cast<hipStream_t>(stream), nullptr);
+}
+
+}  // extern "C"
+
+int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t main_done) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "paged_decode: null arguments");
+    if (int e = check_heads("paged_decode", a->head_dim, a->n_heads, a->n_kv)) return e;
+    const int G = a->n_heads / a->n_kv;
+    if (G > 8) return set_error(EMBER_ERR_INVALID, "paged_decode: query heads per kv head must be 1..8 (got %d)", G);
+    if (!valid_dtype(a->dtype)) return set_error(EMBER_ERR_INVALID, "paged_decode: unknown dtype %d", a->dtype);
+    if (a->T < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
+        return set_error(EMBER_ERR_INVALID, "paged_decode: bad sizes");
+    if (a->num_splits < 1 || a->num_splits > 65535 || a->split_len < kPage || a->split_len % kPage != 0)
+        return set_error(EMBER_ERR_INVALID, "paged_decode: split_len must be a positive multiple of 16 (got %d x %d)",
+                         a->num_splits, a->split_len);
+    if (a->T == 0) return EMBER_OK;
+    if (!a->q || !a->k_cache || !a->v_cache || !a->positions || !a->token_seq || !a->block_tables || !a->out)
+        return set_error(EMBER_ERR_INVALID, "paged_decode: a required pointer is null");
+    if (a->num_splits > 1 && (!a->part_acc || !a->part_ml))
+        return set_error(EMBER_ERR_INVALID, "paged_decode: split scratch is required when num_splits > 1");
+    int max_run = 1;
+    if (a->run_first) {
+        if (!a->run_count || a->num_runs < 0 || a->num_runs > a->T)
+            return set_error(EMBER_ERR_INVALID, "paged_decode: run_first needs run_count and 0 <= num_runs <= T");
+        if (a->max_run < 1 || a->max_run > EMBER_MAX_RUN)
+            return set_error(EMBER_ERR_INVALID, "paged_decode: max_run must be 1..%d (got %d)", EMBER_MAX_RUN, a->max_run);
+        max_run = a->max_run;
+    }
+    const int need = G * max_run;
+    int rows = 0;
+    for (int r : kDecodeRowInstances)
+        if (r >= need) {
+            rows = r;
+            break;
+        }
+    if (!rows) return set_error(EMBER_ERR_INVALID, "paged_decode: %d query rows per work-group exceed 16", need);
+    return hip_status(launch_paged_decode(*a, rows, stream, main_done), "paged_decode");
+}
+
+extern "C" {
+
+int ember_hip_prefill_attn(const EmberPrefillArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "prefill_attn: null arguments");
+    if (int e = check_heads("prefill_attn", a->head_dim, a->n_heads, a->n_kv)) return e;
+    const int G = a->n_heads / a->n_kv;
+    if (G > 4) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1, 2 or 4 (got %d)", G);
+    if (G == 3) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1, 2 or 4 (got 3)");
+    if (a->dtype != EMBER_DTYPE_F16) return set_error(EMBER_ERR_INVALID, "prefill_attn: the MFMA path takes f16 only");
+    if (a->num_tiles < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: bad sizes");
+    if (a->num_tiles == 0) return EMBER_OK;
+    if (!a->q || !a->k_cache || !a->v_cache || !a->tile_start || !a->tile_end || !a->tile_seq || !a->positions ||
+        !a->block_tables || !a->out)
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: a required pointer is null");
+    return hip_status(launch_prefill(*a, static_cast<hipStream_t>(stream)), "prefill_attn");
+}
+
+int ember_hip_copy_pages(const EmberCopyArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "copy_pages: null arguments");
+    if (!valid_dtype(a->dtype)) return set_error(EMBER_ERR_INVALID, "copy_pages: unknown dtype %d", a->dtype);
+    if (a->n < 0 || a->n_layers < 0 || a->n_kv <= 0 || a->head_dim <= 0 || a->num_blocks <= 0 || a->layer_stride < 0)
+        return set_error(EMBER_ERR_INVALID, "copy_pages: bad sizes");
+    if (a->n == 0 || a->n_layers == 0) return EMBER_OK;
+    const long long elem = a->dtype == EMBER_DTYPE_F16 ? 2 : 4;
+    if ((static_cast<long long>(a->n_kv) * kPage * a->head_dim * elem) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "copy_pages: a page must be a multiple of 16 bytes");
+    if (a->layer_stride < static_cast<long long>(a->num_blocks) * a->n_kv * kPage * a->head_dim)
+        return set_error(EMBER_ERR_INVALID, "copy_pages: layer_stride is smaller than a layer's pool");
+    if (!a->k_cache || !a->v_cache || !a->src_blocks || !a->dst_blocks)
+        return set_error(EMBER_ERR_INVALID, "copy_pages: a required pointer is null");
+    return hip_status(launch_copy_pages(*a, static_cast<hipStream_t>(stream)), "copy_pages");
+}
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+// Device-side helpers shared by the gfx950 kernels of the paged-KV path.
+//
+// Everything here is written for CDNA4's 64-wide waves: cross-lane traffic
+// inside a 16-lane row uses DPP (row/quad permutations folded into the VALU
+// op), wider exchanges use ds_bpermute through __shfl_xor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ember::hip {
+
+constexpr int kPage = 16;         // tokens per KV page (kBlockSize)
+constexpr int kHeadDim = 128;     // the only head_dim the kernels are built for
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kHalfMax = 65504.0f;
+
+using f16 = _Float16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// DPP move of a float (row_mask, bank_mask all on; every source lane exists
+// for the quad/mirror patterns used here).
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+constexpr int kDppQuadXor1 = 0xb1;     // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4e;     // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the same,
+// bit-identical result (each step adds two values that both partner lanes
+// hold, and float addition is commutative).
+__device__ __forceinline__ float row16_sum(float x) {
+    x = x + dpp_mov<kDppQuadXor1>(x);
+    x = x + dpp_mov<kDppQuadXor2>(x);
+    x = x + dpp_mov<kDppRowHalfMirror>(x);
+    x = x + dpp_mov<kDppRowMirror>(x);
+    return x;
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, kWave);
+    return x;
+}
+
+__device__ __forceinline__ float clamp_half(float x) { return fminf(fmaxf(x, -kHalfMax), kHalfMax); }
+
+// f16 <-> f32 element conversion for the templated (f16 / f32) kernels.
+template <typename T>
+__device__ __forceinline__ float to_f32(T x) {
+    return static_cast<float>(x);
+}
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+    return static_cast<T>(x);  // f16: v_cvt_f16_f32, round to nearest even
+}
+
+}  // namespace ember::hip

@@ -1,0 +1,336 @@
+// The paged-KV path's host side: pool allocation, the step plan and the
+// per-layer launches through the C ABI.
+#include "backend/hip_paged_kv.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "common/error.hpp"
+#include "kernels.hpp"
+
+#define EMBER_HIP_CHECK(expr)                                                                       \
+    do {                                                                                            \
+        hipError_t err_ = (expr);                                                                   \
+        if (err_ != hipSuccess) ::ember::fail("{} failed: {}", #expr, hipGetErrorString(err_));       \
+    } while (0)
+
+namespace ember {
+
+namespace {
+
+void check_abi(int code, const char *what) {
+    if (code != EMBER_OK) fail("{}: {}", what, ember_hip_last_error());
+}
+
+template <class T>
+T *device_alloc(size_t count) {
+    void *p = nullptr;
+    EMBER_HIP_CHECK(hipMalloc(&p, std::max<size_t>(count, 1) * sizeof(T)));
+    return static_cast<T *>(p);
+}
+
+size_t pad32(size_t n) { return (n + 31) & ~size_t(31); }
+
+}  // namespace
+
+HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStream_t stream)
+    : cfg_(cfg), opt_(opt), stream_(stream) {
+    EMBER_CHECK(cfg_.head_dim == 128, "the paged-KV path needs head_dim 128 (got {})", cfg_.head_dim);
+    EMBER_CHECK(cfg_.n_layers > 0 && cfg_.n_kv_heads > 0 && cfg_.n_heads % cfg_.n_kv_heads == 0 &&
+                    cfg_.group() >= 1 && cfg_.group() <= 8,
+                "unsupported head layout: {} query heads over {} kv heads", cfg_.n_heads, cfg_.n_kv_heads);
+    EMBER_CHECK(opt_.num_blocks > 0, "the KV cache has no blocks");
+    EMBER_CHECK(opt_.dtype == EMBER_DTYPE_F16 || opt_.dtype == EMBER_DTYPE_F32, "unknown dtype {}", opt_.dtype);
+    if (opt_.split_len <= 0) opt_.split_len = 512;
+    EMBER_CHECK(opt_.split_len % kBlockSize == 0, "split_len {} is not a multiple of {}", opt_.split_len, kBlockSize);
+    EMBER_CHECK(opt_.max_batch_tokens > 0 && opt_.max_seqs > 0, "bad batch limits");
+    EMBER_CHECK(cfg_.max_position > 0, "max_position must be set");
+    elem_ = opt_.dtype == EMBER_DTYPE_F16 ? 2 : 4;
+
+    const int64_t block_elems = static_cast<int64_t>(cfg_.n_kv_heads) * kBlockSize * cfg_.head_dim;
+    layer_elems_ = block_elems * (opt_.num_blocks + 1);  // + the spare block
+    const size_t pool_bytes = static_cast<size_t>(layer_elems_) * cfg_.n_layers * elem_;
+    EMBER_HIP_CHECK(hipMalloc(&k_, pool_bytes));
+    EMBER_HIP_CHECK(hipMalloc(&v_, pool_bytes));
+    EMBER_HIP_CHECK(hipMemsetAsync(k_, 0, pool_bytes, stream_));  // unwritten slots read as 0
+    EMBER_HIP_CHECK(hipMemsetAsync(v_, 0, pool_bytes, stream_));
+
+    const size_t T = static_cast<size_t>(opt_.max_batch_tokens);
+    EMBER_HIP_CHECK(hipMalloc(&q_, T * cfg_.n_heads * cfg_.head_dim * elem_));
+    max_blocks_per_seq_ = (cfg_.max_position + kBlockSize - 1) / kBlockSize;
+    max_splits_ = (max_blocks_per_seq_ * kBlockSize + opt_.split_len - 1) / opt_.split_len;
+    const size_t part_rows = T * cfg_.n_heads * static_cast<size_t>(max_splits_);
+    part_acc_ = device_alloc<float>(part_rows * cfg_.head_dim);
+    part_ml_ = device_alloc<float>(part_rows * 2);
+
+    std::vector<float> inv(static_cast<size_t>(cfg_.head_dim / 2));
+    for (int i = 0; i < cfg_.head_dim / 2; i++)  // f32, as the reference computes it (cpu_backend.cpp:85-88)
+        inv[static_cast<size_t>(i)] = 1.0f / std::pow(static_cast<float>(cfg_.rope_theta),
+                                                      static_cast<float>(2 * i) / static_cast<float>(cfg_.head_dim));
+    inv_freq_ = device_alloc<float>(inv.size());
+    EMBER_HIP_CHECK(hipMemcpyAsync(inv_freq_, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice, stream_));
+
+    // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables.
+    ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
+                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + 64;
+    dev_ints_ = device_alloc<int32_t>(ints_capacity_);
+    for (int i = 0; i < 2; i++) {
+        EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
+        EMBER_HIP_CHECK(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming));
+    }
+    EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
+}
+
+HipPagedKv::~HipPagedKv() {
+    (void)hipStreamSynchronize(stream_);
+    for (hipEvent_t e : timing_events_) (void)hipEventDestroy(e);
+    for (int i = 0; i < 2; i++) {
+        if (staged_[i]) (void)hipEventDestroy(staged_[i]);
+        if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
+    }
+    for (void *p : {k_, v_, q_, static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
+                    static_cast<void *>(part_ml_), static_cast<void *>(dev_ints_)})
+        if (p) (void)hipFree(p);
+}
+
+void *HipPagedKv::k_pool(int layer) const {
+    EMBER_CHECK(layer >= 0 && layer < cfg_.n_layers, "layer {} out of range", layer);
+    return static_cast<char *>(k_) + static_cast<size_t>(layer) * layer_elems_ * elem_;
+}
+
+void *HipPagedKv::v_pool(int layer) const {
+    EMBER_CHECK(layer >= 0 && layer < cfg_.n_layers, "layer {} out of range", layer);
+    return static_cast<char *>(v_) + static_cast<size_t>(layer) * layer_elems_ * elem_;
+}
+
+void HipPagedKv::plan(const StepBatch &b) {
+    const int T = b.num_tokens(), S = b.num_seqs();
+    EMBER_CHECK(T > 0 && T <= opt_.max_batch_tokens, "batch of {} tokens (limit {})", T, opt_.max_batch_tokens);
+    EMBER_CHECK(S > 0 && S <= opt_.max_seqs, "batch of {} sequences (limit {})", S, opt_.max_seqs);
+    EMBER_CHECK(static_cast<int>(b.query_start.size()) == S + 1 && b.query_start[0] == 0 && b.query_start[S] == T,
+                "malformed query_start");
+    EMBER_CHECK(static_cast<int>(b.positions.size()) == T, "malformed positions");
+    EMBER_CHECK(b.max_blocks > 0 && b.max_blocks <= max_blocks_per_seq_ &&
+                    static_cast<int64_t>(b.block_tables.size()) == static_cast<int64_t>(S) * b.max_blocks,
+                "malformed block tables ({} x {}, at most {} blocks per sequence)", S, b.max_blocks, max_blocks_per_seq_);
+
+    token_seq_.assign(static_cast<size_t>(T), 0);
+    decode_.clear();
+    run_first_.clear();
+    run_count_.clear();
+    tile_start_.clear();
+    tile_end_.clear();
+    tile_seq_.clear();
+    int max_ctx = 0;
+    max_run_ = 1;
+    for (int s = 0; s < S; s++) {
+        const int q0 = b.query_start[static_cast<size_t>(s)], q1 = b.query_start[static_cast<size_t>(s) + 1];
+        EMBER_CHECK(q0 <= q1, "malformed query_start");
+        int ctx = 0;
+        for (int t = q0; t < q1; t++) {
+            token_seq_[static_cast<size_t>(t)] = s;
+            const int pos = b.positions[static_cast<size_t>(t)];
+            EMBER_CHECK(pos >= 0 && pos < b.max_blocks * kBlockSize, "token {} at position {} is beyond its block table", t,
+                        pos);
+            ctx = std::max(ctx, pos + 1);
+        }
+        // Every page a token of this sequence reads must be a real block (or the spare).
+        const int32_t *row = &b.block_tables[static_cast<size_t>(s) * b.max_blocks];
+        for (int p = 0; p * kBlockSize < ctx; p++)
+            EMBER_CHECK(row[p] >= 0 && row[p] <= opt_.num_blocks, "sequence {} page {} names block {} (pool of {})", s, p,
+                        row[p], opt_.num_blocks);
+        if (q1 - q0 >= kFlashMinTokens && opt_.use_prefill_kernel) {
+            for (int t = q0; t < q1; t += EMBER_PREFILL_TILE) {
+                tile_start_.push_back(t);
+                tile_end_.push_back(std::min(q1, t + EMBER_PREFILL_TILE));
+                tile_seq_.push_back(s);
+            }
+        } else {
+            for (int t = q0; t < q1; t += EMBER_MAX_RUN) {
+                const int n = std::min(EMBER_MAX_RUN, q1 - t);
+                run_first_.push_back(static_cast<int32_t>(decode_.size()));
+                run_count_.push_back(n);
+                max_run_ = std::max(max_run_, n);
+                for (int i = 0; i < n; i++) decode_.push_back(t + i);
+            }
+            if (q1 > q0) max_ctx = std::max(max_ctx, ctx);
+        }
+    }
+    T_ = T;
+    max_blocks_ = b.max_blocks;
+    decode_count_ = static_cast<int>(decode_.size());
+    decode_runs_ = static_cast<int>(run_first_.size());
+    tiles_ = static_cast<int>(tile_start_.size());
+    splits_ = std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
+
+    // Pack into the staging buffer (wait until its previous upload has run), then one copy.
+    stage_ ^= 1;
+    EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));
+    int32_t *hp = host_ints_[stage_];
+    size_t off = 0;
+    std::vector<size_t> at;
+    auto put = [&](const int32_t *src, size_t n) {
+        at.push_back(off);
+        if (n) std::memcpy(hp + off, src, n * sizeof(int32_t));
+        off += pad32(n);
+    };
+    put(b.positions.data(), static_cast<size_t>(T));
+    put(token_seq_.data(), static_cast<size_t>(T));
+    put(b.block_tables.data(), b.block_tables.size());
+    put(decode_.data(), decode_.size());
+    put(run_first_.data(), run_first_.size());
+    put(run_count_.data(), run_count_.size());
+    put(tile_start_.data(), tile_start_.size());
+    put(tile_end_.data(), tile_end_.size());
+    put(tile_seq_.data(), tile_seq_.size());
+    EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
+    EMBER_HIP_CHECK(hipMemcpyAsync(dev_ints_, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+    EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], stream_));
+    d_positions_ = dev_ints_ + at[0];
+    d_token_seq_ = dev_ints_ + at[1];
+    d_tables_ = dev_ints_ + at[2];
+    d_decode_ = dev_ints_ + at[3];
+    d_run_first_ = dev_ints_ + at[4];
+    d_run_count_ = dev_ints_ + at[5];
+    d_tile_start_ = dev_ints_ + at[6];
+    d_tile_end_ = dev_ints_ + at[7];
+    d_tile_seq_ = dev_ints_ + at[8];
+}
+
+void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {
+    EMBER_CHECK(T_ > 0, "layer() before plan()");
+    EMBER_CHECK(qkv && out, "layer(): null qkv or out");
+    void *kc = k_pool(l), *vc = v_pool(l);
+
+    EmberQkvArgs qa{};
+    qa.qkv = qkv;
+    qa.q_out = q_;
+    qa.k_cache = kc;
+    qa.v_cache = vc;
+    qa.q_norm = q_norm;
+    qa.k_norm = k_norm;
+    qa.bias = bias;
+    qa.inv_freq = inv_freq_;
+    qa.positions = d_positions_;
+    qa.token_seq = d_token_seq_;
+    qa.block_tables = d_tables_;
+    qa.max_blocks = max_blocks_;
+    qa.T = T_;
+    qa.n_heads = cfg_.n_heads;
+    qa.n_kv = cfg_.n_kv_heads;
+    qa.head_dim = cfg_.head_dim;
+    qa.eps = cfg_.rms_eps;
+    qa.num_blocks = opt_.num_blocks + 1;
+    qa.dtype = opt_.dtype;
+    check_abi(ember_hip_kv_append(&qa, stream_), "kv_append");
+
+    const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
+    if (decode_runs_ > 0) {
+        EmberAttnArgs at{};
+        at.token_index = d_decode_;
+        at.q = q_;
+        at.k_cache = kc;
+        at.v_cache = vc;
+        at.positions = d_positions_;
+        at.token_seq = d_token_seq_;
+        at.block_tables = d_tables_;
+        at.max_blocks = max_blocks_;
+        at.T = decode_count_;
+        at.n_heads = cfg_.n_heads;
+        at.n_kv = cfg_.n_kv_heads;
+        at.head_dim = cfg_.head_dim;
+        at.scale = scale;
+        at.out = out;
+        at.num_splits = splits_;
+        at.split_len = opt_.split_len;
+        at.part_acc = part_acc_;
+        at.part_ml = part_ml_;
+        at.num_blocks = opt_.num_blocks + 1;
+        at.dtype = opt_.dtype;
+        at.run_first = d_run_first_;
+        at.run_count = d_run_count_;
+        at.num_runs = decode_runs_;
+        at.max_run = max_run_;
+        hipEvent_t stop = nullptr;
+        if (timing_) {
+            if (timing_used_ + 2 > timing_events_.size())
+                for (int i = 0; i < 2; i++) {
+                    hipEvent_t e;
+                    EMBER_HIP_CHECK(hipEventCreate(&e));
+                    timing_events_.push_back(e);
+                }
+            EMBER_HIP_CHECK(hipEventRecord(timing_events_[timing_used_], stream_));
+            stop = timing_events_[timing_used_ + 1];
+            timing_used_ += 2;
+        }
+        check_abi(hip::paged_decode(&at, stream_, stop), "paged_decode");
+    }
+    if (tiles_ > 0) {
+        EmberPrefillArgs pa{};
+        pa.q = q_;
+        pa.k_cache = kc;
+        pa.v_cache = vc;
+        pa.tile_start = d_tile_start_;
+        pa.tile_end = d_tile_end_;
+        pa.tile_seq = d_tile_seq_;
+        pa.positions = d_positions_;
+        pa.block_tables = d_tables_;
+        pa.num_tiles = tiles_;
+        pa.max_blocks = max_blocks_;
+        pa.n_heads = cfg_.n_heads;
+        pa.n_kv = cfg_.n_kv_heads;
+        pa.head_dim = cfg_.head_dim;
+        pa.scale = scale;
+        pa.out = out;
+        pa.num_blocks = opt_.num_blocks + 1;
+        pa.dtype = opt_.dtype;
+        check_abi(ember_hip_prefill_attn(&pa, stream_), "prefill_attn");
+    }
+}
+
+int HipPagedKv::collect_timing(double *total_ms) {
+    double ms = 0;
+    for (size_t i = 0; i + 1 < timing_used_; i += 2) {
+        EMBER_HIP_CHECK(hipEventSynchronize(timing_events_[i + 1]));
+        float one = 0;
+        EMBER_HIP_CHECK(hipEventElapsedTime(&one, timing_events_[i], timing_events_[i + 1]));
+        ms += one;
+    }
+    const int launches = static_cast<int>(timing_used_ / 2);
+    timing_used_ = 0;
+    if (total_ms) *total_ms = ms;
+    return launches;
+}
+
+void HipPagedKv::copy_blocks(std::span<const int32_t> src, std::span<const int32_t> dst) {
+    EMBER_CHECK(src.size() == dst.size(), "copy_blocks: {} sources for {} destinations", src.size(), dst.size());
+    if (src.empty()) return;
+    for (size_t i = 0; i < src.size(); i++)
+        EMBER_CHECK(src[i] >= 0 && src[i] <= opt_.num_blocks && dst[i] >= 0 && dst[i] <= opt_.num_blocks,
+                    "copy_blocks: pair {} ({} -> {}) is outside the pool", i, src[i], dst[i]);
+    const size_t n = src.size();
+    std::vector<int32_t> packed(2 * n);
+    std::copy(src.begin(), src.end(), packed.begin());
+    std::copy(dst.begin(), dst.end(), packed.begin() + static_cast<ptrdiff_t>(n));
+    int32_t *dev = device_alloc<int32_t>(2 * n);
+    EMBER_HIP_CHECK(hipMemcpyAsync(dev, packed.data(), 2 * n * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+    EmberCopyArgs ca{};
+    ca.k_cache = k_;
+    ca.v_cache = v_;
+    ca.src_blocks = dev;
+    ca.dst_blocks = dev + n;
+    ca.n = static_cast<int32_t>(n);
+    ca.n_layers = cfg_.n_layers;
+    ca.layer_stride = layer_elems_;
+    ca.n_kv = cfg_.n_kv_heads;
+    ca.head_dim = cfg_.head_dim;
+    ca.num_blocks = opt_.num_blocks + 1;
+    ca.dtype = opt_.dtype;
+    const int code = ember_hip_copy_pages(&ca, stream_);
+    EMBER_HIP_CHECK(hipStreamSynchronize(stream_));  // the pair list is freed below
+    (void)hipFree(dev);
+    check_abi(code, "copy_pages");
+}
+
+}  // namespace ember

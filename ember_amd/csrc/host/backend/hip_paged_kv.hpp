@@ -1,0 +1,100 @@
+// The paged-KV hot path of a HIP backend: what the reference's CudaBackend
+// does around its attention kernels (src/backend/cuda/cuda_backend.cu:134-205
+// forward: packing, routing, splits, one upload; :288-374 enqueue: the
+// per-layer append + attention; :757-780 the KV pool), on MI355X.
+//
+// Pools: K and V separately, each [layer][block][kv_head][slot][head_dim]
+// with num_blocks + 1 blocks per layer; the last one is a spare block the
+// engine never hands out (padding rows of captured decode steps write there).
+// Pools are zeroed at creation, so slots never written read as 0.
+//
+// Routing: a sequence with >= 16 new tokens goes to 64-token MFMA prefill
+// tiles when that kernel is available; every other run is cut into runs of at
+// most 8 tokens for the paged decode kernel, which reads each page once per
+// run. Decode splits are fixed 512-key chunks ([0, 512), [512, 1024), ...)
+// at every batch size, so a token's result never depends on its batch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <span>
+#include <vector>
+
+#include "backend/backend.hpp"
+#include "ember_hip.h"
+
+namespace ember {
+
+struct PagedKvOptions {
+    int num_blocks = 0;         // blocks the engine may hand out
+    int max_batch_tokens = 2048;
+    int max_seqs = 64;
+    int dtype = EMBER_DTYPE_F16;
+    int split_len = 512;
+    bool use_prefill_kernel = false;  // route runs of >= 16 tokens to MFMA tiles
+};
+
+class HipPagedKv {
+public:
+    static constexpr int kFlashMinTokens = 16;  // a run this long uses prefill tiles (cuda_backend.cu:257)
+
+    HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStream_t stream);
+    ~HipPagedKv();
+    HipPagedKv(const HipPagedKv &) = delete;
+    HipPagedKv &operator=(const HipPagedKv &) = delete;
+
+    // Packs and uploads the step's integers and decides the launches.
+    void plan(const StepBatch &b);
+    // Layer `layer` of the planned step: K/V of every new token into the
+    // pools, then attention of every token into out [T, n_heads, head_dim].
+    void layer(int layer, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out);
+    // Device copies of whole pages, src[i] -> dst[i], all layers, K and V.
+    void copy_blocks(std::span<const int32_t> src, std::span<const int32_t> dst);
+
+    void *k_pool(int layer) const;
+    void *v_pool(int layer) const;
+    int64_t layer_stride() const { return layer_elems_; }
+    int spare_block() const { return opt_.num_blocks; }
+    int decode_runs() const { return decode_runs_; }
+    int prefill_tiles() const { return tiles_; }
+    int num_splits() const { return splits_; }
+    hipStream_t stream() const { return stream_; }
+
+    // Benchmark timing of the paged-decode kernel (events around each launch).
+    void set_timing(bool on) { timing_ = on; }
+    // Waits for the recorded launches; returns their count and total ms, then starts over.
+    int collect_timing(double *total_ms);
+
+private:
+    int32_t *upload(size_t count);  // copies host_ints_[0, count) to the device, returns its device address
+
+    ModelConfig cfg_;
+    PagedKvOptions opt_;
+    hipStream_t stream_;
+    size_t elem_ = 2;
+    int64_t layer_elems_ = 0;       // elements of one layer's K (or V) pool
+    int max_blocks_per_seq_ = 0;
+    int max_splits_ = 0;
+
+    void *k_ = nullptr, *v_ = nullptr, *q_ = nullptr;
+    float *inv_freq_ = nullptr, *part_acc_ = nullptr, *part_ml_ = nullptr;
+    int32_t *dev_ints_ = nullptr;   // this step's integers
+    int32_t *host_ints_[2] = {nullptr, nullptr};  // pinned staging, alternating
+    hipEvent_t staged_[2] = {nullptr, nullptr};   // the upload from each staging buffer has run
+    int stage_ = 0;
+    size_t ints_capacity_ = 0;
+
+    // The current plan (device addresses into dev_ints_).
+    int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;
+    const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
+                  *d_run_first_ = nullptr, *d_run_count_ = nullptr, *d_tile_start_ = nullptr, *d_tile_end_ = nullptr,
+                  *d_tile_seq_ = nullptr;
+    std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, tile_start_, tile_end_, tile_seq_;
+
+    bool timing_ = false;
+    std::vector<hipEvent_t> timing_events_;  // start/stop pairs, reused after collect_timing
+    size_t timing_used_ = 0;
+};
+
+}  // namespace ember

@@ -1,0 +1,38 @@
+// The model hyperparameters the paged-KV path reads. Same fields and helpers
+// as the reference's ModelConfig (src/model/config.hpp:12-43) so that
+// backend.hpp keeps its shape; reading config.json (from_json / load) belongs
+// to the model-IO layer, which this build does not include.
+#pragma once
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+namespace ember {
+
+struct ModelConfig {
+    std::string arch;        // "qwen3", "qwen2", "llama"
+    int vocab_size = 0;
+    int hidden = 0;
+    int intermediate = 0;
+    int n_layers = 0;
+    int n_heads = 0;         // query heads
+    int n_kv_heads = 0;      // key/value heads (GQA)
+    int head_dim = 0;
+    float rms_eps = 1e-6f;
+    double rope_theta = 10000.0;
+    int max_position = 0;
+    bool tie_embeddings = false;
+    bool qk_norm = false;    // RMSNorm on each query/key head before RoPE (Qwen3)
+    bool qkv_bias = false;   // biases on the q/k/v projections (Qwen2)
+    std::vector<int> eos_ids;
+
+    int q_dim() const { return n_heads * head_dim; }
+    int kv_dim() const { return n_kv_heads * head_dim; }
+    int group() const { return n_heads / n_kv_heads; }
+
+    // Bytes of K+V per token over all layers at elem_bytes per element.
+    int64_t kv_bytes_per_token(int elem_bytes) const { return 2LL * n_layers * kv_dim() * elem_bytes; }
+};
+
+}  // namespace ember

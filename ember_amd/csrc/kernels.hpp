@@ -1,0 +1,31 @@
+// Internal launchers of the gfx950 kernels. The C ABI (capi.hip) validates
+// arguments and calls these; each enqueues on `stream` and returns the launch
+// status.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "ember_hip.h"
+
+namespace ember::hip {
+
+hipError_t launch_kv_append(const EmberQkvArgs &a, hipStream_t stream);
+
+// Decode attention (+ the split merge when a.num_splits > 1). `rows` is the
+// kernel's query-row capacity, G * max_run rounded up to a built instance.
+// When `main_done` is given it is recorded right after the attention kernel,
+// before the merge.
+hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t main_done = nullptr);
+
+// Validation + launch behind ember_hip_paged_decode, for in-library callers
+// that want the `main_done` event. Returns an EMBER_* / hipError_t code.
+int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t main_done);
+
+hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream);
+
+hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
+
+// Row capacities with a built decode kernel, ascending.
+constexpr int kDecodeRowInstances[] = {1, 2, 4, 8, 10, 16};
+
+}  // namespace ember::hip

@@ -1,0 +1,428 @@
+// Paged decode attention on gfx950 VALU (no MFMA): a bandwidth-bound gather.
+//
+// Replaces the reference's paged_attention_kernel + combine_splits_kernel
+// (src/backend/cuda/k_attention.cu:29-201). Semantics kept: GQA with the G
+// query heads of a kv head in one work-group (each page is read once for
+// all of them), softmax in base 2 with the scale folded in, fixed context
+// splits merged in a fixed order (batch invariance), slots past a query's
+// position never contribute.
+//
+// Work-group = 4 waves per (query run, kv head, context split). A run is 1..8
+// consecutive tokens of one sequence (decode: 1; speculative verify: k + 1);
+// all of them are served by the same page reads.
+//
+// Page walk: wave w takes pages first + w, first + w + 4, ... A page of one kv
+// head is 16 keys x 128 dims, contiguous (4 KiB in f16). Its load is four
+// dwordx4 instructions per lane, instruction i covering bytes [1024 i, 1024 i
+// + 1024) with lane l at offset 16 l: fully coalesced. So lane l = 16 r + c
+// holds dims [8c, 8c + 8) of keys 4i + r (i = 0..3), for K and for V.
+//   scores: an 8-dim partial dot per key (v_dot2_f32_f16 in the f16 path),
+//           summed over the 16 lanes of DPP row r - every lane of the row then
+//           holds the full score of its 4 keys;
+//   softmax: each DPP row keeps its own running max / sum over the keys it
+//           holds (no cross-row traffic in the loop);
+//   values: each lane accumulates its 8 dims over its 4 keys.
+// At the end: rows merge through two lane exchanges, waves through LDS,
+// splits in the separate merge kernel, all in a fixed order.
+//
+// Exactness of runs: a query row's arithmetic is the same whether its token is
+// alone or in a run. Pages entirely below the run's lowest position take a
+// path with no masking at all; later pages mask per row with selects, so a key
+// past a row's position leaves that row's state bit-for-bit unchanged, and a
+// page with no visible key for a row is an exact no-op for it (correction
+// factor 1 exactly, zero weights). Hence verify of k + 1 tokens equals k + 1
+// single-token decode steps bit-exactly.
+#include <climits>
+
+#include "device.hpp"
+#include "kernels.hpp"
+
+namespace ember::hip {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
+
+struct DecodeParams {
+    const void *q, *k, *v;
+    const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count;
+    void *out;
+    float *part_acc, *part_ml;
+    int max_blocks, n_heads, n_kv, G, num_blocks, num_splits, split_len;
+    float scale_log2;
+};
+
+// One page of K and V as this lane holds it: 4 keys x 8 dims each.
+template <typename T>
+struct PageRegs;
+
+template <>
+struct PageRegs<f16> {
+    uint4 k[4], v[4];
+    bool ok;
+};
+
+template <>
+struct PageRegs<float> {
+    float4 k[4][2], v[4][2];
+    bool ok;
+};
+
+template <typename T>
+__device__ __forceinline__ void load_page(PageRegs<T> &pr, const DecodeParams &p, const int32_t *table, int kvh, int page,
+                                          int lane) {
+    const int blk = table[page];
+    pr.ok = blk >= 0 && blk < p.num_blocks;
+    const int64_t base = (static_cast<int64_t>(pr.ok ? blk : 0) * p.n_kv + kvh) * (kPage * kHeadDim) + 8 * lane;
+    const T *kp = static_cast<const T *>(p.k) + base;
+    const T *vp = static_cast<const T *>(p.v) + base;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if constexpr (sizeof(T) == 2) {
+            pr.k[i] = *reinterpret_cast<const uint4 *>(kp + 512 * i);
+            pr.v[i] = *reinterpret_cast<const uint4 *>(vp + 512 * i);
+        } else {
+            pr.k[i][0] = *reinterpret_cast<const float4 *>(kp + 512 * i);
+            pr.k[i][1] = *reinterpret_cast<const float4 *>(kp + 512 * i + 4);
+            pr.v[i][0] = *reinterpret_cast<const float4 *>(vp + 512 * i);
+            pr.v[i][1] = *reinterpret_cast<const float4 *>(vp + 512 * i + 4);
+        }
+    }
+}
+
+// The query slice a lane needs: dims [8c, 8c + 8) of one row.
+template <typename T>
+struct QSlice;
+template <>
+struct QSlice<f16> {
+    f16x2 h[4];
+};
+template <>
+struct QSlice<float> {
+    float f[8];
+};
+
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+
+__device__ __forceinline__ float dot8(const QSlice<f16> &q, const uint4 &k) {
+    float s = 0.0f;
+    s = __builtin_amdgcn_fdot2(q.h[0], as_f16x2(k.x), s, false);
+    s = __builtin_amdgcn_fdot2(q.h[1], as_f16x2(k.y), s, false);
+    s = __builtin_amdgcn_fdot2(q.h[2], as_f16x2(k.z), s, false);
+    s = __builtin_amdgcn_fdot2(q.h[3], as_f16x2(k.w), s, false);
+    return s;
+}
+
+__device__ __forceinline__ float dot8(const QSlice<float> &q, const float4 (&k)[2]) {
+    float s = 0.0f;
+    s = fmaf(q.f[0], k[0].x, s);
+    s = fmaf(q.f[1], k[0].y, s);
+    s = fmaf(q.f[2], k[0].z, s);
+    s = fmaf(q.f[3], k[0].w, s);
+    s = fmaf(q.f[4], k[1].x, s);
+    s = fmaf(q.f[5], k[1].y, s);
+    s = fmaf(q.f[6], k[1].z, s);
+    s = fmaf(q.f[7], k[1].w, s);
+    return s;
+}
+
+__device__ __forceinline__ void unpack8(const uint4 &v, float (&out)[8]) {
+    const f16x2 a = as_f16x2(v.x), b = as_f16x2(v.y), c = as_f16x2(v.z), d = as_f16x2(v.w);
+    out[0] = static_cast<float>(a.x);
+    out[1] = static_cast<float>(a.y);
+    out[2] = static_cast<float>(b.x);
+    out[3] = static_cast<float>(b.y);
+    out[4] = static_cast<float>(c.x);
+    out[5] = static_cast<float>(c.y);
+    out[6] = static_cast<float>(d.x);
+    out[7] = static_cast<float>(d.y);
+}
+
+__device__ __forceinline__ void unpack8(const float4 (&v)[2], float (&out)[8]) {
+    out[0] = v[0].x;
+    out[1] = v[0].y;
+    out[2] = v[0].z;
+    out[3] = v[0].w;
+    out[4] = v[1].x;
+    out[5] = v[1].y;
+    out[6] = v[1].z;
+    out[7] = v[1].w;
+}
+
+// Merges this lane's (m, l, acc) with the lane `mask` away; both lanes end
+// with the same values.
+__device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8], int mask) {
+    const float mo = __shfl_xor(m, mask, kWave), lo = __shfl_xor(l, mask, kWave);
+    const float M = fmaxf(m, mo);
+    const float fa = m == -INFINITY ? 0.0f : exp2f(m - M);
+    const float fb = mo == -INFINITY ? 0.0f : exp2f(mo - M);
+    l = l * fa + lo * fb;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const float ao = __shfl_xor(acc[e], mask, kWave);
+        acc[e] = acc[e] * fa + ao * fb;
+    }
+    m = M;
+}
+
+template <typename T, int ROWS>
+__global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
+    constexpr int D = kHeadDim;
+    const int run = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
+    const int lane = static_cast<int>(threadIdx.x) % kWave, wave = static_cast<int>(threadIdx.x) / kWave;
+    const int r = lane >> 4, c = lane & 15;
+    const int G = p.G;
+
+    __shared__ float red_acc[ROWS][kWaves][D];
+    __shared__ float red_m[ROWS][kWaves], red_l[ROWS][kWaves];
+
+    // The run: list entries first .. first + nq - 1, one sequence.
+    const int first = p.run_first ? p.run_first[run] : run;
+    int nq = p.run_count ? p.run_count[run] : 1;
+    nq = max(1, min(nq, ROWS / G));
+    const int nrows = nq * G;
+    const int t0 = p.token_index ? p.token_index[first] : first;
+    const int32_t *table = p.tables + static_cast<int64_t>(p.token_seq[t0]) * p.max_blocks;
+
+    int row_pos[ROWS];
+    int min_pos = INT_MAX, max_pos = -1;
+#pragma unroll
+    for (int row = 0; row < ROWS; row++) {
+        row_pos[row] = -1;
+        if (row < nrows) {
+            const int li = first + row / G;
+            const int t = p.token_index ? p.token_index[li] : li;
+            row_pos[row] = p.positions[t];
+            min_pos = min(min_pos, row_pos[row]);
+            max_pos = max(max_pos, row_pos[row]);
+        }
+    }
+    const int ctx_max = min(max_pos + 1, p.max_blocks * kPage);
+    const int begin = split * p.split_len;
+    const int end = min(ctx_max, begin + p.split_len);
+
+    QSlice<T> q[ROWS];
+    float m[ROWS], l[ROWS], acc[ROWS][8];
+#pragma unroll
+    for (int row = 0; row < ROWS; row++) {
+        m[row] = -INFINITY;
+        l[row] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
+        if (row < nrows) {
+            const int li = first + row / G;
+            const int t = p.token_index ? p.token_index[li] : li;
+            const int head = kvh * G + row % G;
+            const T *qp = static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c;
+            if constexpr (sizeof(T) == 2) {
+                const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
+                q[row].h[0] = as_f16x2(raw.x);
+                q[row].h[1] = as_f16x2(raw.y);
+                q[row].h[2] = as_f16x2(raw.z);
+                q[row].h[3] = as_f16x2(raw.w);
+            } else {
+                const float4 a = *reinterpret_cast<const float4 *>(qp);
+                const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
+                q[row].f[0] = a.x;
+                q[row].f[1] = a.y;
+                q[row].f[2] = a.z;
+                q[row].f[3] = a.w;
+                q[row].f[4] = b.x;
+                q[row].f[5] = b.y;
+                q[row].f[6] = b.z;
+                q[row].f[7] = b.w;
+            }
+        }
+    }
+
+    // One page: scores, online softmax per DPP row, value accumulation.
+    auto process = [&](const PageRegs<T> &pr, int page) {
+        const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
+        const bool fast = pr.ok && (page + 1) * kPage <= min_pos + 1;  // every key visible to every row
+        float vf[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) unpack8(pr.v[i], vf[i]);
+#pragma unroll
+        for (int row = 0; row < ROWS; row++) {
+            if (row >= nrows) continue;
+            float s[4];
+            bool vis[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                s[i] = row16_sum(dot8(q[row], pr.k[i])) * p.scale_log2;
+                vis[i] = fast || (pr.ok && key0 + 4 * i <= row_pos[row]);
+                if (!vis[i]) s[i] = -INFINITY;
+            }
+            const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+            const float ref = mn == -INFINITY ? 0.0f : mn;
+            const float corr = m[row] == mn ? 1.0f : exp2f(m[row] - ref);
+            float pj[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) pj[i] = exp2f(s[i] - ref);  // exp2(-inf) = 0 for hidden keys
+            l[row] = l[row] * corr + ((pj[0] + pj[1]) + (pj[2] + pj[3]));
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
+            if (fast) {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[i], vf[i][e], acc[row][e]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[row][e] = vis[i] ? fmaf(pj[i], vf[i][e], acc[row][e]) : acc[row][e];
+            }
+            m[row] = mn;
+        }
+    };
+
+    if (begin < end) {
+        const int first_page = begin / kPage, last_page = (end - 1) / kPage;
+        PageRegs<T> A, B;
+        int pg = first_page + wave;
+        if (pg <= last_page) load_page(A, p, table, kvh, pg, lane);
+        for (; pg <= last_page; pg += 2 * kWaves) {
+            if (pg + kWaves <= last_page) load_page(B, p, table, kvh, pg + kWaves, lane);
+            process(A, pg);
+            if (pg + kWaves > last_page) break;
+            if (pg + 2 * kWaves <= last_page) load_page(A, p, table, kvh, pg + 2 * kWaves, lane);
+            process(B, pg + kWaves);
+        }
+    }
+
+    // Merge the four DPP rows of the wave (rows 0+1 and 2+3, then the pairs).
+#pragma unroll
+    for (int row = 0; row < ROWS; row++) {
+        if (row >= nrows) continue;
+        merge_lanes(m[row], l[row], acc[row], 16);
+        merge_lanes(m[row], l[row], acc[row], 32);
+        if (r == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) red_acc[row][wave][8 * c + e] = acc[row][e];
+            if (c == 0) {
+                red_m[row][wave] = m[row];
+                red_l[row][wave] = l[row];
+            }
+        }
+    }
+    __syncthreads();
+
+    // Merge the waves in order 0..3, then write the output or this split's partial.
+    for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
+        const int row = idx / D, d = idx % D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) M = fmaxf(M, red_m[row][w]);
+        float L = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; w++) {
+            const float mw = red_m[row][w];
+            const float f = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            L = L + red_l[row][w] * f;
+            O = O + red_acc[row][w][d] * f;
+        }
+        const int li = first + row / G;
+        const int head = kvh * G + row % G;
+        if (p.num_splits == 1) {
+            const int t = p.token_index ? p.token_index[li] : li;
+            T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
+            o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
+        } else {
+            const int64_t slot = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits + split;
+            p.part_acc[slot * D + d] = O;
+            if (d == 0) {
+                p.part_ml[slot * 2] = M;
+                p.part_ml[slot * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the splits that
+// hold this token's keys, in split order; splits without a visible key skipped.
+template <typename T>
+__global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) {
+    constexpr int D = kHeadDim;
+    const int li = blockIdx.x, head = blockIdx.y, d = static_cast<int>(threadIdx.x);
+    const int t = p.token_index ? p.token_index[li] : li;
+    const int ctx = min(p.positions[t] + 1, p.max_blocks * kPage);
+    const int ns = min(p.num_splits, max(1, (ctx + p.split_len - 1) / p.split_len));
+    const int64_t base = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+    float L = 0.0f, O = 0.0f;
+    bool any = false;
+    for (int s = 0; s < ns; s++) {
+        const float ms = p.part_ml[(base + s) * 2];
+        if (ms == -INFINITY) continue;
+        const float f = exp2f(ms - M);
+        const float ls = p.part_ml[(base + s) * 2 + 1] * f, os = p.part_acc[(base + s) * D + d] * f;
+        L = any ? L + ls : ls;
+        O = any ? O + os : os;
+        any = true;
+    }
+    T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
+    o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
+}
+
+template <typename T, int ROWS>
+hipError_t launch_rows(const DecodeParams &p, int runs, hipStream_t stream) {
+    const dim3 grid(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv), static_cast<unsigned>(p.num_splits));
+    hipLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_typed(const DecodeParams &p, int runs, int rows, hipStream_t stream) {
+    switch (rows) {
+        case 1: return launch_rows<T, 1>(p, runs, stream);
+        case 2: return launch_rows<T, 2>(p, runs, stream);
+        case 4: return launch_rows<T, 4>(p, runs, stream);
+        case 8: return launch_rows<T, 8>(p, runs, stream);
+        case 10: return launch_rows<T, 10>(p, runs, stream);
+        case 16: return launch_rows<T, 16>(p, runs, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t main_done) {
+    if (a.T <= 0) return hipSuccess;
+    DecodeParams p{};
+    p.q = a.q;
+    p.k = a.k_cache;
+    p.v = a.v_cache;
+    p.positions = a.positions;
+    p.token_seq = a.token_seq;
+    p.tables = a.block_tables;
+    p.token_index = a.token_index;
+    p.run_first = a.run_first;
+    p.run_count = a.run_count;
+    p.out = a.out;
+    p.part_acc = a.part_acc;
+    p.part_ml = a.part_ml;
+    p.max_blocks = a.max_blocks;
+    p.n_heads = a.n_heads;
+    p.n_kv = a.n_kv;
+    p.G = a.n_heads / a.n_kv;
+    p.num_blocks = a.num_blocks;
+    p.num_splits = a.num_splits;
+    p.split_len = a.split_len;
+    p.scale_log2 = a.scale * kLog2e;
+    const int runs = a.run_first ? a.num_runs : a.T;
+    if (runs <= 0) return hipSuccess;
+    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, rows, stream)
+                                              : launch_typed<float>(p, runs, rows, stream);
+    if (e == hipSuccess && main_done) e = hipEventRecord(main_done, stream);
+    if (e != hipSuccess || a.num_splits == 1) return e;
+    const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>(a.n_heads));
+    if (a.dtype == EMBER_DTYPE_F16)
+        hipLaunchKernelGGL(merge_splits_kernel<f16>, grid, dim3(kHeadDim), 0, stream, p);
+    else
+        hipLaunchKernelGGL(merge_splits_kernel<float>, grid, dim3(kHeadDim), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace ember::hip

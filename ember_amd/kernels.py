@@ -1,0 +1,217 @@
+"""Launchers of the gfx950 kernels through the C ABI, for torch tensors.
+
+Mirrors the reference's launcher seam (src/backend/cuda/kernels.cuh:74-120):
+``qk_norm_rope_store`` (-> ember_hip_kv_append), ``paged_attention``
+(-> ember_hip_paged_decode), ``prefill_attention`` (-> ember_hip_prefill_attn),
+plus ``copy_pages`` (copy-on-write). Device tensors carry activations and pools;
+the step's integer arrays are given as host arrays, checked here (every index a
+kernel will follow is in range), then uploaded. Launches go to the current torch
+stream unless ``stream`` is given.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import BLOCK_SIZE, MAX_RUN, AttnArgs, CopyArgs, EmberError, PrefillArgs, QkvArgs, check
+
+HEAD_DIM = 128
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype == torch.float16:
+        return _lib.DTYPE_F16
+    if t.dtype == torch.float32:
+        return _lib.DTYPE_F32
+    raise EmberError(f"unsupported dtype {t.dtype}")
+
+
+def _stream_handle(stream) -> int:
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+def _dev(t: torch.Tensor, name: str) -> int:
+    if not t.is_cuda or not t.is_contiguous():
+        raise EmberError(f"{name} must be a contiguous device tensor")
+    return t.data_ptr()
+
+
+def _opt(t: torch.Tensor | None, name: str) -> int | None:
+    return None if t is None else _dev(t, name)
+
+
+def _ints(a, device) -> torch.Tensor:
+    return torch.as_tensor(np.ascontiguousarray(np.asarray(a, dtype=np.int32)), device=device)
+
+
+@dataclass
+class StepInts:
+    """A step's integers on the host (the StepBatch fields the kernels read) and their device copies.
+
+    positions [T], token_seq [T], block_tables [S, max_blocks].
+    """
+
+    positions: np.ndarray
+    token_seq: np.ndarray
+    block_tables: np.ndarray
+    num_blocks: int  # blocks in each layer's pool (every table entry a kernel reads must be below it)
+
+    def __post_init__(self):
+        self.positions = np.ascontiguousarray(np.asarray(self.positions, dtype=np.int32).reshape(-1))
+        self.token_seq = np.ascontiguousarray(np.asarray(self.token_seq, dtype=np.int32).reshape(-1))
+        bt = np.asarray(self.block_tables, dtype=np.int32)
+        self.block_tables = np.ascontiguousarray(bt.reshape(bt.shape[0], -1))
+        T, S, W = self.positions.size, self.block_tables.shape[0], self.block_tables.shape[1]
+        if self.token_seq.size != T:
+            raise EmberError("positions and token_seq differ in length")
+        if T and (self.token_seq.min() < 0 or self.token_seq.max() >= S):
+            raise EmberError("token_seq names a sequence without a block table")
+        if T and (self.positions.min() < 0 or self.positions.max() >= W * BLOCK_SIZE):
+            raise EmberError("a position lies beyond its block table")
+        for t in range(T):  # every page up to each token's position must be a pool block
+            pages = self.block_tables[self.token_seq[t], : self.positions[t] // BLOCK_SIZE + 1]
+            if pages.size and (pages.min() < 0 or pages.max() >= self.num_blocks):
+                raise EmberError(f"token {t} reads a block outside the pool of {self.num_blocks}")
+        self._dev = None
+
+    @property
+    def T(self) -> int:
+        return int(self.positions.size)
+
+    @property
+    def max_blocks(self) -> int:
+        return int(self.block_tables.shape[1])
+
+    def device(self, device="cuda"):
+        if self._dev is None:
+            self._dev = (_ints(self.positions, device), _ints(self.token_seq, device), _ints(self.block_tables, device))
+        return self._dev
+
+
+def inv_freq(theta: float, head_dim: int = HEAD_DIM) -> np.ndarray:
+    """Rotary frequencies in f32, as the reference computes them (cpu_backend.cpp:85-88)."""
+    i = np.arange(head_dim // 2, dtype=np.float32)
+    return (np.float32(1.0) / np.power(np.float32(theta), (2 * i) / np.float32(head_dim), dtype=np.float32)).astype(np.float32)
+
+
+def qk_norm_rope_store(qkv, q_out, k_pool, v_pool, ints: StepInts, *, n_heads, n_kv, inv_freq_dev, q_norm=None,
+                       k_norm=None, bias=None, eps=1e-6, stream=None):
+    """QK-RMSNorm + RoPE + K/V page write for one layer (≙ cuda::qk_norm_rope_store)."""
+    T = ints.T
+    width = (n_heads + 2 * n_kv) * HEAD_DIM
+    if qkv.numel() != T * width or q_out.numel() != T * n_heads * HEAD_DIM:
+        raise EmberError("qkv / q_out sizes do not match the step")
+    if k_pool.numel() < ints.num_blocks * n_kv * BLOCK_SIZE * HEAD_DIM or v_pool.numel() != k_pool.numel():
+        raise EmberError("pools are smaller than num_blocks pages")
+    pos, seq, tab = ints.device(qkv.device)
+    a = QkvArgs()
+    a.qkv, a.q_out = _dev(qkv, "qkv"), _dev(q_out, "q_out")
+    a.k_cache, a.v_cache = _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    a.q_norm, a.k_norm, a.bias = _opt(q_norm, "q_norm"), _opt(k_norm, "k_norm"), _opt(bias, "bias")
+    a.inv_freq = _dev(inv_freq_dev, "inv_freq")
+    a.positions, a.token_seq, a.block_tables = pos.data_ptr(), seq.data_ptr(), tab.data_ptr()
+    a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = ints.max_blocks, T, n_heads, n_kv, HEAD_DIM
+    a.eps, a.num_blocks, a.dtype = eps, ints.num_blocks, _dtype_code(qkv)
+    check(_lib.lib().ember_hip_kv_append(a, _stream_handle(stream)), "kv_append")
+
+
+def decode_runs(ints: StepInts, token_list, max_run: int = MAX_RUN):
+    """Cuts a list of tokens into runs of consecutive tokens of one sequence (at most max_run each)."""
+    first, count = [], []
+    i, tl = 0, list(token_list)
+    while i < len(tl):
+        j = i + 1
+        while (j < len(tl) and j - i < max_run and tl[j] == tl[j - 1] + 1
+               and ints.token_seq[tl[j]] == ints.token_seq[tl[i]] and ints.positions[tl[j]] == ints.positions[tl[j - 1]] + 1):
+            j += 1
+        first.append(i)
+        count.append(j - i)
+        i = j
+    return np.asarray(first, np.int32), np.asarray(count, np.int32)
+
+
+def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list=None, runs=None,
+                    split_len=512, num_splits=None, scratch=None, stream=None):
+    """Paged decode attention (≙ cuda::paged_attention).
+
+    token_list: tokens to process (None = all). runs: (run_first, run_count) over
+    token_list positions, or None for one token per run. num_splits defaults to
+    what the longest context needs at split_len keys per split.
+    """
+    tl = np.arange(ints.T, dtype=np.int32) if token_list is None else np.asarray(token_list, np.int32)
+    n = int(tl.size)
+    if n == 0:
+        return
+    if tl.min() < 0 or tl.max() >= ints.T:
+        raise EmberError("token_list names a token outside the step")
+    if q.numel() < ints.T * n_heads * HEAD_DIM or out.numel() < ints.T * n_heads * HEAD_DIM:
+        raise EmberError("q / out are smaller than the step")
+    if k_pool.numel() < ints.num_blocks * n_kv * BLOCK_SIZE * HEAD_DIM:
+        raise EmberError("pools are smaller than num_blocks pages")
+    ctx = int(ints.positions[tl].max()) + 1
+    if num_splits is None:
+        num_splits = max(1, math.ceil(ctx / split_len))
+    if num_splits * split_len < ctx:
+        raise EmberError("num_splits x split_len does not cover the context")
+    dev = q.device
+    pos, seq, tab = ints.device(dev)
+    tl_dev = _ints(tl, dev)
+    a = AttnArgs()
+    a.token_index = tl_dev.data_ptr()
+    a.q, a.k_cache, a.v_cache = _dev(q, "q"), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    a.positions, a.token_seq, a.block_tables = pos.data_ptr(), seq.data_ptr(), tab.data_ptr()
+    a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = ints.max_blocks, n, n_heads, n_kv, HEAD_DIM
+    a.scale = 1.0 / math.sqrt(HEAD_DIM)
+    a.out = _dev(out, "out")
+    a.num_splits, a.split_len = num_splits, split_len
+    keep = [tl_dev]
+    if num_splits > 1:
+        need = n * n_heads * num_splits
+        if scratch is None:
+            scratch = (torch.empty(need * HEAD_DIM, dtype=torch.float32, device=dev),
+                       torch.empty(need * 2, dtype=torch.float32, device=dev))
+        if scratch[0].numel() < need * HEAD_DIM or scratch[1].numel() < need * 2:
+            raise EmberError("split scratch too small")
+        a.part_acc, a.part_ml = _dev(scratch[0], "part_acc"), _dev(scratch[1], "part_ml")
+        keep.append(scratch)
+    a.num_blocks, a.dtype = ints.num_blocks, _dtype_code(q)
+    if runs is not None:
+        rf, rc = (np.asarray(x, np.int32) for x in runs)
+        if rf.size != rc.size or rc.min() < 1 or rc.max() > MAX_RUN or rf.min() < 0 or (rf + rc).max() > n:
+            raise EmberError("malformed runs")
+        for f, c in zip(rf, rc):  # one sequence per run
+            if len(set(ints.token_seq[tl[f:f + c]].tolist())) != 1:
+                raise EmberError("a run spans two sequences")
+        rf_dev, rc_dev = _ints(rf, dev), _ints(rc, dev)
+        keep += [rf_dev, rc_dev]
+        a.run_first, a.run_count, a.num_runs, a.max_run = rf_dev.data_ptr(), rc_dev.data_ptr(), int(rf.size), int(rc.max())
+    check(_lib.lib().ember_hip_paged_decode(a, _stream_handle(stream)), "paged_decode")
+    return keep  # the caller keeps the uploads alive until the stream has run
+
+
+def copy_pages(k_pool, v_pool, src, dst, *, n_layers, layer_stride, n_kv, num_blocks, stream=None):
+    """Copies whole pages src[i] -> dst[i] over every layer (the device half of copy-on-write)."""
+    s, d = np.asarray(src, np.int32), np.asarray(dst, np.int32)
+    if s.size != d.size:
+        raise EmberError("src / dst differ in length")
+    if s.size == 0:
+        return
+    if min(s.min(), d.min()) < 0 or max(s.max(), d.max()) >= num_blocks:
+        raise EmberError("a page pair lies outside the pool")
+    if k_pool.numel() < n_layers * layer_stride:
+        raise EmberError("pools are smaller than n_layers x layer_stride")
+    dev = k_pool.device
+    sd, dd = _ints(s, dev), _ints(d, dev)
+    a = CopyArgs()
+    a.k_cache, a.v_cache = _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    a.src_blocks, a.dst_blocks, a.n = sd.data_ptr(), dd.data_ptr(), int(s.size)
+    a.n_layers, a.layer_stride, a.n_kv, a.head_dim = n_layers, layer_stride, n_kv, HEAD_DIM
+    a.num_blocks, a.dtype = num_blocks, _dtype_code(k_pool)
+    check(_lib.lib().ember_hip_copy_pages(a, _stream_handle(stream)), "copy_pages")
+    return (sd, dd)

@@ -1,0 +1,255 @@
+/*
+ * ember_hip.h - C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Three layers, all plain C (pointers, sizes, ints; no C++ or torch types):
+ *
+ *   1. Kernel launchers. Each enqueues work on `stream` (a hipStream_t passed
+ *      as void*; NULL = the null stream) and returns immediately. They replace
+ *      the CUDA launchers of the reference's kernel seam
+ *      (src/backend/cuda/kernels.cuh:74-120) field for field, plus a few
+ *      documented additions (pool size for bounds guards, element type, query
+ *      runs).
+ *   2. The KV block manager (src/kvcache/block_manager.hpp:25-67) behind an
+ *      opaque handle, plus two additive calls (share, copy_on_write) that the
+ *      reference does not have.
+ *   3. The paged-KV path: the KV pool, the step plan (packing, routing,
+ *      splits) and the per-layer append + attention that the reference's
+ *      CudaBackend::forward / enqueue perform
+ *      (src/backend/cuda/cuda_backend.cu:134-205, :288-374).
+ *
+ * Every function returns EMBER_OK (0), EMBER_ERR_INVALID (-1: a bad argument
+ * or unsupported shape; no work was enqueued) or a positive hipError_t. None
+ * throws. ember_hip_last_error() describes the last failure on the calling
+ * thread.
+ *
+ * Layout of a layer's K (and, separately, V) pool, identical to the
+ * reference's (src/backend/cpu/cpu_backend.cpp:256-260, :290):
+ *   [block][kv_head][slot 0..15][head_dim]
+ * token at position `pos` of sequence `s` lives in
+ *   block = block_tables[s * max_blocks + pos / 16], slot = pos % 16.
+ */
+#ifndef EMBER_HIP_H
+#define EMBER_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EMBER_ABI_VERSION 1
+#define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
+#define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
+#define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
+
+#define EMBER_OK 0
+#define EMBER_ERR_INVALID (-1)
+
+/* Element type of q/k/v activations and of the KV pool. f16 is the serving
+ * path; f32 is the parity path checked against the f32 CPU backend. */
+#define EMBER_DTYPE_F16 0
+#define EMBER_DTYPE_F32 1
+
+/* ---- 1. kernel launchers ------------------------------------------------ */
+
+/* Replaces cuda::QkvArgs (kernels.cuh:74-84). */
+typedef struct EmberQkvArgs {
+    const void *qkv;              /* [T, (n_heads + 2 * n_kv) * head_dim]: q heads, k heads, v heads */
+    void *q_out;                  /* [T, n_heads * head_dim] */
+    void *k_cache, *v_cache;      /* this layer's pools, [num_blocks][n_kv][16][head_dim] */
+    const float *q_norm, *k_norm; /* [head_dim], or NULL: no QK-RMSNorm */
+    const float *bias;            /* [(n_heads + 2 * n_kv) * head_dim], or NULL */
+    const float *inv_freq;        /* [head_dim / 2] rotary frequencies */
+    const int32_t *positions;     /* [T] */
+    const int32_t *token_seq;     /* [T] sequence of each token */
+    const int32_t *block_tables;  /* [S * max_blocks] */
+    int32_t max_blocks, T, n_heads, n_kv, head_dim;
+    float eps;
+    /* additions */
+    int32_t num_blocks;           /* blocks in this layer's pool; a slot in any other block is not written */
+    int32_t dtype;                /* EMBER_DTYPE_*: qkv, q_out and the pools */
+} EmberQkvArgs;
+
+/* QK-RMSNorm, rotate-half RoPE and the K/V cache write, fused.
+ * Replaces cuda::qk_norm_rope_store (kernels.cuh:85-86; k_elementwise.cu:159-171).
+ * head_dim must be 128; n_heads and n_kv at most 64. */
+int ember_hip_kv_append(const EmberQkvArgs *args, void *stream);
+
+/* Replaces cuda::AttentionArgs (kernels.cuh:88-101). */
+typedef struct EmberAttnArgs {
+    const int32_t *token_index;   /* [T] tokens to process, or NULL = 0..T-1 */
+    const void *q;                /* [*, n_heads, head_dim] */
+    const void *k_cache, *v_cache;
+    const int32_t *positions, *token_seq, *block_tables;
+    int32_t max_blocks, T, n_heads, n_kv, head_dim;
+    float scale;
+    void *out;                    /* [*, n_heads, head_dim] */
+    int32_t num_splits;           /* context chunks per token: 1 = no split */
+    int32_t split_len;            /* keys per chunk, a multiple of 16 */
+    float *part_acc;              /* [T, n_heads, num_splits, head_dim], indexed by list position 0..T-1 */
+    float *part_ml;               /* [T, n_heads, num_splits, 2] */
+    /* additions */
+    int32_t num_blocks;           /* blocks in this layer's pool; pages outside it are skipped */
+    int32_t dtype;                /* EMBER_DTYPE_* of q, out and the pools */
+    /* Query runs: list entries [run_first[r], run_first[r] + run_count[r]) are
+     * consecutive tokens of one sequence; one work-group reads each page once
+     * for all of them. Each token's result is bit-identical to processing it
+     * alone. NULL = every listed token is its own run. */
+    const int32_t *run_first, *run_count;
+    int32_t num_runs;
+    int32_t max_run;              /* upper bound of run_count, 1..EMBER_MAX_RUN */
+} EmberAttnArgs;
+
+/* Paged attention for short runs (decode, speculative verify): one work-group
+ * per (run, kv head, context split), all G = n_heads / n_kv query heads of the
+ * kv head together, online softmax, then a fixed-order merge of the splits.
+ * Replaces cuda::paged_attention (kernels.cuh:102; k_attention.cu:401-415).
+ * head_dim must be 128; G in 1..8. */
+int ember_hip_paged_decode(const EmberAttnArgs *args, void *stream);
+
+/* Replaces cuda::PrefillArgs (kernels.cuh:109-119). */
+typedef struct EmberPrefillArgs {
+    const void *q;                /* [T, n_heads, head_dim] */
+    const void *k_cache, *v_cache;
+    const int32_t *tile_start;    /* [num_tiles] first token of the tile */
+    const int32_t *tile_end;      /* [num_tiles] one past its last token (at most 64 tokens) */
+    const int32_t *tile_seq;      /* [num_tiles] sequence of the tile */
+    const int32_t *positions, *block_tables;
+    int32_t num_tiles, max_blocks, n_heads, n_kv, head_dim;
+    float scale;
+    void *out;                    /* [T, n_heads, head_dim] */
+    /* additions */
+    int32_t num_blocks;
+    int32_t dtype;                /* must be EMBER_DTYPE_F16 (MFMA path) */
+} EmberPrefillArgs;
+
+/* Causal attention of 64-token query tiles over the paged cache on MFMA
+ * (v_mfma_f32_32x32x16_f16), all G query heads of a kv head per work-group.
+ * Replaces cuda::prefill_attention (kernels.cuh:120; k_attention.cu:390-399). */
+int ember_hip_prefill_attn(const EmberPrefillArgs *args, void *stream);
+
+/* No counterpart in the reference: the device half of copy-on-write. */
+typedef struct EmberCopyArgs {
+    void *k_cache, *v_cache;      /* layer 0's pools; layer l starts layer_stride elements later */
+    const int32_t *src_blocks;    /* [n] device array */
+    const int32_t *dst_blocks;    /* [n] device array */
+    int32_t n;                    /* page pairs */
+    int32_t n_layers;
+    int64_t layer_stride;         /* elements between consecutive layers' pools */
+    int32_t n_kv, head_dim;
+    int32_t num_blocks;           /* blocks per layer pool; pairs naming others are skipped */
+    int32_t dtype;
+} EmberCopyArgs;
+
+/* Copies whole pages (every layer, K and V, every kv head) from src to dst. */
+int ember_hip_copy_pages(const EmberCopyArgs *args, void *stream);
+
+/* Description of the last failure on this thread ("" if none). */
+const char *ember_hip_last_error(void);
+int ember_hip_abi_version(void);
+/* sizeof of each argument struct, for FFI bindings to check their layouts:
+ * 0 EmberQkvArgs, 1 EmberAttnArgs, 2 EmberPrefillArgs, 3 EmberCopyArgs,
+ * 4 EmberKvConfig, 5 EmberStepBatch; -1 otherwise. */
+int32_t ember_hip_sizeof(int32_t which);
+
+/* ---- 2. KV block manager ------------------------------------------------- */
+
+/* Opaque handle to ember::BlockManager (src/kvcache/block_manager.hpp:25-87). */
+typedef struct EmberBlockManager EmberBlockManager;
+
+/* BlockManager(num_blocks, prefix_caching) (block_manager.hpp:27); NULL on error. */
+EmberBlockManager *ember_bm_create(int32_t num_blocks, int32_t prefix_caching);
+void ember_bm_destroy(EmberBlockManager *bm);
+int32_t ember_bm_num_blocks(const EmberBlockManager *bm);  /* :29 */
+int32_t ember_bm_available(const EmberBlockManager *bm);   /* :31 */
+int32_t ember_bm_used(const EmberBlockManager *bm);        /* :32 */
+int32_t ember_bm_cached(const EmberBlockManager *bm);      /* :33 */
+/* allocate (:37): a fresh block, or -1 when none is available. */
+int32_t ember_bm_allocate(EmberBlockManager *bm);
+/* release (:39): EMBER_ERR_INVALID when the block is free (the reference throws). */
+int32_t ember_bm_release(EmberBlockManager *bm, int32_t block);
+/* release_all (:40): releases blocks[n-1] first. */
+int32_t ember_bm_release_all(EmberBlockManager *bm, const int32_t *blocks, int32_t n);
+/* block_hash (:43). */
+uint64_t ember_bm_block_hash(uint64_t parent, const int32_t *tokens, int32_t n);
+/* match_prefix (:47): writes up to n / 16 blocks to out_blocks, returns how many. */
+int32_t ember_bm_match_prefix(EmberBlockManager *bm, const int32_t *tokens, int32_t n, int32_t *out_blocks);
+/* seal (:52): returns the block's hash; 0 (never a valid hash) on error. */
+uint64_t ember_bm_seal(EmberBlockManager *bm, int32_t block, uint64_t parent, const int32_t *tokens, int32_t n);
+int32_t ember_bm_prefix_caching(const EmberBlockManager *bm); /* :54 */
+int32_t ember_bm_refcount(const EmberBlockManager *bm, int32_t block); /* :55 */
+uint64_t ember_bm_hit_tokens(const EmberBlockManager *bm);    /* :58 */
+uint64_t ember_bm_lookup_tokens(const EmberBlockManager *bm); /* :59 */
+/* check (:64): copies the first problem (or "") into buf; returns 0 if consistent, 1 if not. */
+int32_t ember_bm_check(const EmberBlockManager *bm, char *buf, int32_t buflen);
+/* states (:67): one byte per block, 0 free, 1 cached, 2 in use. */
+void ember_bm_states(const EmberBlockManager *bm, uint8_t *out);
+/* No counterpart in the reference: takes one more reference on each of n
+ * blocks held by a sequence being forked, partial last page included. */
+int32_t ember_bm_share(EmberBlockManager *bm, const int32_t *blocks, int32_t n);
+/* No counterpart in the reference: before writing into `block`, a holder calls
+ * this. Returns `block` itself when the caller is its only holder; otherwise
+ * drops the caller's reference and returns a fresh private block (the caller
+ * copies the page into it), or -1 when none is available (the reference is
+ * kept then). -2 when `block` is not held. */
+int32_t ember_bm_copy_on_write(EmberBlockManager *bm, int32_t block);
+
+/* ---- 3. the paged-KV path -------------------------------------------------- */
+
+typedef struct EmberKvConfig {
+    int32_t n_layers, n_heads, n_kv_heads, head_dim;
+    float rms_eps;
+    double rope_theta;
+    int32_t max_position;     /* bounds the block-table width */
+    int32_t num_blocks;       /* blocks the engine may hand out; one spare block per layer is added */
+    int32_t max_batch_tokens; /* tokens per step */
+    int32_t max_seqs;         /* sequences per step */
+    int32_t dtype;            /* EMBER_DTYPE_* of activations and pools */
+    int32_t qk_norm;          /* nonzero: q_norm / k_norm weights are given per layer */
+    int32_t split_len;        /* keys per decode split, multiple of 16 (0 = 512) */
+} EmberKvConfig;
+
+/* Replaces ember::StepBatch (src/backend/backend.hpp:56-76); host arrays. */
+typedef struct EmberStepBatch {
+    const int32_t *tokens;        /* [num_tokens] */
+    const int32_t *positions;     /* [num_tokens] */
+    const int32_t *query_start;   /* [num_seqs + 1] */
+    const int32_t *context_len;   /* [num_seqs] */
+    const int32_t *block_tables;  /* [num_seqs * max_blocks] */
+    int32_t num_tokens, num_seqs, max_blocks;
+} EmberStepBatch;
+
+typedef struct EmberPagedKv EmberPagedKv;
+
+/* Allocates the pools (zeroed), rotary table, q buffer, split scratch and
+ * step buffers on the current device; all work goes to `stream`. NULL on error. */
+EmberPagedKv *ember_kv_create(const EmberKvConfig *cfg, void *stream);
+void ember_kv_destroy(EmberPagedKv *kv);
+/* Packs the step's integers, routes runs of >= 16 new tokens to prefill tiles
+ * and the rest to decode runs, fixes the splits and uploads the plan with one
+ * host-to-device copy (cuda_backend.cu:153-205). */
+int32_t ember_kv_plan(EmberPagedKv *kv, const EmberStepBatch *batch);
+/* One layer of the planned step: append K/V of every new token, then attention
+ * for every token into out [num_tokens, n_heads, head_dim] (cuda_backend.cu:357-361). */
+int32_t ember_kv_layer(EmberPagedKv *kv, int32_t layer, const void *qkv, const float *q_norm, const float *k_norm,
+                       const float *bias, void *out);
+/* Device copies of whole pages, src[i] -> dst[i] (host arrays of n blocks), all layers. */
+int32_t ember_kv_copy_blocks(EmberPagedKv *kv, const int32_t *src, const int32_t *dst, int32_t n);
+void *ember_kv_k_pool(EmberPagedKv *kv, int32_t layer);
+void *ember_kv_v_pool(EmberPagedKv *kv, int32_t layer);
+int64_t ember_kv_layer_stride(const EmberPagedKv *kv); /* elements between layers' pools */
+int32_t ember_kv_spare_block(const EmberPagedKv *kv);  /* the block padding rows write to */
+/* What the current plan launches per layer: decode runs, prefill tiles, splits. */
+int32_t ember_kv_plan_info(const EmberPagedKv *kv, int32_t *decode_runs, int32_t *prefill_tiles, int32_t *num_splits);
+/* Kernel timing for benchmarks: while on, every layer() records HIP events on
+ * the path's stream right before and right after the paged-decode kernel
+ * (before the split merge). ember_kv_timing waits for them and returns the
+ * number of timed launches and their total duration in ms, then starts over. */
+int32_t ember_kv_set_timing(EmberPagedKv *kv, int32_t on);
+int32_t ember_kv_timing(EmberPagedKv *kv, int32_t *launches, double *total_ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMBER_HIP_H */

@@ -1,0 +1,115 @@
+/*
+ * oracle.h - CPU restatement of the reference's paged-KV path. TEST
+ * INFRASTRUCTURE ONLY: the checker that tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg call. Nothing in the product (ember_amd/,
+ * include/) links, loads or calls it.
+ *
+ * Each function restates one piece of YUStulinu/Ember's CPU backend or block
+ * manager and cites the lines it follows (paths under the reference's root).
+ * How each is pinned (checked against something other than itself) is noted
+ * per function; see tests/test_oracle_*.py.
+ */
+#ifndef EMBER_ORACLE_H
+#define EMBER_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE half <-> float, round to nearest even, overflow to inf
+ * (src/common/fp16.hpp:25-71). Pinned: numpy.float16, exhaustively / on
+ * random and edge values. */
+float ember_oracle_f16_to_f32(uint16_t h);
+uint16_t ember_oracle_f32_to_f16(float f);
+void ember_oracle_f16_to_f32_n(const uint16_t *src, float *dst, int64_t n);
+void ember_oracle_f32_to_f16_n(const float *src, uint16_t *dst, int64_t n);
+
+/* inv_freq[i] = 1 / powf(theta, 2i / D) in f32 (src/backend/cpu/cpu_backend.cpp:85-88).
+ * Pinned: transformers' Qwen3RotaryEmbedding frequencies. */
+void ember_oracle_inv_freq(double theta, int32_t head_dim, float *out);
+
+/* RMSNorm with a double sum of squares (cpu_backend.cpp:34-39). In place is allowed.
+ * Pinned: transformers' Qwen3RMSNorm; unit-weight outputs have unit RMS. */
+void ember_oracle_rmsnorm(const float *x, const float *w, int32_t n, float eps, float *out);
+
+/* Rotate-half RoPE of one head vector in place (cpu_backend.cpp:262-272).
+ * Pinned: transformers' apply_rotary_pos_emb; pos 0 is the identity; pair norms kept. */
+void ember_oracle_rope(float *x, int32_t head_dim, int32_t pos, const float *inv_freq);
+
+/* The f32 dot product of the CPU kernels: two 8-wide FMA accumulators over
+ * 16-element strides, then a fixed horizontal sum (cpu_kernels_avx2.cpp:27-33,
+ * :58-69); the scalar loop of cpu_kernels.cpp:74-79 without AVX2+FMA.
+ * Pinned: float64 dot within f32 rounding. */
+float ember_oracle_dot(const float *a, const float *b, int32_t n);
+
+/* Offset of (seq, layer, kv_head, pos) in a pool of num_blocks blocks per
+ * layer (cpu_backend.cpp:256-260). Pinned: brute-force enumeration of slots. */
+int64_t ember_oracle_cache_offset(const int32_t *block_tables, int32_t max_blocks, int32_t num_blocks, int32_t n_kv,
+                                  int32_t head_dim, int32_t seq, int32_t layer, int32_t kv_head, int32_t pos);
+
+/* One layer's QK-norm + RoPE + cache store (cpu_backend.cpp:146-172).
+ * qkv: [T, (n_heads + 2 n_kv) D] f32 (the q/k/v projections), bias optional.
+ * q_out: [T, n_heads, D] f32 after norm + rope.
+ * k_cache/v_cache: THIS layer's pools [num_blocks][n_kv][16][D]; f32, or f16
+ * bits when kv_f16 (then values are clamped to +-65504 and rounded, as the
+ * reference's CUDA store does, k_elementwise.cu:125).
+ * Returns 0, or -1 when a slot falls outside the pool. */
+int32_t ember_oracle_append_layer(const float *qkv, int32_t T, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                                  const float *q_norm, const float *k_norm, const float *bias, float eps,
+                                  const float *inv_freq, const int32_t *positions, const int32_t *query_start,
+                                  int32_t num_seqs, const int32_t *block_tables, int32_t max_blocks, float *q_out,
+                                  void *k_cache, void *v_cache, int32_t num_blocks, int32_t kv_f16);
+
+/* Causal attention of every token over its sequence's cache, token t seeing
+ * positions 0..positions[t] (cpu_backend.cpp:173-198): scores by
+ * ember_oracle_dot times 1/sqrt(D), max, exp in f32 summed in double, weights
+ * cast to f32, out += w * v. q is [T, n_heads, D] f32 (rounded to f16 first
+ * when q_f16, modelling an f16 q buffer). Runs on `threads` threads with the
+ * reference pool's chunking (src/common/thread_pool.cpp:57-82).
+ * Pinned: float64 textbook softmax(q K^T / sqrt(D)) V (numpy), torch SDPA, and
+ * closed forms (ctx 1 -> V0, equal keys -> mean of V). */
+int32_t ember_oracle_attention_layer(const float *q, int32_t T, int32_t n_heads, int32_t n_kv, int32_t head_dim,
+                                     const int32_t *positions, const int32_t *query_start, int32_t num_seqs,
+                                     const int32_t *block_tables, int32_t max_blocks, const void *k_cache,
+                                     const void *v_cache, int32_t num_blocks, int32_t kv_f16, int32_t q_f16,
+                                     float *out, int32_t threads);
+
+/* ---- block manager (src/kvcache/block_manager.cpp:9-139) ----
+ * Pinned: the reference's own unit test (tests/test_engine.cpp:47-78, as a
+ * fixture), published FNV-1a 64 vectors and the published inverse of the
+ * MurmurHash3 finalizer, check() invariants. */
+typedef struct EmberOracleBM EmberOracleBM;
+EmberOracleBM *ember_oracle_bm_create(int32_t num_blocks, int32_t prefix_caching);
+void ember_oracle_bm_destroy(EmberOracleBM *bm);
+int32_t ember_oracle_bm_num_blocks(const EmberOracleBM *bm);
+int32_t ember_oracle_bm_available(const EmberOracleBM *bm);
+int32_t ember_oracle_bm_cached(const EmberOracleBM *bm);
+int32_t ember_oracle_bm_allocate(EmberOracleBM *bm);
+int32_t ember_oracle_bm_release(EmberOracleBM *bm, int32_t block);
+int32_t ember_oracle_bm_release_all(EmberOracleBM *bm, const int32_t *blocks, int32_t n);
+uint64_t ember_oracle_bm_block_hash(uint64_t parent, const int32_t *tokens, int32_t n);
+/* The two stages of block_hash, for pinning each against published vectors. */
+uint64_t ember_oracle_fnv1a_words(uint64_t parent, const int32_t *tokens, int32_t n);
+uint64_t ember_oracle_fmix64(uint64_t h);
+int32_t ember_oracle_bm_match_prefix(EmberOracleBM *bm, const int32_t *tokens, int32_t n, int32_t *out_blocks);
+uint64_t ember_oracle_bm_seal(EmberOracleBM *bm, int32_t block, uint64_t parent, const int32_t *tokens, int32_t n);
+int32_t ember_oracle_bm_refcount(const EmberOracleBM *bm, int32_t block);
+uint64_t ember_oracle_bm_hit_tokens(const EmberOracleBM *bm);
+uint64_t ember_oracle_bm_lookup_tokens(const EmberOracleBM *bm);
+int32_t ember_oracle_bm_check(const EmberOracleBM *bm, char *buf, int32_t buflen);
+void ember_oracle_bm_states(const EmberOracleBM *bm, uint8_t *out);
+/* The additive fork / copy-on-write semantics (no reference counterpart):
+ * share() takes one more reference on each held block; copy_on_write(b)
+ * returns b when its refcount is 1, else drops one reference and returns
+ * allocate() (or -1). Pinned: invariants only (parity unpinned vs Ember,
+ * which has no such call). */
+int32_t ember_oracle_bm_share(EmberOracleBM *bm, const int32_t *blocks, int32_t n);
+int32_t ember_oracle_bm_copy_on_write(EmberOracleBM *bm, int32_t block);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EMBER_ORACLE_H */

@@ -1,0 +1,65 @@
+"""The C ABI library loads without a GPU and exports every function include/*.h declares."""
+import ctypes
+import re
+from pathlib import Path
+
+import ember_amd
+from ember_amd import _lib
+
+HEADERS = sorted((Path(__file__).resolve().parent.parent / "include").glob("*.h"))
+
+
+def _declared():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        for m in re.finditer(r"\b(ember_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_every_declared_function_is_exported_and_bound():
+    names = _declared()
+    assert len(names) > 30
+    so = ctypes.CDLL(str(_lib.LIB_PATH))
+    for n in sorted(names):
+        assert hasattr(so, n), f"{n} is declared in include/ but not exported"
+    assert names == set(_lib.PROTOTYPES), "the ctypes binding and the header disagree"
+
+
+def test_struct_layouts_and_version():
+    lib = ember_amd.lib()
+    assert lib.ember_hip_abi_version() == _lib.ABI_VERSION
+    for i, st in enumerate(_lib.STRUCTS):
+        assert lib.ember_hip_sizeof(i) == ctypes.sizeof(st), st.__name__
+    assert lib.ember_hip_sizeof(99) == -1
+
+
+def test_launchers_reject_bad_arguments_without_a_gpu():
+    lib = ember_amd.lib()
+    a = _lib.QkvArgs()
+    a.head_dim, a.n_heads, a.n_kv = 64, 16, 8
+    assert lib.ember_hip_kv_append(a, None) == _lib.ERR_INVALID
+    assert "head_dim 64" in _lib.last_error()
+    at = _lib.AttnArgs()
+    at.head_dim, at.n_heads, at.n_kv = 128, 16, 1  # 16 query heads per kv head: more than 8
+    assert lib.ember_hip_paged_decode(at, None) == _lib.ERR_INVALID
+    at.n_kv, at.max_blocks, at.num_blocks, at.T, at.num_splits, at.split_len = 8, 4, 4, 1, 1, 24
+    assert lib.ember_hip_paged_decode(at, None) == _lib.ERR_INVALID  # split_len not a multiple of 16
+    assert "split_len" in _lib.last_error()
+    pf = _lib.PrefillArgs()
+    pf.head_dim, pf.n_heads, pf.n_kv, pf.dtype = 128, 16, 8, _lib.DTYPE_F32
+    assert lib.ember_hip_prefill_attn(pf, None) == _lib.ERR_INVALID
+    assert lib.ember_hip_copy_pages(None, None) == _lib.ERR_INVALID
+    # T = 0 is a no-op, not an error
+    at.split_len, at.T = 512, 0
+    assert lib.ember_hip_paged_decode(at, None) == _lib.OK
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    import pytest
+
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libember_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(ImportError):
+        _lib.lib()

@@ -1,0 +1,260 @@
+"""GPU parity of the gfx950 kernels, called through the C ABI, against the CPU oracle.
+
+Tolerances (north star): page placement and slot indices bit-exact; attention
+within 2e-3 relative error for f16 KV and 1e-5 for f32 KV, where the relative
+error of a result is max|got - want| / max|want| over each (token, head)
+vector, worst vector reported (helpers.rel_err).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ember_amd import kernels as K
+from helpers import D, PAGE, attention_f64, make_step, rel_err
+
+pytestmark = pytest.mark.gpu
+
+H, KVH = 16, 8
+W = (H + 2 * KVH) * D
+THETA = 1e6
+
+
+def _pools(NB, dtype, fill=0.0, dev="cuda"):
+    k = torch.full((NB, KVH, PAGE, D), fill, dtype=dtype, device=dev)
+    return k, k.clone()
+
+
+def _host(t):
+    a = t.cpu().numpy()
+    return a.view(np.uint16) if a.dtype == np.float16 else a
+
+
+def _random_pools(rng, step, NB, f16):
+    """Pools holding random K/V at every cached position, NaN in every other slot (never written)."""
+    k = np.full((NB, KVH, PAGE, D), np.nan, np.float32)
+    v = k.copy()
+    for s in range(step.S):
+        ctx = int(step.positions[step.query_start[s + 1] - 1]) + 1
+        for p0 in range(0, ctx, PAGE):
+            b = step.tables[s, p0 // PAGE]
+            n = min(PAGE, ctx - p0)
+            k[b, :, :n] = rng.standard_normal((KVH, n, D)) * 0.35
+            v[b, :, :n] = rng.standard_normal((KVH, n, D))
+    if f16:
+        k, v = k.astype(np.float16), v.astype(np.float16)
+    return k, v
+
+
+# ---- fused QK-norm + RoPE + append ----
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("bias,norm", [(False, True), (True, True), (False, False)])
+def test_append_matches_oracle(rng, device, dtype, bias, norm):
+    NB = 64
+    step = make_step(rng, [1, 16, 17, 200, 33], [1, 16, 2, 5, 3], NB)
+    qkv = rng.standard_normal((step.T, W)).astype(np.float32)
+    qn = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    kn = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32) if norm else None
+    bs = (0.1 * rng.standard_normal(W)).astype(np.float32) if bias else None
+    f16 = dtype == torch.float16
+    qkv_in = qkv.astype(np.float16) if f16 else qkv
+    inv = oracle.inv_freq(THETA, D)
+    # Sentinel pools: a slot never written keeps its NaN pattern.
+    sent = np.uint16(0x7E01)
+    kp, vp = _pools(NB, dtype, float("nan"), device)
+    if f16:
+        kp.view(torch.int16).fill_(int(sent))
+        vp.view(torch.int16).fill_(int(sent))
+    q_out = torch.empty((step.T, H, D), dtype=dtype, device=device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    dv = lambda a: None if a is None else torch.from_numpy(a).to(device)  # noqa: E731
+    K.qk_norm_rope_store(torch.from_numpy(qkv_in).to(device), q_out, kp, vp, ints, n_heads=H, n_kv=KVH,
+                         inv_freq_dev=dv(inv), q_norm=dv(qn), k_norm=dv(kn), bias=dv(bs))
+    torch.cuda.synchronize()
+
+    ko = np.full((NB, KVH, PAGE, D), sent if f16 else np.nan, np.uint16 if f16 else np.float32)
+    vo = ko.copy()
+    q_ref = oracle.append_layer(qkv_in.astype(np.float32), step.positions, step.query_start, step.tables, ko, vo,
+                                n_heads=H, n_kv=KVH, inv_freq_=inv, q_norm=qn, k_norm=kn, bias=bs, num_blocks=NB,
+                                kv_f16=f16)
+    kg, vg = _host(kp), _host(vp)
+    written = (lambda a: a != sent) if f16 else (lambda a: ~np.isnan(a))
+    written_o = written(ko)
+    assert np.array_equal(written(kg), written_o), "the set of written K slots differs"
+    assert np.array_equal(written(vg), written(vo)) and np.array_equal(written(vo), written_o)
+    assert np.array_equal(vg[written_o], vo[written_o])  # V is stored as given (clamped and rounded in f16)
+    if f16:
+        kgf, kof = kg.view(np.float16).astype(np.float32), ko.view(np.float16).astype(np.float32)
+        diff_bits = np.abs(kg.astype(np.int32) - ko.astype(np.int32))[written_o]
+        assert diff_bits.max() <= 1, "K differs from the oracle by more than one f16 ulp"
+        assert (diff_bits == 0).mean() > 0.999
+        qg = q_out.float().cpu().numpy()
+        np.testing.assert_allclose(qg, q_ref.astype(np.float16).astype(np.float32), rtol=1e-3, atol=1e-3)
+        assert np.isfinite(kgf[written_o]).all() and np.isfinite(kof[written_o]).all()
+    else:
+        np.testing.assert_allclose(kg[written_o], ko[written_o], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(q_out.cpu().numpy(), q_ref, rtol=1e-5, atol=1e-6)
+
+
+def test_append_far_positions_and_clamp(rng, device):
+    """Positions up to 40959 (Qwen3 max), and V beyond the f16 range is clamped to +-65504."""
+    NB = 2600
+    step = make_step(rng, [40960, 1000], [2, 1], NB, max_blocks=2560)
+    qkv = rng.standard_normal((step.T, W)).astype(np.float32)
+    qkv[:, (H + KVH) * D:(H + KVH) * D + 4] = [1e5, -1e5, 7e4, 65504.0]
+    kp, vp = _pools(NB, torch.float32, 0.0, device)
+    q_out = torch.empty((step.T, H, D), dtype=torch.float32, device=device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    inv = oracle.inv_freq(THETA, D)
+    K.qk_norm_rope_store(torch.from_numpy(qkv).to(device), q_out, kp, vp, ints, n_heads=H, n_kv=KVH,
+                         inv_freq_dev=torch.from_numpy(inv).to(device),
+                         q_norm=torch.ones(D, device=device), k_norm=torch.ones(D, device=device))
+    ko, vo = np.zeros((NB, KVH, PAGE, D), np.float32), np.zeros((NB, KVH, PAGE, D), np.float32)
+    q_ref = oracle.append_layer(qkv, step.positions, step.query_start, step.tables, ko, vo, n_heads=H, n_kv=KVH,
+                                inv_freq_=inv, q_norm=np.ones(D, np.float32), k_norm=np.ones(D, np.float32),
+                                num_blocks=NB, kv_f16=False)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(q_out.cpu().numpy(), q_ref, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(kp.cpu().numpy(), ko, rtol=2e-5, atol=2e-5)
+    # f16 pools clamp V
+    kh, vh = _pools(NB, torch.float16, 0.0, device)
+    qh = torch.empty((step.T, H, D), dtype=torch.float16, device=device)
+    K.qk_norm_rope_store(torch.from_numpy(qkv.astype(np.float16)).to(device), qh, kh, vh, ints, n_heads=H, n_kv=KVH,
+                         inv_freq_dev=torch.from_numpy(inv).to(device),
+                         q_norm=torch.ones(D, device=device), k_norm=torch.ones(D, device=device))
+    torch.cuda.synchronize()
+    t = step.T - 1
+    s, p = step.token_seq[t], step.positions[t]
+    row = vh[step.tables[s, p // PAGE], 0, p % PAGE, :4].float().cpu().numpy()
+    assert row.tolist() == [65504.0, -65504.0, 65504.0, 65504.0]
+
+
+# ---- paged decode attention ----
+
+def _run_decode(q, kp, vp, step, NB, device, **kw):
+    dtype = kp.dtype
+    out = torch.full((step.T, H, D), float("nan"), dtype=dtype, device=device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    K.paged_attention(torch.from_numpy(q).to(device), kp, vp, out, ints, n_heads=H, n_kv=KVH, **kw)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("split_len", [16, 64, 512, 8192])
+def test_decode_f32_matches_oracle(rng, device, split_len):
+    NB = 1200
+    ctxs = [1, 15, 16, 17, 100, 511, 512, 513, 1500, 4096]
+    step = make_step(rng, ctxs, [1] * len(ctxs), NB)
+    k, v = _random_pools(rng, step, NB, f16=False)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float32)
+    out = _run_decode(q, torch.from_numpy(k).to(device), torch.from_numpy(v).to(device), step, NB, device,
+                      split_len=split_len).cpu().numpy()
+    want = oracle.attention_layer(q, step.positions, step.query_start, step.tables, np.nan_to_num(k), np.nan_to_num(v),
+                                  n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=False, threads=8)
+    assert np.isfinite(out).all()
+    assert rel_err(out, want) < 1e-5
+    assert rel_err(out, attention_f64(q, step, np.nan_to_num(k), np.nan_to_num(v), H, KVH)) < 1e-5
+
+
+def test_decode_f16_matches_oracle(rng, device):
+    NB = 2400
+    ctxs = list(rng.integers(256, 4097, 12)) + [1, 2, 16, 17]
+    step = make_step(rng, ctxs, [1] * len(ctxs), NB)
+    k, v = _random_pools(rng, step, NB, f16=True)
+    q32 = rng.standard_normal((step.T, H, D)).astype(np.float32)
+    q16 = q32.astype(np.float16)
+    out = _run_decode(q16, torch.from_numpy(k).to(device), torch.from_numpy(v).to(device), step, NB, device)
+    got = out.float().cpu().numpy()
+    kf, vf = np.nan_to_num(k.astype(np.float32)), np.nan_to_num(v.astype(np.float32))
+    # against the f32 CPU path on the same (f16-valued) inputs
+    want = oracle.attention_layer(q16.astype(np.float32), step.positions, step.query_start, step.tables, kf, vf,
+                                  n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=False, threads=8)
+    assert rel_err(got, want) < 2e-3
+    # and against the f32 CPU path with an f32 query: the error budget of f16 storage
+    want32 = oracle.attention_layer(q32, step.positions, step.query_start, step.tables, kf, vf, n_heads=H, n_kv=KVH,
+                                    num_blocks=NB, kv_f16=False, threads=8)
+    assert rel_err(got, want32) < 2e-3
+
+
+def test_decode_is_batch_invariant(rng, device):
+    """A token's output is bit-identical alone, in a batch, and with any number of splits launched."""
+    NB = 1600
+    ctxs = [3000, 700, 64, 1, 2049]
+    step = make_step(rng, ctxs, [1] * len(ctxs), NB)
+    k, v = _random_pools(rng, step, NB, f16=True)
+    kp, vp = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float16)
+    full = _run_decode(q, kp, vp, step, NB, device).cpu().numpy().view(np.uint16)
+    for t in range(step.T):
+        s = step.token_seq[t]
+        one = make_step(rng, [ctxs[s]], [1], NB)
+        one.tables = step.tables[s:s + 1]
+        alone = _run_decode(q[t:t + 1], kp, vp, one, NB, device).cpu().numpy().view(np.uint16)
+        assert np.array_equal(alone[0], full[t]), f"token {t} differs alone vs in the batch"
+        # a launch with more splits than this token needs (as in a batch with a longer context)
+        wide = _run_decode(q[t:t + 1], kp, vp, one, NB, device, num_splits=8).cpu().numpy().view(np.uint16)
+        assert np.array_equal(wide[0], full[t])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_verify_run_equals_sequential_decode(rng, device, dtype):
+    """q_len = 5 runs (speculative verify) read each page once for 5 tokens; every token's output is
+    bit-identical to decoding it alone."""
+    NB = 900
+    base = [511, 512, 1000, 2045, 5, 16, 27]
+    n = 5
+    step = make_step(rng, [c + n for c in base], [n] * len(base), NB)
+    f16 = dtype == torch.float16
+    k, v = _random_pools(rng, step, NB, f16=f16)
+    kp, vp = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float16 if f16 else np.float32)
+    runs = K.decode_runs(K.StepInts(step.positions, step.token_seq, step.tables, NB), range(step.T), max_run=n)
+    assert runs[1].tolist() == [n] * len(base)
+    verify = _run_decode(q, kp, vp, step, NB, device, runs=runs).cpu().numpy()
+    seq = _run_decode(q, kp, vp, step, NB, device).cpu().numpy()  # one run per token
+    assert np.array_equal(verify.view(np.uint8), seq.view(np.uint8))
+    # runs of 2 and 3 too
+    for m in (2, 3, 8):
+        r = K.decode_runs(K.StepInts(step.positions, step.token_seq, step.tables, NB), range(step.T), max_run=m)
+        other = _run_decode(q, kp, vp, step, NB, device, runs=r).cpu().numpy()
+        assert np.array_equal(other.view(np.uint8), seq.view(np.uint8))
+    want = oracle.attention_layer(q.astype(np.float32), step.positions, step.query_start, step.tables,
+                                  np.nan_to_num(k.astype(np.float32)), np.nan_to_num(v.astype(np.float32)),
+                                  n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=False, threads=8)
+    assert rel_err(verify.astype(np.float32), want) < (2e-3 if f16 else 1e-5)
+
+
+def test_decode_group_sizes(rng, device):
+    """GQA groups 1, 2, 4, 8 (n_heads / n_kv)."""
+    NB = 300
+    for g, kvh in ((1, 8), (2, 8), (4, 4), (8, 2)):
+        h = g * kvh
+        step = make_step(rng, [700, 33, 1], [1, 1, 1], NB)
+        k = rng.standard_normal((NB, kvh, PAGE, D)).astype(np.float32)
+        v = rng.standard_normal((NB, kvh, PAGE, D)).astype(np.float32)
+        q = rng.standard_normal((step.T, h, D)).astype(np.float32)
+        out = torch.empty((step.T, h, D), dtype=torch.float32, device=device)
+        ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+        K.paged_attention(torch.from_numpy(q).to(device), torch.from_numpy(k).to(device), torch.from_numpy(v).to(device),
+                          out, ints, n_heads=h, n_kv=kvh, split_len=256)
+        torch.cuda.synchronize()
+        want = oracle.attention_layer(q, step.positions, step.query_start, step.tables, k, v, n_heads=h, n_kv=kvh,
+                                      num_blocks=NB, kv_f16=False)
+        assert rel_err(out.cpu().numpy(), want) < 1e-5, f"group {g}"
+
+
+def test_copy_pages(rng, device):
+    NB, L = 40, 3
+    stride = NB * KVH * PAGE * D
+    kp = torch.from_numpy(rng.standard_normal(L * stride).astype(np.float16)).to(device)
+    vp = torch.from_numpy(rng.standard_normal(L * stride).astype(np.float16)).to(device)
+    k0, v0 = kp.cpu().numpy().reshape(L, NB, -1), vp.cpu().numpy().reshape(L, NB, -1)
+    src, dst = [3, 7, 11], [30, 31, 5]
+    K.copy_pages(kp, vp, src, dst, n_layers=L, layer_stride=stride, n_kv=KVH, num_blocks=NB)
+    torch.cuda.synchronize()
+    k1, v1 = kp.cpu().numpy().reshape(L, NB, -1), vp.cpu().numpy().reshape(L, NB, -1)
+    ek, ev = k0.copy(), v0.copy()
+    for s, d in zip(src, dst):
+        ek[:, d], ev[:, d] = k0[:, s], v0[:, s]
+    assert np.array_equal(k1.view(np.uint16), ek.view(np.uint16)) and np.array_equal(v1.view(np.uint16), ev.view(np.uint16))

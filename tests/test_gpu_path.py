@@ -1,0 +1,256 @@
+"""GPU parity of the whole paged-KV path (C++ HipPagedKv + BlockManager through the C ABI) against the
+CPU oracle, on the BASELINE.json workloads at test scale.
+
+Tolerances: slots and pages bit-exact; attention within 2e-3 (f16 KV) / 1e-5 (f32 KV) relative error
+(helpers.rel_err), against the oracle's f32 CPU path fed the same activations.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ember_amd import BlockManager
+from ember_amd.paged_kv import PagedKv, StepBatch
+from helpers import D, PAGE, rel_err
+
+pytestmark = pytest.mark.gpu
+
+H, KVH = 16, 8
+W = (H + 2 * KVH) * D
+EPS, THETA = 1e-6, 1e6
+
+
+class World:
+    """The GPU path and the oracle side by side, driven with identical steps."""
+
+    def __init__(self, device, dtype, num_blocks, n_layers=1, max_position=8192, max_batch_tokens=1024, seed=0):
+        self.dev, self.dtype, self.NB, self.L = device, dtype, num_blocks, n_layers
+        self.kv = PagedKv(n_layers=n_layers, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,
+                          max_position=max_position, num_blocks=num_blocks, max_batch_tokens=max_batch_tokens,
+                          max_seqs=64, dtype=dtype)
+        r = np.random.default_rng(seed)
+        self.qn = [(1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(n_layers)]
+        self.kn = [(1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(n_layers)]
+        self.qn_d = [torch.from_numpy(a).to(device) for a in self.qn]
+        self.kn_d = [torch.from_numpy(a).to(device) for a in self.kn]
+        # the oracle keeps f32 pools with the same number of blocks (+ the spare, never read)
+        self.ko = [np.zeros((num_blocks + 1, KVH, PAGE, D), np.float32) for _ in range(n_layers)]
+        self.vo = [np.zeros_like(self.ko[0]) for _ in range(n_layers)]
+        self.inv = oracle.inv_freq(THETA, D)
+
+    def step(self, positions, query_start, tables, qkv_layers, check=True):
+        """One step: plan, then per layer append + attention. qkv_layers: [L][T, W] f32 values (f16-exact
+        when the pools are f16). Returns (gpu outputs, oracle outputs or None when not check) per layer,
+        f32 arrays [T, H, D]."""
+        positions = np.asarray(positions, np.int32)
+        query_start = np.asarray(query_start, np.int32)
+        tables = np.asarray(tables, np.int32)
+        S, T = tables.shape[0], positions.size
+        ctx = [int(positions[query_start[s + 1] - 1]) + 1 for s in range(S)]
+        self.kv.plan(StepBatch(tokens=[0] * T, positions=positions.tolist(), query_start=query_start.tolist(),
+                               context_len=ctx, block_tables=tables.reshape(-1).tolist(), max_blocks=tables.shape[1]))
+        res = []
+        for layer in range(self.L):
+            qkv = qkv_layers[layer]
+            qkv_d = torch.from_numpy(qkv).to(self.dev, self.dtype)
+            out = torch.full((T, H, D), float("nan"), dtype=self.dtype, device=self.dev)
+            self.kv.layer(layer, qkv_d, out, q_norm=self.qn_d[layer], k_norm=self.kn_d[layer])
+            q_ref = oracle.append_layer(qkv, positions, query_start, tables, self.ko[layer], self.vo[layer], n_heads=H,
+                                        n_kv=KVH, inv_freq_=self.inv, eps=EPS, q_norm=self.qn[layer],
+                                        k_norm=self.kn[layer], num_blocks=self.NB + 1, kv_f16=False)
+            want = None
+            if check:
+                want = oracle.attention_layer(q_ref, positions, query_start, tables, self.ko[layer], self.vo[layer],
+                                              n_heads=H, n_kv=KVH, num_blocks=self.NB + 1, kv_f16=False, threads=8)
+            torch.cuda.synchronize()
+            res.append((out.float().cpu().numpy(), want))
+        return res
+
+    def pools(self, layer):
+        return (self.kv.pool_view(layer, "k").float().cpu().numpy(), self.kv.pool_view(layer, "v").float().cpu().numpy())
+
+    @property
+    def tol(self):
+        return 2e-3 if self.dtype == torch.float16 else 1e-5
+
+
+def _acts(rng, T, L, f16):
+    a = [rng.standard_normal((T, W)).astype(np.float32) for _ in range(L)]
+    return [x.astype(np.float16).astype(np.float32) for x in a] if f16 else a
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_config1_prefill_then_decode(rng, device, dtype):
+    """one Qwen3-0.6B-shaped layer, batch 1, a 512-token prefill into 16-token pages,
+    then 128 decode steps; the block table is the first 40 entries of a seeded permutation of 4096 pages."""
+    f16 = dtype == torch.float16
+    w = World(device, dtype, num_blocks=4096, max_position=640)
+    table = rng.permutation(4096)[:40].astype(np.int32)[None, :]
+    outs = w.step(np.arange(512), [0, 512], table, _acts(rng, 512, 1, f16))
+    worst = rel_err(*outs[0])
+    for pos in range(512, 640):
+        outs = w.step([pos], [0, 1], table, _acts(rng, 1, 1, f16))
+        worst = max(worst, rel_err(*outs[0]))
+    assert worst < w.tol, f"worst relative error {worst:.2e}"
+    # page placement: exactly the table's 40 pages hold data, slot for slot
+    kg, vg = w.pools(0)
+    written_g = np.abs(kg).sum(axis=(1, 3)) > 0  # [NB+1, 16] per (block, slot), any kv head
+    written_o = np.abs(w.ko[0]).sum(axis=(1, 3)) > 0
+    assert np.array_equal(written_g, written_o)
+    assert set(np.nonzero(written_g.any(axis=1))[0]) == set(table[0].tolist())
+    tolk = 2e-3 if f16 else 1e-5
+    assert rel_err(kg[table[0]], w.ko[0][table[0]]) < tolk and rel_err(vg[table[0]], w.vo[0][table[0]]) < tolk
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_mixed_step(rng, device, dtype):
+    """Prompt chunks and decodes in one step (continuous batching), 2 layers."""
+    f16 = dtype == torch.float16
+    w = World(device, dtype, num_blocks=600, n_layers=2)
+    perm = rng.permutation(600).astype(np.int32)
+    ctx0 = [0, 100, 1030, 0, 16, 511]          # cached before the step
+    new = [40, 1, 1, 16, 1, 37]                # new tokens this step
+    tables = np.zeros((6, 100), np.int32)
+    at = 0
+    for s in range(6):
+        n_pages = (ctx0[s] + new[s] + PAGE - 1) // PAGE
+        tables[s, :n_pages] = perm[at:at + n_pages]
+        at += n_pages
+    # fill the cached contexts through the path itself (prefill steps), then the mixed step
+    for s in range(6):
+        if ctx0[s]:
+            w.step(np.arange(ctx0[s]), [0, ctx0[s]], tables[s:s + 1], _acts(rng, ctx0[s], 2, f16), check=False)
+    pos, qs = [], [0]
+    for s in range(6):
+        pos += list(range(ctx0[s], ctx0[s] + new[s]))
+        qs.append(len(pos))
+    res = w.step(pos, qs, tables, _acts(rng, len(pos), 2, f16))
+    for got, want in res:
+        assert rel_err(got, want) < w.tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_verify_rollback_equals_sequential_decode(rng, device, dtype):
+    """BASELINE config 5 at test scale: 4 drafts + the last token verified in one step (q_len 5, causal
+    inside the window), rollback with accepted count ~U{0..4}; outputs and the slots that stay valid are
+    bit-identical to plain one-token-per-step decoding."""
+    f16 = dtype == torch.float16
+    B, k = 8, 4
+    c = rng.integers(512, 1500, B)              # cached context per sequence
+    NB = int(((c + k + 2 + PAGE) // PAGE).sum()) + 8
+    perm = rng.permutation(NB).astype(np.int32)
+    mb = int((c.max() + k + 2 + PAGE) // PAGE)
+    tables = np.zeros((B, mb), np.int32)
+    at = 0
+    for s in range(B):
+        n_pages = int((c[s] + k + 2 + PAGE - 1) // PAGE)
+        tables[s, :n_pages] = perm[at:at + n_pages]
+        at += n_pages
+    A = World(device, dtype, num_blocks=NB, max_position=mb * PAGE)   # verify world
+    C = World(device, dtype, num_blocks=NB, max_position=mb * PAGE)   # sequential world
+    for s in range(B):  # identical cached prefixes in both worlds
+        acts = _acts(rng, int(c[s]), 1, f16)
+        A.step(np.arange(c[s]), [0, c[s]], tables[s:s + 1], acts, check=False)
+        C.step(np.arange(c[s]), [0, c[s]], tables[s:s + 1], acts, check=False)
+    win = _acts(rng, B * (k + 1), 1, f16)[0].reshape(B, k + 1, W)
+    pos = np.concatenate([np.arange(c[s], c[s] + k + 1) for s in range(B)])
+    qs = np.arange(0, B * (k + 1) + 1, k + 1)
+    (va, _), = A.step(pos, qs, tables, [win.reshape(-1, W)])
+    accepted = rng.integers(0, k + 1, B)
+    # the sequential world decodes only the accepted window tokens, one step per position
+    seq_out = np.zeros_like(va).reshape(B, k + 1, H, D)
+    for i in range(k + 1):
+        live = [s for s in range(B) if i <= accepted[s]]
+        (o, _), = C.step([c[s] + i for s in live], np.arange(len(live) + 1), tables[live],
+                         [np.stack([win[s, i] for s in live])])
+        for j, s in enumerate(live):
+            seq_out[s, i] = o[j]
+    va = va.reshape(B, k + 1, H, D)
+    for s in range(B):
+        a = va[s, :accepted[s] + 1]
+        b = seq_out[s, :accepted[s] + 1]
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"sequence {s}: verify != sequential decode"
+    # after rollback the next token goes to position c + accepted + 1 in both worlds
+    nxt = _acts(rng, B, 1, f16)[0]
+    npos = [int(c[s] + accepted[s] + 1) for s in range(B)]
+    (oa, wa), = A.step(npos, np.arange(B + 1), tables, [nxt])
+    (oc, _), = C.step(npos, np.arange(B + 1), tables, [nxt])
+    assert np.array_equal(oa.view(np.uint32), oc.view(np.uint32))
+    assert rel_err(oa, wa) < A.tol
+    ka, va_ = A.pools(0)
+    kc, vc = C.pools(0)
+    for s in range(B):
+        for p in range(npos[s] + 1):  # every slot that is valid after the rollback
+            b, sl = tables[s, p // PAGE], p % PAGE
+            assert np.array_equal(ka[b, :, sl], kc[b, :, sl]) and np.array_equal(va_[b, :, sl], vc[b, :, sl])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_fork_copy_on_write(rng, device, dtype):
+    """BASELINE config 3's sharing at test scale: sequences share a system prefix of full sealed pages
+    (refcounted via match_prefix) plus a partial last page (via share, a fork); the first write into the
+    shared partial page copies it (copy_on_write + a device page copy), bit-exactly, over every layer."""
+    f16 = dtype == torch.float16
+    NB, L, n_children = 64, 3, 6
+    prefix_len = 4 * PAGE + 5                 # 4 full pages + 5 tokens in a partial page
+    bm = BlockManager(NB, True)
+    w = World(device, dtype, num_blocks=NB, n_layers=L, max_position=256)
+    tokens = rng.integers(2, 1000, prefix_len).tolist()
+    parent = [bm.allocate() for _ in range(5)]
+    chain = 0
+    for i in range(4):
+        chain = bm.seal(parent[i], chain, tokens[i * PAGE:(i + 1) * PAGE])
+    tab = np.zeros((1, 8), np.int32)
+    tab[0, :5] = parent
+    w.step(np.arange(prefix_len), [0, prefix_len], tab, _acts(rng, prefix_len, L, f16), check=False)
+    # children: the sealed pages by prefix match, the partial page by fork
+    kids = []
+    for _ in range(n_children):
+        got = bm.match_prefix(tokens[:-1])
+        assert got == parent[:4]
+        bm.share([parent[4]])
+        kids.append(got + [parent[4]])
+    for b in parent[:4]:
+        assert bm.refcount(b) == 1 + n_children
+    assert bm.refcount(parent[4]) == 1 + n_children
+    k_before = [w.pools(layer) for layer in range(L)]
+    # every holder about to write position prefix_len: copy-on-write
+    seqs = kids + [list(parent)]
+    src, dst = [], []
+    for blocks in seqs:
+        nb = bm.copy_on_write(blocks[4])
+        assert nb >= 0
+        if nb != blocks[4]:
+            src.append(blocks[4])
+            dst.append(nb)
+            blocks[4] = nb
+    assert len(src) == n_children and bm.refcount(parent[4]) == 1  # the last holder writes in place
+    w.kv.copy_blocks(src, dst)
+    for o in range(L):  # mirror the copies in the oracle's pools
+        for s_, d_ in zip(src, dst):
+            w.ko[o][d_] = w.ko[o][s_]
+            w.vo[o][d_] = w.vo[o][s_]
+    torch.cuda.synchronize()
+    for layer in range(L):
+        kg, vg = w.pools(layer)
+        k0, v0 = k_before[layer]
+        for s_, d_ in zip(src, dst):  # page copies are bit-exact, every layer, K and V
+            assert np.array_equal(kg[d_].view(np.uint32), k0[s_].view(np.uint32))
+            assert np.array_equal(vg[d_].view(np.uint32), v0[s_].view(np.uint32))
+    tables = np.zeros((len(seqs), 8), np.int32)
+    for i, blocks in enumerate(seqs):
+        tables[i, :5] = blocks
+    res = w.step([prefix_len] * len(seqs), np.arange(len(seqs) + 1), tables, _acts(rng, len(seqs), L, f16))
+    for got, want in res:
+        assert rel_err(got, want) < w.tol
+    kg, _ = w.pools(0)
+    k0, _ = k_before[0]
+    slot = prefix_len % PAGE
+    for i, blocks in enumerate(seqs):  # each sequence's new token landed in its own page
+        assert not np.array_equal(kg[blocks[4], :, slot], k0[parent[4], :, slot])
+        assert np.array_equal(kg[blocks[4], :, :slot].view(np.uint32), k0[parent[4], :, :slot].view(np.uint32))
+    for b in parent[:4]:  # shared sealed pages were never written
+        assert np.array_equal(kg[b].view(np.uint32), k0[b].view(np.uint32))
+    for blocks in seqs:
+        bm.release_all(blocks)
+    assert bm.check() == "" and bm.used() == 0 and bm.cached() == 4
