@@ -45,6 +45,7 @@ class AttnArgs(ctypes.Structure):
         ("scale", c_float), ("out", c_void_p), ("num_splits", c_int32), ("split_len", c_int32),
         ("part_acc", c_void_p), ("part_ml", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
         ("run_first", c_void_p), ("run_count", c_void_p), ("num_runs", c_int32), ("max_run", c_int32),
+        ("work", c_void_p), ("num_work", c_int32),
     ]
 
 

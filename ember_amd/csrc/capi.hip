@@ -115,6 +115,12 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
             return set_error(EMBER_ERR_INVALID, "paged_decode: max_run must be 1..%d (got %d)", EMBER_MAX_RUN, a->max_run);
         max_run = a->max_run;
     }
+    if (a->work) {
+        const long long runs = a->run_first ? a->num_runs : a->T;
+        if (a->num_work < 0 || a->num_work > runs * a->num_splits ||
+            static_cast<long long>(a->num_work) * a->n_kv > 0x7fffffffLL)
+            return set_error(EMBER_ERR_INVALID, "paged_decode: num_work %d out of range", a->num_work);
+    }
     const int need = G * max_run;
     int rows = 0;
     for (int r : kDecodeRowInstances)

@@ -71,9 +71,9 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     inv_freq_ = device_alloc<float>(inv.size());
     EMBER_HIP_CHECK(hipMemcpyAsync(inv_freq_, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice, stream_));
 
-    // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables.
+    // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables, work items.
     ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
-                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + 64;
+                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) + 64;
     dev_ints_ = device_alloc<int32_t>(ints_capacity_);
     for (int i = 0; i < 2; i++) {
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
@@ -119,6 +119,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     decode_.clear();
     run_first_.clear();
     run_count_.clear();
+    run_ctx_.clear();
     tile_start_.clear();
     tile_end_.clear();
     tile_seq_.clear();
@@ -149,8 +150,11 @@ void HipPagedKv::plan(const StepBatch &b) {
         } else {
             for (int t = q0; t < q1; t += EMBER_MAX_RUN) {
                 const int n = std::min(EMBER_MAX_RUN, q1 - t);
+                int run_ctx = 0;
+                for (int i = 0; i < n; i++) run_ctx = std::max(run_ctx, b.positions[static_cast<size_t>(t + i)] + 1);
                 run_first_.push_back(static_cast<int32_t>(decode_.size()));
                 run_count_.push_back(n);
+                run_ctx_.push_back(run_ctx);
                 max_run_ = std::max(max_run_, n);
                 for (int i = 0; i < n; i++) decode_.push_back(t + i);
             }
@@ -163,6 +167,27 @@ void HipPagedKv::plan(const StepBatch &b) {
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
     splits_ = std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
+
+    // Decode work items (run, split), dispatched in list order: every full
+    // split first, then the partial last splits, longest first, so the short
+    // ones fill the tail of the launch.
+    work_.clear();
+    std::vector<std::pair<int, int>> partial;  // (keys, run)
+    for (int r = 0; r < decode_runs_; r++) {
+        const int ctx = run_ctx_[static_cast<size_t>(r)];
+        const int full = ctx / opt_.split_len;
+        for (int s = 0; s < full; s++) {
+            work_.push_back(r);
+            work_.push_back(s);
+        }
+        if (ctx % opt_.split_len) partial.emplace_back(ctx % opt_.split_len, r);
+    }
+    std::stable_sort(partial.begin(), partial.end(), [](const auto &a, const auto &b) { return a.first > b.first; });
+    for (const auto &[keys, r] : partial) {
+        work_.push_back(r);
+        work_.push_back(run_ctx_[static_cast<size_t>(r)] / opt_.split_len);
+    }
+    num_work_ = static_cast<int>(work_.size() / 2);
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.
     stage_ ^= 1;
@@ -184,6 +209,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     put(tile_start_.data(), tile_start_.size());
     put(tile_end_.data(), tile_end_.size());
     put(tile_seq_.data(), tile_seq_.size());
+    put(work_.data(), work_.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
     EMBER_HIP_CHECK(hipMemcpyAsync(dev_ints_, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
     EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], stream_));
@@ -196,6 +222,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     d_tile_start_ = dev_ints_ + at[6];
     d_tile_end_ = dev_ints_ + at[7];
     d_tile_seq_ = dev_ints_ + at[8];
+    d_work_ = dev_ints_ + at[9];
 }
 
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {
@@ -252,6 +279,8 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         at.run_count = d_run_count_;
         at.num_runs = decode_runs_;
         at.max_run = max_run_;
+        at.work = d_work_;
+        at.num_work = num_work_;
         hipEvent_t stop = nullptr;
         if (timing_) {
             if (timing_used_ + 2 > timing_events_.size())

@@ -89,8 +89,9 @@ private:
     int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;
     const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
                   *d_run_first_ = nullptr, *d_run_count_ = nullptr, *d_tile_start_ = nullptr, *d_tile_end_ = nullptr,
-                  *d_tile_seq_ = nullptr;
-    std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, tile_start_, tile_end_, tile_seq_;
+                  *d_tile_seq_ = nullptr, *d_work_ = nullptr;
+    std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, run_ctx_, tile_start_, tile_end_, tile_seq_, work_;
+    int num_work_ = 0;
 
     bool timing_ = false;
     std::vector<hipEvent_t> timing_events_;  // start/stop pairs, reused after collect_timing

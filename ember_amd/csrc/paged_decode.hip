@@ -22,6 +22,9 @@
 //   softmax: each DPP row keeps its own running max / sum over the keys it
 //           holds (no cross-row traffic in the loop);
 //   values: each lane accumulates its 8 dims over its 4 keys.
+// Latency: block ids are wave-uniform scalar loads (they never wait on the
+// page loads), and each wave keeps the next two pages in flight in registers
+// while it works on the current one.
 // At the end: rows merge through two lane exchanges, waves through LDS,
 // splits in the separate merge kernel, all in a fixed order.
 //
@@ -45,12 +48,22 @@ constexpr int kThreads = kWaves * kWave;
 
 struct DecodeParams {
     const void *q, *k, *v;
-    const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count;
+    const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count, *work;
     void *out;
     float *part_acc, *part_ml;
-    int max_blocks, n_heads, n_kv, G, num_blocks, num_splits, split_len;
+    int max_blocks, n_heads, n_kv, G, num_blocks, num_splits, split_len, num_runs;
     float scale_log2;
 };
+
+// A load through the constant address space: with a wave-uniform address the
+// compiler emits s_load (scalar cache, lgkmcnt), which never waits for the
+// vector page loads in flight. Only for data the kernel does not write.
+template <class T>
+__device__ __forceinline__ T uniform_load(const T *p) {
+    return *(const __attribute__((address_space(4))) T *)(p);  // an address-space cast
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // One page of K and V as this lane holds it: 4 keys x 8 dims each.
 template <typename T>
@@ -59,23 +72,17 @@ struct PageRegs;
 template <>
 struct PageRegs<f16> {
     uint4 k[4], v[4];
-    bool ok;
 };
 
 template <>
 struct PageRegs<float> {
     float4 k[4][2], v[4][2];
-    bool ok;
 };
 
 template <typename T>
-__device__ __forceinline__ void load_page(PageRegs<T> &pr, const DecodeParams &p, const int32_t *table, int kvh, int page,
-                                          int lane) {
-    const int blk = table[page];
-    pr.ok = blk >= 0 && blk < p.num_blocks;
-    const int64_t base = (static_cast<int64_t>(pr.ok ? blk : 0) * p.n_kv + kvh) * (kPage * kHeadDim) + 8 * lane;
-    const T *kp = static_cast<const T *>(p.k) + base;
-    const T *vp = static_cast<const T *>(p.v) + base;
+__device__ __forceinline__ void load_page(PageRegs<T> &pr, const T *kbase, const T *vbase, int64_t page_off, int lane) {
+    const T *kp = kbase + page_off + 8 * lane;
+    const T *vp = vbase + page_off + 8 * lane;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (sizeof(T) == 2) {
@@ -149,13 +156,18 @@ __device__ __forceinline__ void unpack8(const float4 (&v)[2], float (&out)[8]) {
     out[7] = v[1].w;
 }
 
+// 2^x by the hardware instruction (v_exp_f32): exact powers of two at
+// integers, 0 at -inf; results below 2^-126 may flush to 0, which only drops
+// weights that cannot move an f32 sum.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Merges this lane's (m, l, acc) with the lane `mask` away; both lanes end
 // with the same values.
 __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8], int mask) {
     const float mo = __shfl_xor(m, mask, kWave), lo = __shfl_xor(l, mask, kWave);
     const float M = fmaxf(m, mo);
-    const float fa = m == -INFINITY ? 0.0f : exp2f(m - M);
-    const float fb = mo == -INFINITY ? 0.0f : exp2f(mo - M);
+    const float fa = m == -INFINITY ? 0.0f : exp2_hw(m - M);
+    const float fb = mo == -INFINITY ? 0.0f : exp2_hw(mo - M);
     l = l * fa + lo * fb;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -168,21 +180,37 @@ __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8],
 template <typename T, int ROWS>
 __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
     constexpr int D = kHeadDim;
-    const int run = blockIdx.x, kvh = blockIdx.y, split = blockIdx.z;
-    const int lane = static_cast<int>(threadIdx.x) % kWave, wave = static_cast<int>(threadIdx.x) / kWave;
+    // Two pages in flight per wave while it works on a third, unless the
+    // query rows already need the registers.
+    constexpr int STAGES = ROWS <= 4 ? 3 : 2;
+    const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int wave = uniform(static_cast<int>(threadIdx.x) / kWave);
     const int r = lane >> 4, c = lane & 15;
     const int G = p.G;
+
+    int run, kvh, split;
+    if (p.work) {
+        const int item = static_cast<int>(blockIdx.x) / p.n_kv;
+        kvh = static_cast<int>(blockIdx.x) % p.n_kv;
+        run = uniform_load(p.work + 2 * item);
+        split = uniform_load(p.work + 2 * item + 1);
+        if (run < 0 || run >= p.num_runs || split < 0 || split >= p.num_splits) return;  // whole work-group
+    } else {
+        run = blockIdx.x;
+        kvh = blockIdx.y;
+        split = blockIdx.z;
+    }
 
     __shared__ float red_acc[ROWS][kWaves][D];
     __shared__ float red_m[ROWS][kWaves], red_l[ROWS][kWaves];
 
     // The run: list entries first .. first + nq - 1, one sequence.
-    const int first = p.run_first ? p.run_first[run] : run;
-    int nq = p.run_count ? p.run_count[run] : 1;
+    const int first = p.run_first ? uniform_load(p.run_first + run) : run;
+    int nq = p.run_count ? uniform_load(p.run_count + run) : 1;
     nq = max(1, min(nq, ROWS / G));
     const int nrows = nq * G;
-    const int t0 = p.token_index ? p.token_index[first] : first;
-    const int32_t *table = p.tables + static_cast<int64_t>(p.token_seq[t0]) * p.max_blocks;
+    const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
+    const int32_t *table = p.tables + static_cast<int64_t>(uniform_load(p.token_seq + t0)) * p.max_blocks;
 
     int row_pos[ROWS];
     int min_pos = INT_MAX, max_pos = -1;
@@ -191,8 +219,8 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         row_pos[row] = -1;
         if (row < nrows) {
             const int li = first + row / G;
-            const int t = p.token_index ? p.token_index[li] : li;
-            row_pos[row] = p.positions[t];
+            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+            row_pos[row] = uniform_load(p.positions + t);
             min_pos = min(min_pos, row_pos[row]);
             max_pos = max(max_pos, row_pos[row]);
         }
@@ -211,7 +239,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
         if (row < nrows) {
             const int li = first + row / G;
-            const int t = p.token_index ? p.token_index[li] : li;
+            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
             const int head = kvh * G + row % G;
             const T *qp = static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c;
             if constexpr (sizeof(T) == 2) {
@@ -235,10 +263,15 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         }
     }
 
+    const T *kbase = static_cast<const T *>(p.k);
+    const T *vbase = static_cast<const T *>(p.v);
+    const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
+    const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
+
     // One page: scores, online softmax per DPP row, value accumulation.
-    auto process = [&](const PageRegs<T> &pr, int page) {
+    auto process = [&](const PageRegs<T> &pr, int page, bool ok) {
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
-        const bool fast = pr.ok && (page + 1) * kPage <= min_pos + 1;  // every key visible to every row
+        const bool fast = ok && (page + 1) * kPage <= min_pos + 1;  // every key visible to every row
         float vf[4][8];
 #pragma unroll
         for (int i = 0; i < 4; i++) unpack8(pr.v[i], vf[i]);
@@ -250,15 +283,15 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 s[i] = row16_sum(dot8(q[row], pr.k[i])) * p.scale_log2;
-                vis[i] = fast || (pr.ok && key0 + 4 * i <= row_pos[row]);
+                vis[i] = fast || (ok && key0 + 4 * i <= row_pos[row]);
                 if (!vis[i]) s[i] = -INFINITY;
             }
             const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
             const float ref = mn == -INFINITY ? 0.0f : mn;
-            const float corr = m[row] == mn ? 1.0f : exp2f(m[row] - ref);
+            const float corr = m[row] == mn ? 1.0f : exp2_hw(m[row] - ref);
             float pj[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) pj[i] = exp2f(s[i] - ref);  // exp2(-inf) = 0 for hidden keys
+            for (int i = 0; i < 4; i++) pj[i] = exp2_hw(s[i] - ref);  // 2^-inf = 0 for hidden keys
             l[row] = l[row] * corr + ((pj[0] + pj[1]) + (pj[2] + pj[3]));
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
@@ -279,15 +312,60 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 
     if (begin < end) {
         const int first_page = begin / kPage, last_page = (end - 1) / kPage;
-        PageRegs<T> A, B;
-        int pg = first_page + wave;
-        if (pg <= last_page) load_page(A, p, table, kvh, pg, lane);
-        for (; pg <= last_page; pg += 2 * kWaves) {
-            if (pg + kWaves <= last_page) load_page(B, p, table, kvh, pg + kWaves, lane);
-            process(A, pg);
-            if (pg + kWaves > last_page) break;
-            if (pg + 2 * kWaves <= last_page) load_page(A, p, table, kvh, pg + 2 * kWaves, lane);
-            process(B, pg + kWaves);
+        const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
+        // Block id of this wave's j-th page (a scalar load) and whether it lies in the pool.
+        auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
+        auto block_of = [&](int j) { return uniform_load(table + page_of(j)); };
+        auto offset_of = [&](int blk) {
+            const bool ok = blk >= 0 && blk < p.num_blocks;
+            return static_cast<int64_t>(ok ? blk : 0) * block_stride + head_off;
+        };
+        auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
+        if constexpr (STAGES == 3) {
+            // Loads are unconditional (past the wave's last page they re-read it,
+            // from cache), so every page is used with exactly two pages' loads
+            // issued after it and the wait before it is vmcnt(16), never vmcnt(0).
+            auto fetch = [&](PageRegs<T> &pr, int j) {
+                const int blk = block_of(min(j, n - 1));
+                load_page(pr, kbase, vbase, offset_of(blk), lane);
+                return blk;
+            };
+            PageRegs<T> A, B, C;
+            if (n > 0) {
+                int ba = fetch(A, 0);
+                int bb = fetch(B, 1);
+                for (int j = 0;; j += 3) {
+                    const int bc = fetch(C, j + 2);
+                    process(A, page_of(j), in_pool(ba));
+                    if (j + 1 >= n) break;
+                    ba = fetch(A, j + 3);
+                    process(B, page_of(j + 1), in_pool(bb));
+                    if (j + 2 >= n) break;
+                    bb = fetch(B, j + 4);
+                    process(C, page_of(j + 2), in_pool(bc));
+                    if (j + 3 >= n) break;
+                }
+            }
+        } else {
+            PageRegs<T> A, B;
+            int ba = 0, bb = 0;
+            if (n > 0) {
+                ba = block_of(0);
+                load_page(A, kbase, vbase, offset_of(ba), lane);
+            }
+            for (int j = 0; j < n; j += 2) {
+                if (j + 1 < n) {
+                    bb = block_of(j + 1);
+                    load_page(B, kbase, vbase, offset_of(bb), lane);
+                }
+                process(A, page_of(j), in_pool(ba));
+                if (j + 1 >= n) break;
+                if (j + 2 < n) {
+                    ba = block_of(j + 2);
+                    load_page(A, kbase, vbase, offset_of(ba), lane);
+                }
+                process(B, page_of(j + 1), in_pool(bb));
+            }
         }
     }
 
@@ -318,7 +396,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 #pragma unroll
         for (int w = 0; w < kWaves; w++) {
             const float mw = red_m[row][w];
-            const float f = mw == -INFINITY ? 0.0f : exp2f(mw - M);
+            const float f = mw == -INFINITY ? 0.0f : exp2_hw(mw - M);
             L = L + red_l[row][w] * f;
             O = O + red_acc[row][w][d] * f;
         }
@@ -356,7 +434,7 @@ __global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) 
     for (int s = 0; s < ns; s++) {
         const float ms = p.part_ml[(base + s) * 2];
         if (ms == -INFINITY) continue;
-        const float f = exp2f(ms - M);
+        const float f = exp2_hw(ms - M);
         const float ls = p.part_ml[(base + s) * 2 + 1] * f, os = p.part_acc[(base + s) * D + d] * f;
         L = any ? L + ls : ls;
         O = any ? O + os : os;
@@ -367,21 +445,23 @@ __global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) 
 }
 
 template <typename T, int ROWS>
-hipError_t launch_rows(const DecodeParams &p, int runs, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv), static_cast<unsigned>(p.num_splits));
+hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_t stream) {
+    const dim3 grid = p.work ? dim3(static_cast<unsigned>(num_work * p.n_kv))
+                             : dim3(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv),
+                                    static_cast<unsigned>(p.num_splits));
     hipLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
 template <typename T>
-hipError_t launch_typed(const DecodeParams &p, int runs, int rows, hipStream_t stream) {
+hipError_t launch_typed(const DecodeParams &p, int runs, int num_work, int rows, hipStream_t stream) {
     switch (rows) {
-        case 1: return launch_rows<T, 1>(p, runs, stream);
-        case 2: return launch_rows<T, 2>(p, runs, stream);
-        case 4: return launch_rows<T, 4>(p, runs, stream);
-        case 8: return launch_rows<T, 8>(p, runs, stream);
-        case 10: return launch_rows<T, 10>(p, runs, stream);
-        case 16: return launch_rows<T, 16>(p, runs, stream);
+        case 1: return launch_rows<T, 1>(p, runs, num_work, stream);
+        case 2: return launch_rows<T, 2>(p, runs, num_work, stream);
+        case 4: return launch_rows<T, 4>(p, runs, num_work, stream);
+        case 8: return launch_rows<T, 8>(p, runs, num_work, stream);
+        case 10: return launch_rows<T, 10>(p, runs, num_work, stream);
+        case 16: return launch_rows<T, 16>(p, runs, num_work, stream);
         default: return hipErrorInvalidValue;
     }
 }
@@ -400,6 +480,7 @@ hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t str
     p.token_index = a.token_index;
     p.run_first = a.run_first;
     p.run_count = a.run_count;
+    p.work = a.work;
     p.out = a.out;
     p.part_acc = a.part_acc;
     p.part_ml = a.part_ml;
@@ -412,9 +493,10 @@ hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t str
     p.split_len = a.split_len;
     p.scale_log2 = a.scale * kLog2e;
     const int runs = a.run_first ? a.num_runs : a.T;
-    if (runs <= 0) return hipSuccess;
-    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, rows, stream)
-                                              : launch_typed<float>(p, runs, rows, stream);
+    p.num_runs = runs;
+    if (runs <= 0 || (a.work && a.num_work <= 0)) return hipSuccess;
+    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, a.num_work, rows, stream)
+                                              : launch_typed<float>(p, runs, a.num_work, rows, stream);
     if (e == hipSuccess && main_done) e = hipEventRecord(main_done, stream);
     if (e != hipSuccess || a.num_splits == 1) return e;
     const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>(a.n_heads));

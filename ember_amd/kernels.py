@@ -136,13 +136,27 @@ def decode_runs(ints: StepInts, token_list, max_run: int = MAX_RUN):
     return np.asarray(first, np.int32), np.asarray(count, np.int32)
 
 
+def work_list(run_ctx, split_len: int) -> np.ndarray:
+    """(run, split) items, every full split first, then the partial last splits longest first
+    (the order the C++ planner uses)."""
+    full, partial = [], []
+    for r, ctx in enumerate(int(c) for c in run_ctx):
+        full += [(r, s) for s in range(ctx // split_len)]
+        if ctx % split_len:
+            partial.append((ctx % split_len, r, ctx // split_len))
+    partial.sort(key=lambda x: -x[0])  # stable: equal sizes keep run order
+    items = full + [(r, s) for _, r, s in partial]
+    return np.asarray(items, np.int32).reshape(-1, 2)
+
+
 def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list=None, runs=None,
-                    split_len=512, num_splits=None, scratch=None, stream=None):
+                    split_len=512, num_splits=None, scratch=None, use_work_list=False, stream=None):
     """Paged decode attention (≙ cuda::paged_attention).
 
     token_list: tokens to process (None = all). runs: (run_first, run_count) over
     token_list positions, or None for one token per run. num_splits defaults to
-    what the longest context needs at split_len keys per split.
+    what the longest context needs at split_len keys per split. use_work_list:
+    dispatch through a sorted (run, split) list instead of the dense grid.
     """
     tl = np.arange(ints.T, dtype=np.int32) if token_list is None else np.asarray(token_list, np.int32)
     n = int(tl.size)
@@ -191,6 +205,16 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
         rf_dev, rc_dev = _ints(rf, dev), _ints(rc, dev)
         keep += [rf_dev, rc_dev]
         a.run_first, a.run_count, a.num_runs, a.max_run = rf_dev.data_ptr(), rc_dev.data_ptr(), int(rf.size), int(rc.max())
+        run_ctx = [int(ints.positions[tl[f:f + c]].max()) + 1 for f, c in zip(rf, rc)]
+    else:
+        run_ctx = [int(ints.positions[t]) + 1 for t in tl]
+    if use_work_list:
+        items = work_list(run_ctx, split_len)
+        if items.size and items[:, 1].max() >= num_splits:
+            raise EmberError("num_splits is too small for the work list")
+        w_dev = _ints(items.reshape(-1), dev)
+        keep.append(w_dev)
+        a.work, a.num_work = w_dev.data_ptr(), int(items.shape[0])
     check(_lib.lib().ember_hip_paged_decode(a, _stream_handle(stream)), "paged_decode")
     return keep  # the caller keeps the uploads alive until the stream has run
 

@@ -98,6 +98,14 @@ typedef struct EmberAttnArgs {
     const int32_t *run_first, *run_count;
     int32_t num_runs;
     int32_t max_run;              /* upper bound of run_count, 1..EMBER_MAX_RUN */
+    /* Optional work list: num_work (run, split) pairs, [2 * num_work] ints,
+     * each split of each run listed once (splits holding none of the run's
+     * keys may be left out). One work-group per (item, kv head), dispatched in
+     * list order, so a list with the longest items first balances the tail.
+     * NULL = every (run, split < num_splits) pair, splits beyond a run's
+     * context finishing at once. */
+    const int32_t *work;
+    int32_t num_work;
 } EmberAttnArgs;
 
 /* Paged attention for short runs (decode, speculative verify): one work-group

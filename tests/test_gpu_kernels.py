@@ -99,7 +99,7 @@ def test_append_matches_oracle(rng, device, dtype, bias, norm):
 
 def test_append_far_positions_and_clamp(rng, device):
     """Positions up to 40959 (Qwen3 max), and V beyond the f16 range is clamped to +-65504."""
-    NB = 2600
+    NB = 2700  # 2560 + 63 pages for the two contexts
     step = make_step(rng, [40960, 1000], [2, 1], NB, max_blocks=2560)
     qkv = rng.standard_normal((step.T, W)).astype(np.float32)
     qkv[:, (H + KVH) * D:(H + KVH) * D + 4] = [1e5, -1e5, 7e4, 65504.0]
@@ -141,15 +141,15 @@ def _run_decode(q, kp, vp, step, NB, device, **kw):
     return out
 
 
-@pytest.mark.parametrize("split_len", [16, 64, 512, 8192])
-def test_decode_f32_matches_oracle(rng, device, split_len):
+@pytest.mark.parametrize("split_len,work", [(16, False), (64, True), (512, False), (512, True), (8192, False)])
+def test_decode_f32_matches_oracle(rng, device, split_len, work):
     NB = 1200
     ctxs = [1, 15, 16, 17, 100, 511, 512, 513, 1500, 4096]
     step = make_step(rng, ctxs, [1] * len(ctxs), NB)
     k, v = _random_pools(rng, step, NB, f16=False)
     q = rng.standard_normal((step.T, H, D)).astype(np.float32)
     out = _run_decode(q, torch.from_numpy(k).to(device), torch.from_numpy(v).to(device), step, NB, device,
-                      split_len=split_len).cpu().numpy()
+                      split_len=split_len, use_work_list=work).cpu().numpy()
     want = oracle.attention_layer(q, step.positions, step.query_start, step.tables, np.nan_to_num(k), np.nan_to_num(v),
                                   n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=False, threads=8)
     assert np.isfinite(out).all()
@@ -214,6 +214,8 @@ def test_verify_run_equals_sequential_decode(rng, device, dtype):
     verify = _run_decode(q, kp, vp, step, NB, device, runs=runs).cpu().numpy()
     seq = _run_decode(q, kp, vp, step, NB, device).cpu().numpy()  # one run per token
     assert np.array_equal(verify.view(np.uint8), seq.view(np.uint8))
+    listed = _run_decode(q, kp, vp, step, NB, device, runs=runs, use_work_list=True).cpu().numpy()
+    assert np.array_equal(listed.view(np.uint8), seq.view(np.uint8))
     # runs of 2 and 3 too
     for m in (2, 3, 8):
         r = K.decode_runs(K.StepInts(step.positions, step.token_seq, step.tables, NB), range(step.T), max_run=m)

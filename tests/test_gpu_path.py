@@ -23,7 +23,7 @@ EPS, THETA = 1e-6, 1e6
 class World:
     """The GPU path and the oracle side by side, driven with identical steps."""
 
-    def __init__(self, device, dtype, num_blocks, n_layers=1, max_position=8192, max_batch_tokens=1024, seed=0):
+    def __init__(self, device, dtype, num_blocks, n_layers=1, max_position=8192, max_batch_tokens=2048, seed=0):
         self.dev, self.dtype, self.NB, self.L = device, dtype, num_blocks, n_layers
         self.kv = PagedKv(n_layers=n_layers, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,
                           max_position=max_position, num_blocks=num_blocks, max_batch_tokens=max_batch_tokens,
