@@ -48,7 +48,7 @@ def log(msg: str) -> None:
 class Workload:
     """Config 2 on the GPU path."""
 
-    def __init__(self, total_steps: int):
+    def __init__(self, total_steps: int, split_len: int = 512):
         import torch
 
         from ember_amd import BlockManager
@@ -71,7 +71,7 @@ class Workload:
         self.stream = torch.cuda.Stream()
         self.kv = PagedKv(n_layers=N_LAYERS, n_heads=H, n_kv_heads=KVH, rms_eps=1e-6, rope_theta=1e6,
                           max_position=self.max_blocks * PAGE, num_blocks=POOL_PAGES, max_batch_tokens=BATCH,
-                          max_seqs=BATCH, dtype=torch.float16, stream=self.stream)
+                          max_seqs=BATCH, dtype=torch.float16, split_len=split_len, stream=self.stream)
         g = torch.Generator(device="cuda").manual_seed(SEED)
         with torch.cuda.stream(self.stream):
             for layer in range(N_LAYERS):  # cached K/V: random f16 in every page (the values do not matter)
@@ -113,6 +113,30 @@ class Workload:
             self.kv.layer(layer, self.qkv[layer], self.out, q_norm=self.qn[layer], k_norm=self.kn[layer])
         self.ctx += 1
         return int(pos.sum() + BATCH)  # sum of contexts after this step's append
+
+
+def copy_calibration(steps: int) -> int:
+    """Known-size HBM traffic for scaling the rocprofv3 FETCH_SIZE / WRITE_SIZE counters: each launch of the
+    page-copy kernel reads and writes exactly 2,048 pages x 28 layers x (K + V) x 32 KiB = 3.76 GB."""
+    import torch
+
+    from ember_amd import kernels as K
+
+    n_pages, per_page = 4096, KVH * PAGE * D  # elements of one layer's K page (all kv heads)
+    pool_k = torch.zeros(N_LAYERS * n_pages * per_page, dtype=torch.float16, device="cuda")
+    pool_v = torch.zeros_like(pool_k)
+    rng = np.random.default_rng(SEED)
+    src = rng.permutation(n_pages)[: n_pages // 2]
+    dst = np.setdiff1d(np.arange(n_pages), src)
+    rng.shuffle(dst)
+    for _ in range(steps):
+        K.copy_pages(pool_k, pool_v, src, dst, n_layers=N_LAYERS, layer_stride=n_pages * per_page, n_kv=KVH,
+                     num_blocks=n_pages)
+    torch.cuda.synchronize()
+    per_launch = src.size * N_LAYERS * 2 * per_page * 2
+    print(json.dumps({"copy_pages_launches": steps, "bytes_read_per_launch": per_launch,
+                      "bytes_written_per_launch": per_launch}), flush=True)
+    return 0
 
 
 def cpu_baseline(seconds: float) -> dict:
@@ -180,11 +204,16 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 = skip)")
+    ap.add_argument("--split-len", type=int, default=512, help="keys per decode split (a multiple of 16)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only the known-size page copy used to scale the HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (this path has no multi-GPU "
               "part to measure; see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
 
     import torch
 
@@ -193,7 +222,7 @@ def main() -> int:
     lib()  # fails loudly when the HIP library is not built
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     log(f"[bench] setting up config 2 ({N_LAYERS} layers, batch {BATCH}, {POOL_PAGES}-page pool)")
-    w = Workload(args.steps + args.warmup)
+    w = Workload(args.steps + args.warmup, args.split_len)
     for _ in range(args.warmup):
         w.step()
     w.stream.synchronize()

@@ -85,12 +85,12 @@ int ember_hip_kv_append(const EmberQkvArgs *a, void *stream) {
 }
 
 int ember_hip_paged_decode(const EmberAttnArgs *a, void *stream) {
-    return paged_decode(a, static_cast<hipStream_t>(stream), nullptr);
+    return paged_decode(a, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
 }  // extern "C"
 
-int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t main_done) {
+int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     g_last_error.clear();
     if (!a) return set_error(EMBER_ERR_INVALID, "paged_decode: null arguments");
     if (int e = check_heads("paged_decode", a->head_dim, a->n_heads, a->n_kv)) return e;
@@ -129,7 +129,7 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
             break;
         }
     if (!rows) return set_error(EMBER_ERR_INVALID, "paged_decode: %d query rows per work-group exceed 16", need);
-    return hip_status(launch_paged_decode(*a, rows, stream, main_done), "paged_decode");
+    return hip_status(launch_paged_decode(*a, rows, stream, start, stop), "paged_decode");
 }
 
 extern "C" {

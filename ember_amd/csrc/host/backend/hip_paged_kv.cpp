@@ -281,19 +281,19 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         at.max_run = max_run_;
         at.work = d_work_;
         at.num_work = num_work_;
-        hipEvent_t stop = nullptr;
-        if (timing_) {
+        hipEvent_t start = nullptr, stop = nullptr;
+        if (timing_) {  // the kernel's own dispatch is timed (hipExtLaunchKernel), not the gap before it
             if (timing_used_ + 2 > timing_events_.size())
                 for (int i = 0; i < 2; i++) {
                     hipEvent_t e;
                     EMBER_HIP_CHECK(hipEventCreate(&e));
                     timing_events_.push_back(e);
                 }
-            EMBER_HIP_CHECK(hipEventRecord(timing_events_[timing_used_], stream_));
+            start = timing_events_[timing_used_];
             stop = timing_events_[timing_used_ + 1];
             timing_used_ += 2;
         }
-        check_abi(hip::paged_decode(&at, stream_, stop), "paged_decode");
+        check_abi(hip::paged_decode(&at, stream_, start, stop), "paged_decode");
     }
     if (tiles_ > 0) {
         EmberPrefillArgs pa{};

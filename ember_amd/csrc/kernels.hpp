@@ -13,13 +13,14 @@ hipError_t launch_kv_append(const EmberQkvArgs &a, hipStream_t stream);
 
 // Decode attention (+ the split merge when a.num_splits > 1). `rows` is the
 // kernel's query-row capacity, G * max_run rounded up to a built instance.
-// When `main_done` is given it is recorded right after the attention kernel,
-// before the merge.
-hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t main_done = nullptr);
+// Given events, the attention kernel's own dispatch is timed into them
+// (hipExtLaunchKernel: the start and end of that kernel, the merge excluded).
+hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start = nullptr,
+                               hipEvent_t stop = nullptr);
 
 // Validation + launch behind ember_hip_paged_decode, for in-library callers
-// that want the `main_done` event. Returns an EMBER_* / hipError_t code.
-int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t main_done);
+// that time the kernel. Returns an EMBER_* / hipError_t code.
+int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream);
 

@@ -37,6 +37,8 @@
 // single-token decode steps bit-exactly.
 #include <climits>
 
+#include <hip/hip_ext.h>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -268,45 +270,50 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
     const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
 
-    // One page: scores, online softmax per DPP row, value accumulation.
+    // One page: scores and online softmax for every row, then the values key by
+    // key (each key's 8 dims converted once, used by every row). Per row the
+    // operations and their order are: rescale by corr, then fma over keys 0..3.
     auto process = [&](const PageRegs<T> &pr, int page, bool ok) {
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
         const bool fast = ok && (page + 1) * kPage <= min_pos + 1;  // every key visible to every row
-        float vf[4][8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) unpack8(pr.v[i], vf[i]);
+        float pj[ROWS][4];
+        bool vis[ROWS][4];
 #pragma unroll
         for (int row = 0; row < ROWS; row++) {
             if (row >= nrows) continue;
             float s[4];
-            bool vis[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 s[i] = row16_sum(dot8(q[row], pr.k[i])) * p.scale_log2;
-                vis[i] = fast || (ok && key0 + 4 * i <= row_pos[row]);
-                if (!vis[i]) s[i] = -INFINITY;
+                vis[row][i] = fast || (ok && key0 + 4 * i <= row_pos[row]);
+                if (!vis[row][i]) s[i] = -INFINITY;
             }
             const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
             const float ref = mn == -INFINITY ? 0.0f : mn;
             const float corr = m[row] == mn ? 1.0f : exp2_hw(m[row] - ref);
-            float pj[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) pj[i] = exp2_hw(s[i] - ref);  // 2^-inf = 0 for hidden keys
-            l[row] = l[row] * corr + ((pj[0] + pj[1]) + (pj[2] + pj[3]));
+            for (int i = 0; i < 4; i++) pj[row][i] = exp2_hw(s[i] - ref);  // 2^-inf = 0 for hidden keys
+            l[row] = l[row] * corr + ((pj[row][0] + pj[row][1]) + (pj[row][2] + pj[row][3]));
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
-            if (fast) {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[i], vf[i][e], acc[row][e]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[row][e] = vis[i] ? fmaf(pj[i], vf[i][e], acc[row][e]) : acc[row][e];
-            }
             m[row] = mn;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float vf[8];
+            unpack8(pr.v[i], vf);
+#pragma unroll
+            for (int row = 0; row < ROWS; row++) {
+                if (row >= nrows) continue;
+                if (fast) {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[row][i], vf[e], acc[row][e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        acc[row][e] = vis[row][i] ? fmaf(pj[row][i], vf[e], acc[row][e]) : acc[row][e];
+                }
+            }
         }
     };
 
@@ -445,30 +452,36 @@ __global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) 
 }
 
 template <typename T, int ROWS>
-hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_t stream) {
+hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_t stream, hipEvent_t start,
+                       hipEvent_t stop) {
     const dim3 grid = p.work ? dim3(static_cast<unsigned>(num_work * p.n_kv))
                              : dim3(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv),
                                     static_cast<unsigned>(p.num_splits));
-    hipLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, p);
+    if (start || stop)
+        hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, start, stop, 0, p);
+    else
+        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
 template <typename T>
-hipError_t launch_typed(const DecodeParams &p, int runs, int num_work, int rows, hipStream_t stream) {
+hipError_t launch_typed(const DecodeParams &p, int runs, int num_work, int rows, hipStream_t stream, hipEvent_t start,
+                        hipEvent_t stop) {
     switch (rows) {
-        case 1: return launch_rows<T, 1>(p, runs, num_work, stream);
-        case 2: return launch_rows<T, 2>(p, runs, num_work, stream);
-        case 4: return launch_rows<T, 4>(p, runs, num_work, stream);
-        case 8: return launch_rows<T, 8>(p, runs, num_work, stream);
-        case 10: return launch_rows<T, 10>(p, runs, num_work, stream);
-        case 16: return launch_rows<T, 16>(p, runs, num_work, stream);
+        case 1: return launch_rows<T, 1>(p, runs, num_work, stream, start, stop);
+        case 2: return launch_rows<T, 2>(p, runs, num_work, stream, start, stop);
+        case 4: return launch_rows<T, 4>(p, runs, num_work, stream, start, stop);
+        case 8: return launch_rows<T, 8>(p, runs, num_work, stream, start, stop);
+        case 10: return launch_rows<T, 10>(p, runs, num_work, stream, start, stop);
+        case 16: return launch_rows<T, 16>(p, runs, num_work, stream, start, stop);
         default: return hipErrorInvalidValue;
     }
 }
 
 }  // namespace
 
-hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t main_done) {
+hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start,
+                               hipEvent_t stop) {
     if (a.T <= 0) return hipSuccess;
     DecodeParams p{};
     p.q = a.q;
@@ -495,9 +508,8 @@ hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t str
     const int runs = a.run_first ? a.num_runs : a.T;
     p.num_runs = runs;
     if (runs <= 0 || (a.work && a.num_work <= 0)) return hipSuccess;
-    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, a.num_work, rows, stream)
-                                              : launch_typed<float>(p, runs, a.num_work, rows, stream);
-    if (e == hipSuccess && main_done) e = hipEventRecord(main_done, stream);
+    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, a.num_work, rows, stream, start, stop)
+                                              : launch_typed<float>(p, runs, a.num_work, rows, stream, start, stop);
     if (e != hipSuccess || a.num_splits == 1) return e;
     const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>(a.n_heads));
     if (a.dtype == EMBER_DTYPE_F16)
