@@ -244,8 +244,11 @@ def main() -> int:
     tokens_s = BATCH * args.steps / wall
     step_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + TOKEN_BYTES * BATCH)
     step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-    # Decode kernel roofline: algorithmic bytes per launch = K+V of every context token + the queries.
-    kernel_bytes = KV_BYTES_PER_TOKEN * sum_ctx + 4096 * BATCH * args.steps  # over all timed launches / 28
+    # Decode kernel roofline: algorithmic bytes per launch = K+V of every context token, plus per new token
+    # either the query (4 KiB, unfused) or, fused, qkv in (8 KiB) + its K/V written (4 KiB) + the output (4 KiB).
+    fused = w.kv.fused()
+    per_token = 16384 if fused else 4096
+    kernel_bytes = KV_BYTES_PER_TOKEN * sum_ctx + per_token * BATCH * args.steps  # over all timed launches / 28
     kernel_bytes *= N_LAYERS
     kernel_gbs = kernel_bytes / (kernel_ms * 1e-3) / 1e9 if kernel_ms > 0 else 0.0
     log(f"[bench] {args.steps} steps in {wall:.3f} s: {ms_per_step:.3f} ms/step, {tokens_s:.0f} tokens/s, "
@@ -284,7 +287,7 @@ def main() -> int:
             "host_blockmanager_us_per_step": round(w.alloc_s / args.steps * 1e6, 2),
         },
         "roofline": {
-            "kernel": "paged_decode_kernel",
+            "kernel": "paged_decode_kernel<f16, rows 2, fused append + merge>" if fused else "paged_decode_kernel",
             "bound": "hbm",
             "achieved": round(kernel_gbs, 1),
             "peak": HBM_PEAK_GBS,

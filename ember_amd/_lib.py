@@ -45,7 +45,7 @@ class AttnArgs(ctypes.Structure):
         ("scale", c_float), ("out", c_void_p), ("num_splits", c_int32), ("split_len", c_int32),
         ("part_acc", c_void_p), ("part_ml", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
         ("run_first", c_void_p), ("run_count", c_void_p), ("num_runs", c_int32), ("max_run", c_int32),
-        ("work", c_void_p), ("num_work", c_int32),
+        ("work", c_void_p), ("num_work", c_int32), ("merge_counters", c_void_p),
     ]
 
 
@@ -89,6 +89,7 @@ STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC]
 PROTOTYPES = {
     "ember_hip_kv_append": (c_int32, [POINTER(QkvArgs), c_void_p]),
     "ember_hip_paged_decode": (c_int32, [POINTER(AttnArgs), c_void_p]),
+    "ember_hip_decode_step": (c_int32, [POINTER(QkvArgs), POINTER(AttnArgs), c_void_p]),
     "ember_hip_prefill_attn": (c_int32, [POINTER(PrefillArgs), c_void_p]),
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
     "ember_hip_last_error": (c_char_p, []),
@@ -123,7 +124,7 @@ PROTOTYPES = {
     "ember_kv_v_pool": (c_void_p, [c_void_p, c_int32]),
     "ember_kv_layer_stride": (c_int64, [c_void_p]),
     "ember_kv_spare_block": (c_int32, [c_void_p]),
-    "ember_kv_plan_info": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
+    "ember_kv_plan_info": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "ember_kv_set_timing": (c_int32, [c_void_p, c_int32]),
     "ember_kv_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
 }

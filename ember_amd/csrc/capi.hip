@@ -88,11 +88,29 @@ int ember_hip_paged_decode(const EmberAttnArgs *a, void *stream) {
     return paged_decode(a, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
+int ember_hip_decode_step(const EmberQkvArgs *qkv, const EmberAttnArgs *attn, void *stream) {
+    if (!qkv) return set_error(EMBER_ERR_INVALID, "decode_step: null qkv arguments");
+    return paged_decode(attn, static_cast<hipStream_t>(stream), nullptr, nullptr, qkv);
+}
+
 }  // extern "C"
 
-int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                             const EmberQkvArgs *qkv) {
     g_last_error.clear();
     if (!a) return set_error(EMBER_ERR_INVALID, "paged_decode: null arguments");
+    if (qkv) {  // the fused form: both argument sets describe the same step
+        if (qkv->n_heads != a->n_heads || qkv->n_kv != a->n_kv || qkv->head_dim != a->head_dim ||
+            qkv->dtype != a->dtype || qkv->max_blocks != a->max_blocks || qkv->num_blocks != a->num_blocks ||
+            qkv->positions != a->positions || qkv->token_seq != a->token_seq || qkv->block_tables != a->block_tables)
+            return set_error(EMBER_ERR_INVALID, "decode_step: the qkv and attention arguments describe different steps");
+        if (!qkv->qkv || !qkv->inv_freq || (qkv->q_norm == nullptr) != (qkv->k_norm == nullptr))
+            return set_error(EMBER_ERR_INVALID, "decode_step: qkv, inv_freq (and q_norm with k_norm) are required");
+        if (a->run_first && a->max_run > EMBER_MAX_RUN)
+            return set_error(EMBER_ERR_INVALID, "decode_step: a run holds at most %d tokens", EMBER_MAX_RUN);
+        if (qkv->T != a->T)
+            return set_error(EMBER_ERR_INVALID, "decode_step: every token of qkv (%d) must be listed (%d)", qkv->T, a->T);
+    }
     if (int e = check_heads("paged_decode", a->head_dim, a->n_heads, a->n_kv)) return e;
     const int G = a->n_heads / a->n_kv;
     if (G > 8) return set_error(EMBER_ERR_INVALID, "paged_decode: query heads per kv head must be 1..8 (got %d)", G);
@@ -103,7 +121,7 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
         return set_error(EMBER_ERR_INVALID, "paged_decode: split_len must be a positive multiple of 16 (got %d x %d)",
                          a->num_splits, a->split_len);
     if (a->T == 0) return EMBER_OK;
-    if (!a->q || !a->k_cache || !a->v_cache || !a->positions || !a->token_seq || !a->block_tables || !a->out)
+    if ((!a->q && !qkv) || !a->k_cache || !a->v_cache || !a->positions || !a->token_seq || !a->block_tables || !a->out)
         return set_error(EMBER_ERR_INVALID, "paged_decode: a required pointer is null");
     if (a->num_splits > 1 && (!a->part_acc || !a->part_ml))
         return set_error(EMBER_ERR_INVALID, "paged_decode: split scratch is required when num_splits > 1");
@@ -129,6 +147,7 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
             break;
         }
     if (!rows) return set_error(EMBER_ERR_INVALID, "paged_decode: %d query rows per work-group exceed 16", need);
+    if (qkv) return hip_status(launch_decode_step(*qkv, *a, rows, stream, start, stop), "decode_step");
     return hip_status(launch_paged_decode(*a, rows, stream, start, stop), "paged_decode");
 }
 

@@ -53,6 +53,40 @@ __device__ __forceinline__ double wave_sum_f64(double x) {
 
 __device__ __forceinline__ float clamp_half(float x) { return fminf(fmaxf(x, -kHalfMax), kHalfMax); }
 
+// QK-RMSNorm (optional) and rotate-half RoPE of one 128-dim head vector held
+// by a wave64: lane l holds x0 = x[l] and x1 = x[l + 64], exactly one rotary
+// pair. Follows the reference's f32 CPU backend (src/backend/cpu/cpu_backend.cpp
+// :34-39 rmsnorm with a double sum of squares, :262-272 rope): the sum of
+// squares is taken in double (f32 products are exact there), sine and cosine
+// in double rounded once to f32, and the rest in f32 as the CPU writes it.
+// Every lane of the wave must call it (the sum is a wave reduction).
+__device__ __forceinline__ void qk_norm_rope(float &x0, float &x1, const float *w, float eps, int pos,
+                                             const float *inv_freq, int lane) {
+    constexpr int HALF = kHeadDim / 2;
+    if (w) {
+        double ss = static_cast<double>(x0) * x0 + static_cast<double>(x1) * x1;
+        ss = wave_sum_f64(ss);
+        const float scale = static_cast<float>(1.0 / sqrt(ss / kHeadDim + static_cast<double>(eps)));
+        x0 = w[lane] * (x0 * scale);
+        x1 = w[lane + HALF] * (x1 * scale);
+    }
+    const float angle = static_cast<float>(pos) * inv_freq[lane];
+    double sd, cd;
+    sincos(static_cast<double>(angle), &sd, &cd);
+    const float s = static_cast<float>(sd), c = static_cast<float>(cd);
+    const float lo = x0, hi = x1;
+    x0 = lo * c - hi * s;
+    x1 = hi * c + lo * s;
+}
+
+// The value a K/V element is stored as: f16 pages clamp to the finite range
+// first (as the reference's store does, k_elementwise.cu:125); f32 pages keep it.
+template <typename T>
+__device__ __forceinline__ T to_page(float x) {
+    if constexpr (sizeof(T) == 2) return static_cast<T>(clamp_half(x));
+    else return x;
+}
+
 // f16 <-> f32 element conversion for the templated (f16 / f32) kernels.
 template <typename T>
 __device__ __forceinline__ float to_f32(T x) {

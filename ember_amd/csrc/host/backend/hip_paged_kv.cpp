@@ -63,6 +63,9 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     const size_t part_rows = T * cfg_.n_heads * static_cast<size_t>(max_splits_);
     part_acc_ = device_alloc<float>(part_rows * cfg_.head_dim);
     part_ml_ = device_alloc<float>(part_rows * 2);
+    const size_t counters = T * static_cast<size_t>(cfg_.n_kv_heads);  // one per (run, kv head); runs <= tokens
+    merge_counters_ = device_alloc<uint32_t>(counters);
+    EMBER_HIP_CHECK(hipMemsetAsync(merge_counters_, 0, counters * sizeof(uint32_t), stream_));
 
     std::vector<float> inv(static_cast<size_t>(cfg_.head_dim / 2));
     for (int i = 0; i < cfg_.head_dim / 2; i++)  // f32, as the reference computes it (cpu_backend.cpp:85-88)
@@ -90,7 +93,7 @@ HipPagedKv::~HipPagedKv() {
         if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
     }
     for (void *p : {k_, v_, q_, static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
-                    static_cast<void *>(part_ml_), static_cast<void *>(dev_ints_)})
+                    static_cast<void *>(part_ml_), static_cast<void *>(merge_counters_), static_cast<void *>(dev_ints_)})
         if (p) (void)hipFree(p);
 }
 
@@ -125,6 +128,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     tile_seq_.clear();
     int max_ctx = 0;
     max_run_ = 1;
+    fused_ = true;
     for (int s = 0; s < S; s++) {
         const int q0 = b.query_start[static_cast<size_t>(s)], q1 = b.query_start[static_cast<size_t>(s) + 1];
         EMBER_CHECK(q0 <= q1, "malformed query_start");
@@ -135,7 +139,9 @@ void HipPagedKv::plan(const StepBatch &b) {
             EMBER_CHECK(pos >= 0 && pos < b.max_blocks * kBlockSize, "token {} at position {} is beyond its block table", t,
                         pos);
             ctx = std::max(ctx, pos + 1);
+            if (t > q0 && pos != b.positions[static_cast<size_t>(t) - 1] + 1) fused_ = false;
         }
+        if (q1 - q0 > EMBER_MAX_RUN) fused_ = false;  // one run per sequence, or runs would read each other's new slots
         // Every page a token of this sequence reads must be a real block (or the spare).
         const int32_t *row = &b.block_tables[static_cast<size_t>(s) * b.max_blocks];
         for (int p = 0; p * kBlockSize < ctx; p++)
@@ -166,6 +172,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     decode_count_ = static_cast<int>(decode_.size());
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
+    fused_ = fused_ && tiles_ == 0 && decode_count_ == T;
     splits_ = std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
 
     // Decode work items (run, split), dispatched in list order: every full
@@ -250,7 +257,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
     qa.eps = cfg_.rms_eps;
     qa.num_blocks = opt_.num_blocks + 1;
     qa.dtype = opt_.dtype;
-    check_abi(ember_hip_kv_append(&qa, stream_), "kv_append");
+    if (!fused_) check_abi(ember_hip_kv_append(&qa, stream_), "kv_append");
 
     const float scale = 1.0f / std::sqrt(static_cast<float>(cfg_.head_dim));
     if (decode_runs_ > 0) {
@@ -281,6 +288,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         at.max_run = max_run_;
         at.work = d_work_;
         at.num_work = num_work_;
+        at.merge_counters = merge_counters_;
         hipEvent_t start = nullptr, stop = nullptr;
         if (timing_) {  // the kernel's own dispatch is timed (hipExtLaunchKernel), not the gap before it
             if (timing_used_ + 2 > timing_events_.size())
@@ -293,7 +301,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
             stop = timing_events_[timing_used_ + 1];
             timing_used_ += 2;
         }
-        check_abi(hip::paged_decode(&at, stream_, start, stop), "paged_decode");
+        check_abi(hip::paged_decode(&at, stream_, start, stop, fused_ ? &qa : nullptr), "paged_decode");
     }
     if (tiles_ > 0) {
         EmberPrefillArgs pa{};

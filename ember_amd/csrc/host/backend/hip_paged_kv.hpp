@@ -57,6 +57,7 @@ public:
     int64_t layer_stride() const { return layer_elems_; }
     int spare_block() const { return opt_.num_blocks; }
     int decode_runs() const { return decode_runs_; }
+    bool fused() const { return fused_; }
     int prefill_tiles() const { return tiles_; }
     int num_splits() const { return splits_; }
     hipStream_t stream() const { return stream_; }
@@ -79,6 +80,7 @@ private:
 
     void *k_ = nullptr, *v_ = nullptr, *q_ = nullptr;
     float *inv_freq_ = nullptr, *part_acc_ = nullptr, *part_ml_ = nullptr;
+    uint32_t *merge_counters_ = nullptr;  // [max_batch_tokens * n_kv], zero between launches
     int32_t *dev_ints_ = nullptr;   // this step's integers
     int32_t *host_ints_[2] = {nullptr, nullptr};  // pinned staging, alternating
     hipEvent_t staged_[2] = {nullptr, nullptr};   // the upload from each staging buffer has run
@@ -87,6 +89,7 @@ private:
 
     // The current plan (device addresses into dev_ints_).
     int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;
+    bool fused_ = false;  // every sequence's new tokens form one run: append + attention in one launch
     const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
                   *d_run_first_ = nullptr, *d_run_count_ = nullptr, *d_tile_start_ = nullptr, *d_tile_end_ = nullptr,
                   *d_tile_seq_ = nullptr, *d_work_ = nullptr;

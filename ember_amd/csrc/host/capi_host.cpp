@@ -222,10 +222,12 @@ void *ember_kv_v_pool(EmberPagedKv *h, int32_t layer) {
 int64_t ember_kv_layer_stride(const EmberPagedKv *h) { return h->kv.layer_stride(); }
 int32_t ember_kv_spare_block(const EmberPagedKv *h) { return h->kv.spare_block(); }
 
-int32_t ember_kv_plan_info(const EmberPagedKv *h, int32_t *decode_runs, int32_t *prefill_tiles, int32_t *num_splits) {
+int32_t ember_kv_plan_info(const EmberPagedKv *h, int32_t *decode_runs, int32_t *prefill_tiles, int32_t *num_splits,
+                           int32_t *fused) {
     if (decode_runs) *decode_runs = h->kv.decode_runs();
     if (prefill_tiles) *prefill_tiles = h->kv.prefill_tiles();
     if (num_splits) *num_splits = h->kv.num_splits();
+    if (fused) *fused = h->kv.fused() ? 1 : 0;
     return EMBER_OK;
 }
 

@@ -18,9 +18,15 @@ hipError_t launch_kv_append(const EmberQkvArgs &a, hipStream_t stream);
 hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start = nullptr,
                                hipEvent_t stop = nullptr);
 
-// Validation + launch behind ember_hip_paged_decode, for in-library callers
-// that time the kernel. Returns an EMBER_* / hipError_t code.
-int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+// The fused append + decode launch (ember_hip_decode_step).
+hipError_t launch_decode_step(const EmberQkvArgs &qa, const EmberAttnArgs &a, int rows, hipStream_t stream,
+                              hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+
+// Validation + launch behind ember_hip_paged_decode / ember_hip_decode_step
+// (qkv == nullptr: the unfused kernel), for in-library callers that time the
+// kernel. Returns an EMBER_* / hipError_t code.
+int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
+                 const EmberQkvArgs *qkv = nullptr);
 
 hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream);
 

@@ -38,23 +38,7 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) kv_append_kernel(Ember
 
     const int pos = a.positions[t];
     const bool is_q = head < a.n_heads, is_k = !is_q && head < a.n_heads + a.n_kv;
-    if (is_q || is_k) {
-        const float *w = is_q ? a.q_norm : a.k_norm;
-        if (w) {
-            double ss = static_cast<double>(x0) * x0 + static_cast<double>(x1) * x1;
-            ss = wave_sum_f64(ss);
-            const float scale = static_cast<float>(1.0 / sqrt(ss / D + static_cast<double>(a.eps)));
-            x0 = w[lane] * (x0 * scale);
-            x1 = w[lane + HALF] * (x1 * scale);
-        }
-        const float angle = static_cast<float>(pos) * a.inv_freq[lane];
-        double sd, cd;
-        sincos(static_cast<double>(angle), &sd, &cd);
-        const float s = static_cast<float>(sd), c = static_cast<float>(cd);
-        const float lo = x0, hi = x1;
-        x0 = lo * c - hi * s;
-        x1 = hi * c + lo * s;
-    }
+    if (is_q || is_k) qk_norm_rope(x0, x1, is_q ? a.q_norm : a.k_norm, a.eps, pos, a.inv_freq, lane);
 
     if (is_q) {
         T *dst = static_cast<T *>(a.q_out) + (static_cast<int64_t>(t) * a.n_heads + head) * D;
@@ -69,14 +53,8 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) kv_append_kernel(Ember
     if (block < 0 || block >= a.num_blocks) return;  // never write outside the pool
     T *pool = static_cast<T *>(is_k ? a.k_cache : a.v_cache);
     T *dst = pool + ((static_cast<int64_t>(block) * a.n_kv + kvh) * kPage + pos % kPage) * D;
-    if constexpr (sizeof(T) == 2) {
-        // f16 pages: clamp to the finite range first, as the reference's store does (k_elementwise.cu:125).
-        dst[lane] = from_f32<T>(clamp_half(x0));
-        dst[lane + HALF] = from_f32<T>(clamp_half(x1));
-    } else {
-        dst[lane] = x0;
-        dst[lane + HALF] = x1;
-    }
+    dst[lane] = to_page<T>(x0);
+    dst[lane + HALF] = to_page<T>(x1);
 }
 
 }  // namespace

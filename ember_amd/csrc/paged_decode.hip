@@ -1,11 +1,12 @@
 // Paged decode attention on gfx950 VALU (no MFMA): a bandwidth-bound gather.
 //
 // Replaces the reference's paged_attention_kernel + combine_splits_kernel
-// (src/backend/cuda/k_attention.cu:29-201). Semantics kept: GQA with the G
-// query heads of a kv head in one work-group (each page is read once for
-// all of them), softmax in base 2 with the scale folded in, fixed context
-// splits merged in a fixed order (batch invariance), slots past a query's
-// position never contribute.
+// (src/backend/cuda/k_attention.cu:29-201), and in its fused form also its
+// qk_norm_rope_store_kernel (k_elementwise.cu:67-126) for decode steps.
+// Semantics kept: GQA with the G query heads of a kv head in one work-group
+// (each page is read once for all of them), softmax in base 2 with the scale
+// folded in, fixed context splits merged in a fixed order (batch invariance),
+// slots past a query's position never contribute.
 //
 // Work-group = 4 waves per (query run, kv head, context split). A run is 1..8
 // consecutive tokens of one sequence (decode: 1; speculative verify: k + 1);
@@ -25,8 +26,15 @@
 // Latency: block ids are wave-uniform scalar loads (they never wait on the
 // page loads), and each wave keeps the next two pages in flight in registers
 // while it works on the current one.
-// At the end: rows merge through two lane exchanges, waves through LDS,
-// splits in the separate merge kernel, all in a fixed order.
+// At the end: rows merge through two lane exchanges, waves through LDS, and
+// splits either in the separate merge kernel or, with merge counters, in the
+// last work-group of the (run, kv head) to finish - all in one fixed order.
+//
+// Fused form (decode steps): the work-group computes its rows' q from qkv
+// (QK-RMSNorm + RoPE, the append kernel's arithmetic), and the K/V of the
+// run's new tokens that fall in its split; it stores them to the pool and uses
+// them in place of those slots of the pages it reads. Only this work-group
+// reads those slots in this launch, so nothing waits for another work-group.
 //
 // Exactness of runs: a query row's arithmetic is the same whether its token is
 // alone or in a run. Pages entirely below the run's lowest position take a
@@ -53,8 +61,13 @@ struct DecodeParams {
     const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count, *work;
     void *out;
     float *part_acc, *part_ml;
+    uint32_t *counters;
     int max_blocks, n_heads, n_kv, G, num_blocks, num_splits, split_len, num_runs;
     float scale_log2;
+    // fused form
+    const void *qkv;
+    const float *q_norm, *k_norm, *bias, *inv_freq;
+    float eps;
 };
 
 // A load through the constant address space: with a wave-uniform address the
@@ -99,6 +112,20 @@ __device__ __forceinline__ void load_page(PageRegs<T> &pr, const T *kbase, const
     }
 }
 
+// Replaces key i of a page with the 8 dims this lane holds, read from LDS.
+template <typename T>
+__device__ __forceinline__ void put_key(PageRegs<T> &pr, int i, const T *k8, const T *v8) {
+    if constexpr (sizeof(T) == 2) {
+        pr.k[i] = *reinterpret_cast<const uint4 *>(k8);
+        pr.v[i] = *reinterpret_cast<const uint4 *>(v8);
+    } else {
+        pr.k[i][0] = *reinterpret_cast<const float4 *>(k8);
+        pr.k[i][1] = *reinterpret_cast<const float4 *>(k8 + 4);
+        pr.v[i][0] = *reinterpret_cast<const float4 *>(v8);
+        pr.v[i][1] = *reinterpret_cast<const float4 *>(v8 + 4);
+    }
+}
+
 // The query slice a lane needs: dims [8c, 8c + 8) of one row.
 template <typename T>
 struct QSlice;
@@ -112,6 +139,28 @@ struct QSlice<float> {
 };
 
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+
+template <typename T>
+__device__ __forceinline__ void load_q(QSlice<T> &q, const T *qp) {
+    if constexpr (sizeof(T) == 2) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
+        q.h[0] = as_f16x2(raw.x);
+        q.h[1] = as_f16x2(raw.y);
+        q.h[2] = as_f16x2(raw.z);
+        q.h[3] = as_f16x2(raw.w);
+    } else {
+        const float4 a = *reinterpret_cast<const float4 *>(qp);
+        const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
+        q.f[0] = a.x;
+        q.f[1] = a.y;
+        q.f[2] = a.z;
+        q.f[3] = a.w;
+        q.f[4] = b.x;
+        q.f[5] = b.y;
+        q.f[6] = b.z;
+        q.f[7] = b.w;
+    }
+}
 
 __device__ __forceinline__ float dot8(const QSlice<f16> &q, const uint4 &k) {
     float s = 0.0f;
@@ -179,12 +228,41 @@ __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8],
     m = M;
 }
 
-template <typename T, int ROWS>
+// The split merge of one output element (token list entry li, head, dim d):
+// out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the splits that
+// hold the token's keys, in split order; splits without a visible key skipped.
+// Used by the merge kernel and by the in-kernel merge alike.
+template <typename T>
+__device__ __forceinline__ void merge_one(const DecodeParams &p, int li, int head, int d) {
+    constexpr int D = kHeadDim;
+    const int t = p.token_index ? p.token_index[li] : li;
+    const int ctx = min(p.positions[t] + 1, p.max_blocks * kPage);
+    const int ns = min(p.num_splits, max(1, (ctx + p.split_len - 1) / p.split_len));
+    const int64_t base = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+    float L = 0.0f, O = 0.0f;
+    bool any = false;
+    for (int s = 0; s < ns; s++) {
+        const float ms = p.part_ml[(base + s) * 2];
+        if (ms == -INFINITY) continue;
+        const float f = ms == M ? 1.0f : exp2_hw(ms - M);  // one split: exactly O / L, as a direct write
+        const float ls = p.part_ml[(base + s) * 2 + 1] * f, os = p.part_acc[(base + s) * D + d] * f;
+        L = any ? L + ls : ls;
+        O = any ? O + os : os;
+        any = true;
+    }
+    T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
+    o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
+}
+
+template <typename T, int ROWS, bool FUSED>
 __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
     constexpr int D = kHeadDim;
     // Two pages in flight per wave while it works on a third, unless the
     // query rows already need the registers.
     constexpr int STAGES = ROWS <= 4 ? 3 : 2;
+    constexpr int NEW = FUSED ? EMBER_MAX_RUN : 1;
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int wave = uniform(static_cast<int>(threadIdx.x) / kWave);
     const int r = lane >> 4, c = lane & 15;
@@ -205,6 +283,9 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 
     __shared__ float red_acc[ROWS][kWaves][D];
     __shared__ float red_m[ROWS][kWaves], red_l[ROWS][kWaves];
+    __shared__ __align__(16) T q_lds[FUSED ? ROWS : 1][D];
+    __shared__ __align__(16) T new_k[NEW][D], new_v[NEW][D];
+    __shared__ int merge_here;
 
     // The run: list entries first .. first + nq - 1, one sequence.
     const int first = p.run_first ? uniform_load(p.run_first + run) : run;
@@ -229,7 +310,68 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     }
     const int ctx_max = min(max_pos + 1, p.max_blocks * kPage);
     const int begin = split * p.split_len;
+    if (begin >= ctx_max) return;  // a split past the run's context: nothing reads its partial
     const int end = min(ctx_max, begin + p.split_len);
+    const int run_splits = (ctx_max + p.split_len - 1) / p.split_len;
+
+    const T *kbase = static_cast<const T *>(p.k);
+    const T *vbase = static_cast<const T *>(p.v);
+    const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
+    const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
+
+    if constexpr (FUSED) {
+        // q of every row and the new K/V in this split, one head vector per
+        // wave at a time; lane l holds dims l and l + 64 (a rotary pair).
+        const int n_total = p.n_heads + 2 * p.n_kv;
+        const T *qkv = static_cast<const T *>(p.qkv);
+        for (int row = wave; row < nrows; row += kWaves) {
+            const int li = first + row / G;
+            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+            const int head = kvh * G + row % G;
+            const T *src = qkv + (static_cast<int64_t>(t) * n_total + head) * D;
+            float x0 = to_f32(src[lane]), x1 = to_f32(src[lane + D / 2]);
+            if (p.bias) {
+                x0 = x0 + p.bias[head * D + lane];
+                x1 = x1 + p.bias[head * D + lane + D / 2];
+            }
+            qk_norm_rope(x0, x1, p.q_norm, p.eps, uniform_load(p.positions + t), p.inv_freq, lane);
+            q_lds[row][lane] = from_f32<T>(x0);
+            q_lds[row][lane + D / 2] = from_f32<T>(x1);
+        }
+        for (int i = wave; i < nq; i += kWaves) {
+            const int t = p.token_index ? uniform_load(p.token_index + first + i) : first + i;
+            const int pos = uniform_load(p.positions + t);
+            if (pos < begin || pos >= end) continue;  // another split's work-group appends it
+            const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
+            const T *ks = qkv + (static_cast<int64_t>(t) * n_total + kh) * D;
+            const T *vs = qkv + (static_cast<int64_t>(t) * n_total + vh) * D;
+            float k0 = to_f32(ks[lane]), k1 = to_f32(ks[lane + D / 2]);
+            float v0 = to_f32(vs[lane]), v1 = to_f32(vs[lane + D / 2]);
+            if (p.bias) {
+                k0 = k0 + p.bias[kh * D + lane];
+                k1 = k1 + p.bias[kh * D + lane + D / 2];
+                v0 = v0 + p.bias[vh * D + lane];
+                v1 = v1 + p.bias[vh * D + lane + D / 2];
+            }
+            qk_norm_rope(k0, k1, p.k_norm, p.eps, pos, p.inv_freq, lane);
+            const T ek0 = to_page<T>(k0), ek1 = to_page<T>(k1), ev0 = to_page<T>(v0), ev1 = to_page<T>(v1);
+            new_k[i][lane] = ek0;
+            new_k[i][lane + D / 2] = ek1;
+            new_v[i][lane] = ev0;
+            new_v[i][lane + D / 2] = ev1;
+            const int blk = uniform_load(table + pos / kPage);
+            if (blk >= 0 && blk < p.num_blocks) {
+                const int64_t off = static_cast<int64_t>(blk) * block_stride + head_off + (pos % kPage) * D;
+                T *kd = const_cast<T *>(kbase) + off;
+                T *vd = const_cast<T *>(vbase) + off;
+                kd[lane] = ek0;
+                kd[lane + D / 2] = ek1;
+                vd[lane] = ev0;
+                vd[lane + D / 2] = ev1;
+            }
+        }
+        __syncthreads();
+    }
 
     QSlice<T> q[ROWS];
     float m[ROWS], l[ROWS], acc[ROWS][8];
@@ -240,35 +382,16 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
         if (row < nrows) {
-            const int li = first + row / G;
-            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-            const int head = kvh * G + row % G;
-            const T *qp = static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c;
-            if constexpr (sizeof(T) == 2) {
-                const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
-                q[row].h[0] = as_f16x2(raw.x);
-                q[row].h[1] = as_f16x2(raw.y);
-                q[row].h[2] = as_f16x2(raw.z);
-                q[row].h[3] = as_f16x2(raw.w);
+            if constexpr (FUSED) {
+                load_q(q[row], &q_lds[row][8 * c]);
             } else {
-                const float4 a = *reinterpret_cast<const float4 *>(qp);
-                const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
-                q[row].f[0] = a.x;
-                q[row].f[1] = a.y;
-                q[row].f[2] = a.z;
-                q[row].f[3] = a.w;
-                q[row].f[4] = b.x;
-                q[row].f[5] = b.y;
-                q[row].f[6] = b.z;
-                q[row].f[7] = b.w;
+                const int li = first + row / G;
+                const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+                const int head = kvh * G + row % G;
+                load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
             }
         }
     }
-
-    const T *kbase = static_cast<const T *>(p.k);
-    const T *vbase = static_cast<const T *>(p.v);
-    const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
-    const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
 
     // One page: scores and online softmax for every row, then the values key by
     // key (each key's 8 dims converted once, used by every row). Per row the
@@ -316,8 +439,22 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             }
         }
     };
+    // The fused form first puts this launch's new keys into the page they land
+    // in (in place: the registers are reloaded after use anyway).
+    auto consume = [&](PageRegs<T> &pr, int page, bool ok) {
+        if constexpr (FUSED) {
+            if (page * kPage <= max_pos && (page + 1) * kPage > min_pos) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int j = page * kPage + r + 4 * i - min_pos;  // the run's positions are consecutive
+                    if (j >= 0 && j < nq) put_key(pr, i, &new_k[j][8 * c], &new_v[j][8 * c]);
+                }
+            }
+        }
+        process(pr, page, ok);
+    };
 
-    if (begin < end) {
+    {
         const int first_page = begin / kPage, last_page = (end - 1) / kPage;
         const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
         // Block id of this wave's j-th page (a scalar load) and whether it lies in the pool.
@@ -343,13 +480,13 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
                 int bb = fetch(B, 1);
                 for (int j = 0;; j += 3) {
                     const int bc = fetch(C, j + 2);
-                    process(A, page_of(j), in_pool(ba));
+                    consume(A, page_of(j), in_pool(ba));
                     if (j + 1 >= n) break;
                     ba = fetch(A, j + 3);
-                    process(B, page_of(j + 1), in_pool(bb));
+                    consume(B, page_of(j + 1), in_pool(bb));
                     if (j + 2 >= n) break;
                     bb = fetch(B, j + 4);
-                    process(C, page_of(j + 2), in_pool(bc));
+                    consume(C, page_of(j + 2), in_pool(bc));
                     if (j + 3 >= n) break;
                 }
             }
@@ -365,13 +502,13 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
                     bb = block_of(j + 1);
                     load_page(B, kbase, vbase, offset_of(bb), lane);
                 }
-                process(A, page_of(j), in_pool(ba));
+                consume(A, page_of(j), in_pool(ba));
                 if (j + 1 >= n) break;
                 if (j + 2 < n) {
                     ba = block_of(j + 2);
                     load_page(A, kbase, vbase, offset_of(ba), lane);
                 }
-                process(B, page_of(j + 1), in_pool(bb));
+                consume(B, page_of(j + 1), in_pool(bb));
             }
         }
     }
@@ -393,7 +530,9 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     }
     __syncthreads();
 
-    // Merge the waves in order 0..3, then write the output or this split's partial.
+    // Merge the waves in order 0..3, then write the output (a run with one
+    // split) or this split's partial.
+    const bool direct = p.counters ? run_splits == 1 : p.num_splits == 1;
     for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
         const int row = idx / D, d = idx % D;
         float M = -INFINITY;
@@ -409,7 +548,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         }
         const int li = first + row / G;
         const int head = kvh * G + row % G;
-        if (p.num_splits == 1) {
+        if (direct) {
             const int t = p.token_index ? p.token_index[li] : li;
             T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
             o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
@@ -422,67 +561,63 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             }
         }
     }
+    if (direct || !p.counters) return;
+
+    // In-kernel split merge: every work-group of this (run, kv head) counts in
+    // after its partial is visible device-wide (agent-scope release: the write
+    // back of this XCD's L2); the last one merges, after an acquire, and resets
+    // the counter for the next launch. Nothing waits.
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t *counter = p.counters + static_cast<int64_t>(run) * p.n_kv + kvh;
+        const uint32_t before = atomicAdd(counter, 1u);
+        merge_here = before + 1 == static_cast<uint32_t>(run_splits);
+        if (merge_here) atomicExch(counter, 0u);
+    }
+    __syncthreads();
+    if (!merge_here) return;
+    __threadfence();
+    for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
+        const int row = idx / D, d = idx % D;
+        merge_one<T>(p, first + row / G, kvh * G + row % G, d);
+    }
 }
 
-// out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the splits that
-// hold this token's keys, in split order; splits without a visible key skipped.
+// The split merge as its own launch: one work-group per (token, head).
 template <typename T>
 __global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) {
-    constexpr int D = kHeadDim;
-    const int li = blockIdx.x, head = blockIdx.y, d = static_cast<int>(threadIdx.x);
-    const int t = p.token_index ? p.token_index[li] : li;
-    const int ctx = min(p.positions[t] + 1, p.max_blocks * kPage);
-    const int ns = min(p.num_splits, max(1, (ctx + p.split_len - 1) / p.split_len));
-    const int64_t base = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, p.part_ml[(base + s) * 2]);
-    float L = 0.0f, O = 0.0f;
-    bool any = false;
-    for (int s = 0; s < ns; s++) {
-        const float ms = p.part_ml[(base + s) * 2];
-        if (ms == -INFINITY) continue;
-        const float f = exp2_hw(ms - M);
-        const float ls = p.part_ml[(base + s) * 2 + 1] * f, os = p.part_acc[(base + s) * D + d] * f;
-        L = any ? L + ls : ls;
-        O = any ? O + os : os;
-        any = true;
-    }
-    T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
-    o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
+    merge_one<T>(p, blockIdx.x, blockIdx.y, static_cast<int>(threadIdx.x));
 }
 
-template <typename T, int ROWS>
+template <typename T, int ROWS, bool FUSED>
 hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_t stream, hipEvent_t start,
                        hipEvent_t stop) {
     const dim3 grid = p.work ? dim3(static_cast<unsigned>(num_work * p.n_kv))
                              : dim3(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv),
                                     static_cast<unsigned>(p.num_splits));
     if (start || stop)
-        hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, start, stop, 0, p);
+        hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, start, stop, 0, p);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, p);
     return hipGetLastError();
 }
 
-template <typename T>
+template <typename T, bool FUSED>
 hipError_t launch_typed(const DecodeParams &p, int runs, int num_work, int rows, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
     switch (rows) {
-        case 1: return launch_rows<T, 1>(p, runs, num_work, stream, start, stop);
-        case 2: return launch_rows<T, 2>(p, runs, num_work, stream, start, stop);
-        case 4: return launch_rows<T, 4>(p, runs, num_work, stream, start, stop);
-        case 8: return launch_rows<T, 8>(p, runs, num_work, stream, start, stop);
-        case 10: return launch_rows<T, 10>(p, runs, num_work, stream, start, stop);
-        case 16: return launch_rows<T, 16>(p, runs, num_work, stream, start, stop);
+        case 1: return launch_rows<T, 1, FUSED>(p, runs, num_work, stream, start, stop);
+        case 2: return launch_rows<T, 2, FUSED>(p, runs, num_work, stream, start, stop);
+        case 4: return launch_rows<T, 4, FUSED>(p, runs, num_work, stream, start, stop);
+        case 8: return launch_rows<T, 8, FUSED>(p, runs, num_work, stream, start, stop);
+        case 10: return launch_rows<T, 10, FUSED>(p, runs, num_work, stream, start, stop);
+        case 16: return launch_rows<T, 16, FUSED>(p, runs, num_work, stream, start, stop);
         default: return hipErrorInvalidValue;
     }
 }
 
-}  // namespace
-
-hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start,
-                               hipEvent_t stop) {
-    if (a.T <= 0) return hipSuccess;
+DecodeParams params_of(const EmberAttnArgs &a) {
     DecodeParams p{};
     p.q = a.q;
     p.k = a.k_cache;
@@ -497,6 +632,7 @@ hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t str
     p.out = a.out;
     p.part_acc = a.part_acc;
     p.part_ml = a.part_ml;
+    p.counters = a.merge_counters;
     p.max_blocks = a.max_blocks;
     p.n_heads = a.n_heads;
     p.n_kv = a.n_kv;
@@ -504,19 +640,49 @@ hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t str
     p.num_blocks = a.num_blocks;
     p.num_splits = a.num_splits;
     p.split_len = a.split_len;
+    p.num_runs = a.run_first ? a.num_runs : a.T;
     p.scale_log2 = a.scale * kLog2e;
-    const int runs = a.run_first ? a.num_runs : a.T;
-    p.num_runs = runs;
-    if (runs <= 0 || (a.work && a.num_work <= 0)) return hipSuccess;
-    hipError_t e = a.dtype == EMBER_DTYPE_F16 ? launch_typed<f16>(p, runs, a.num_work, rows, stream, start, stop)
-                                              : launch_typed<float>(p, runs, a.num_work, rows, stream, start, stop);
-    if (e != hipSuccess || a.num_splits == 1) return e;
+    return p;
+}
+
+hipError_t launch(const DecodeParams &p, const EmberAttnArgs &a, int rows, bool fused, hipStream_t stream,
+                  hipEvent_t start, hipEvent_t stop) {
+    if (p.num_runs <= 0 || (a.work && a.num_work <= 0)) return hipSuccess;
+    hipError_t e;
+    if (a.dtype == EMBER_DTYPE_F16)
+        e = fused ? launch_typed<f16, true>(p, p.num_runs, a.num_work, rows, stream, start, stop)
+                  : launch_typed<f16, false>(p, p.num_runs, a.num_work, rows, stream, start, stop);
+    else
+        e = fused ? launch_typed<float, true>(p, p.num_runs, a.num_work, rows, stream, start, stop)
+                  : launch_typed<float, false>(p, p.num_runs, a.num_work, rows, stream, start, stop);
+    if (e != hipSuccess || a.num_splits == 1 || a.merge_counters) return e;
     const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>(a.n_heads));
     if (a.dtype == EMBER_DTYPE_F16)
         hipLaunchKernelGGL(merge_splits_kernel<f16>, grid, dim3(kHeadDim), 0, stream, p);
     else
         hipLaunchKernelGGL(merge_splits_kernel<float>, grid, dim3(kHeadDim), 0, stream, p);
     return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start,
+                               hipEvent_t stop) {
+    if (a.T <= 0) return hipSuccess;
+    return launch(params_of(a), a, rows, false, stream, start, stop);
+}
+
+hipError_t launch_decode_step(const EmberQkvArgs &qa, const EmberAttnArgs &a, int rows, hipStream_t stream,
+                              hipEvent_t start, hipEvent_t stop) {
+    if (a.T <= 0) return hipSuccess;
+    DecodeParams p = params_of(a);
+    p.qkv = qa.qkv;
+    p.q_norm = qa.q_norm;
+    p.k_norm = qa.k_norm;
+    p.bias = qa.bias;
+    p.inv_freq = qa.inv_freq;
+    p.eps = qa.eps;
+    return launch(p, a, rows, true, stream, start, stop);
 }
 
 }  // namespace ember::hip

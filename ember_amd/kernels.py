@@ -150,21 +150,70 @@ def work_list(run_ctx, split_len: int) -> np.ndarray:
 
 
 def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list=None, runs=None,
-                    split_len=512, num_splits=None, scratch=None, use_work_list=False, stream=None):
+                    split_len=512, num_splits=None, scratch=None, use_work_list=False, merge_in_kernel=False,
+                    stream=None):
     """Paged decode attention (≙ cuda::paged_attention).
 
     token_list: tokens to process (None = all). runs: (run_first, run_count) over
     token_list positions, or None for one token per run. num_splits defaults to
     what the longest context needs at split_len keys per split. use_work_list:
     dispatch through a sorted (run, split) list instead of the dense grid.
+    merge_in_kernel: merge the splits in the last work-group of each (run, kv
+    head) instead of a second launch.
     """
+    a, keep = _attn_args(q, k_pool, v_pool, out, ints, n_heads=n_heads, n_kv=n_kv, token_list=token_list, runs=runs,
+                         split_len=split_len, num_splits=num_splits, scratch=scratch, use_work_list=use_work_list,
+                         merge_in_kernel=merge_in_kernel)
+    if a is None:
+        return keep
+    check(_lib.lib().ember_hip_paged_decode(a, _stream_handle(stream)), "paged_decode")
+    return keep  # the caller keeps the uploads alive until the stream has run
+
+
+def decode_step(qkv, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, inv_freq_dev, q_norm=None, k_norm=None,
+                bias=None, eps=1e-6, runs=None, split_len=512, num_splits=None, use_work_list=False,
+                merge_in_kernel=False, stream=None):
+    """Append + attention in one launch (ember_hip_decode_step); every token of the step is listed, each
+    sequence's tokens forming one run of consecutive positions."""
+    T = ints.T
+    width = (n_heads + 2 * n_kv) * HEAD_DIM
+    if qkv.numel() != T * width:
+        raise EmberError("qkv does not match the step")
+    a, keep = _attn_args(None, k_pool, v_pool, out, ints, n_heads=n_heads, n_kv=n_kv, token_list=None, runs=runs,
+                         split_len=split_len, num_splits=num_splits, scratch=None, use_work_list=use_work_list,
+                         merge_in_kernel=merge_in_kernel, dtype_of=qkv)
+    seqs = ints.token_seq.tolist()
+    if runs is None and len(set(seqs)) != len(seqs):
+        raise EmberError("a sequence with several tokens needs them as one run")
+    if runs is not None:  # one run per sequence, consecutive positions (the kernel relies on both)
+        seen = set()
+        for f, c in zip(*runs):
+            s = int(ints.token_seq[f])
+            if s in seen or np.any(np.diff(ints.positions[f:f + c]) != 1):
+                raise EmberError("each sequence's tokens must form one run of consecutive positions")
+            seen.add(s)
+    pos, seq, tab = ints.device(qkv.device)
+    qa = QkvArgs()
+    qa.qkv, qa.q_out = _dev(qkv, "qkv"), None
+    qa.k_cache, qa.v_cache = a.k_cache, a.v_cache
+    qa.q_norm, qa.k_norm, qa.bias = _opt(q_norm, "q_norm"), _opt(k_norm, "k_norm"), _opt(bias, "bias")
+    qa.inv_freq = _dev(inv_freq_dev, "inv_freq")
+    qa.positions, qa.token_seq, qa.block_tables = pos.data_ptr(), seq.data_ptr(), tab.data_ptr()
+    qa.max_blocks, qa.T, qa.n_heads, qa.n_kv, qa.head_dim = ints.max_blocks, T, n_heads, n_kv, HEAD_DIM
+    qa.eps, qa.num_blocks, qa.dtype = eps, ints.num_blocks, _dtype_code(qkv)
+    check(_lib.lib().ember_hip_decode_step(qa, a, _stream_handle(stream)), "decode_step")
+    return keep
+
+
+def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list, runs, split_len, num_splits,
+               scratch, use_work_list, merge_in_kernel, dtype_of=None):
     tl = np.arange(ints.T, dtype=np.int32) if token_list is None else np.asarray(token_list, np.int32)
     n = int(tl.size)
     if n == 0:
-        return
+        return None, []
     if tl.min() < 0 or tl.max() >= ints.T:
         raise EmberError("token_list names a token outside the step")
-    if q.numel() < ints.T * n_heads * HEAD_DIM or out.numel() < ints.T * n_heads * HEAD_DIM:
+    if (q is not None and q.numel() < ints.T * n_heads * HEAD_DIM) or out.numel() < ints.T * n_heads * HEAD_DIM:
         raise EmberError("q / out are smaller than the step")
     if k_pool.numel() < ints.num_blocks * n_kv * BLOCK_SIZE * HEAD_DIM:
         raise EmberError("pools are smaller than num_blocks pages")
@@ -173,12 +222,13 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
         num_splits = max(1, math.ceil(ctx / split_len))
     if num_splits * split_len < ctx:
         raise EmberError("num_splits x split_len does not cover the context")
-    dev = q.device
+    dev = k_pool.device
     pos, seq, tab = ints.device(dev)
     tl_dev = _ints(tl, dev)
     a = AttnArgs()
     a.token_index = tl_dev.data_ptr()
-    a.q, a.k_cache, a.v_cache = _dev(q, "q"), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    a.q = None if q is None else _dev(q, "q")
+    a.k_cache, a.v_cache = _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
     a.positions, a.token_seq, a.block_tables = pos.data_ptr(), seq.data_ptr(), tab.data_ptr()
     a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = ints.max_blocks, n, n_heads, n_kv, HEAD_DIM
     a.scale = 1.0 / math.sqrt(HEAD_DIM)
@@ -194,7 +244,7 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
             raise EmberError("split scratch too small")
         a.part_acc, a.part_ml = _dev(scratch[0], "part_acc"), _dev(scratch[1], "part_ml")
         keep.append(scratch)
-    a.num_blocks, a.dtype = ints.num_blocks, _dtype_code(q)
+    a.num_blocks, a.dtype = ints.num_blocks, _dtype_code(q if q is not None else dtype_of)
     if runs is not None:
         rf, rc = (np.asarray(x, np.int32) for x in runs)
         if rf.size != rc.size or rc.min() < 1 or rc.max() > MAX_RUN or rf.min() < 0 or (rf + rc).max() > n:
@@ -215,8 +265,11 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
         w_dev = _ints(items.reshape(-1), dev)
         keep.append(w_dev)
         a.work, a.num_work = w_dev.data_ptr(), int(items.shape[0])
-    check(_lib.lib().ember_hip_paged_decode(a, _stream_handle(stream)), "paged_decode")
-    return keep  # the caller keeps the uploads alive until the stream has run
+    if merge_in_kernel:
+        counters = torch.zeros(len(run_ctx) * n_kv, dtype=torch.int32, device=dev)
+        keep.append(counters)
+        a.merge_counters = counters.data_ptr()
+    return a, keep
 
 
 def copy_pages(k_pool, v_pool, src, dst, *, n_layers, layer_stride, n_kv, num_blocks, stream=None):

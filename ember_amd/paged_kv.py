@@ -110,10 +110,15 @@ class PagedKv:
         check(_lib.lib().ember_kv_timing(self._h, ctypes.byref(n), ctypes.byref(ms)), "kv_timing")
         return n.value, ms.value
 
-    def plan_info(self) -> tuple[int, int, int]:
-        r, t, s = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
-        _lib.lib().ember_kv_plan_info(self._h, ctypes.byref(r), ctypes.byref(t), ctypes.byref(s))
-        return r.value, t.value, s.value
+    def plan_info(self) -> tuple[int, int, int, bool]:
+        """(decode runs, prefill tiles, splits, fused) of the current plan."""
+        r, t, s, f = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()
+        _lib.lib().ember_kv_plan_info(self._h, ctypes.byref(r), ctypes.byref(t), ctypes.byref(s), ctypes.byref(f))
+        return r.value, t.value, s.value, bool(f.value)
+
+    def fused(self) -> bool:
+        """Whether the current plan appends and attends in one launch per layer."""
+        return self.plan_info()[3]
 
 
 def _wrap_device(addr: int, numel: int, dtype: torch.dtype) -> torch.Tensor:

@@ -106,6 +106,12 @@ typedef struct EmberAttnArgs {
      * context finishing at once. */
     const int32_t *work;
     int32_t num_work;
+    /* Optional in-kernel split merge: [num_runs * n_kv] counters, zero on
+     * entry and left zero. The last work-group of each (run, kv head) to
+     * finish merges that run's splits, with the same arithmetic and order as
+     * the merge kernel, so no second launch is needed. NULL = a separate
+     * merge kernel when num_splits > 1. */
+    uint32_t *merge_counters;
 } EmberAttnArgs;
 
 /* Paged attention for short runs (decode, speculative verify): one work-group
@@ -114,6 +120,19 @@ typedef struct EmberAttnArgs {
  * Replaces cuda::paged_attention (kernels.cuh:102; k_attention.cu:401-415).
  * head_dim must be 128; G in 1..8. */
 int ember_hip_paged_decode(const EmberAttnArgs *args, void *stream);
+
+/* Append + attention in one launch, for a step in which every sequence's new
+ * tokens form one decode run (decode: 1 token; speculative verify: k + 1 <= 8)
+ * with consecutive positions. Each work-group computes its rows' q
+ * (QK-RMSNorm + RoPE) from qkv->qkv, and the K/V of the new tokens that fall
+ * in its split: those are stored to the pools and used in place of the page
+ * slots they overwrite, so no work-group waits for another. attn->q and
+ * qkv->q_out are not used. Every token of qkv must be listed in attn.
+ * Results (pools and attention) are bit-identical to ember_hip_kv_append
+ * followed by ember_hip_paged_decode. No counterpart in the reference, which
+ * launches qk_norm_rope_store and paged_attention separately
+ * (src/backend/cuda/cuda_backend.cu:357-360). */
+int ember_hip_decode_step(const EmberQkvArgs *qkv, const EmberAttnArgs *attn, void *stream);
 
 /* Replaces cuda::PrefillArgs (kernels.cuh:109-119). */
 typedef struct EmberPrefillArgs {
@@ -247,8 +266,11 @@ void *ember_kv_k_pool(EmberPagedKv *kv, int32_t layer);
 void *ember_kv_v_pool(EmberPagedKv *kv, int32_t layer);
 int64_t ember_kv_layer_stride(const EmberPagedKv *kv); /* elements between layers' pools */
 int32_t ember_kv_spare_block(const EmberPagedKv *kv);  /* the block padding rows write to */
-/* What the current plan launches per layer: decode runs, prefill tiles, splits. */
-int32_t ember_kv_plan_info(const EmberPagedKv *kv, int32_t *decode_runs, int32_t *prefill_tiles, int32_t *num_splits);
+/* What the current plan launches per layer: decode runs, prefill tiles,
+ * splits, and whether append and attention share one launch (every
+ * sequence's new tokens form one run: ember_hip_decode_step). */
+int32_t ember_kv_plan_info(const EmberPagedKv *kv, int32_t *decode_runs, int32_t *prefill_tiles, int32_t *num_splits,
+                           int32_t *fused);
 /* Kernel timing for benchmarks: while on, every layer() records HIP events on
  * the path's stream right before and right after the paged-decode kernel
  * (before the split merge). ember_kv_timing waits for them and returns the

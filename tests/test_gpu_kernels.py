@@ -260,3 +260,77 @@ def test_copy_pages(rng, device):
     for s, d in zip(src, dst):
         ek[:, d], ev[:, d] = k0[:, s], v0[:, s]
     assert np.array_equal(k1.view(np.uint16), ek.view(np.uint16)) and np.array_equal(v1.view(np.uint16), ev.view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("work,merge", [(False, False), (True, True), (False, True)])
+def test_fused_decode_step_equals_append_then_decode(rng, device, dtype, work, merge):
+    """ember_hip_decode_step (append + attention in one launch) leaves the same pools and outputs, to the
+    bit, as ember_hip_kv_append followed by ember_hip_paged_decode; with the split merge in a second launch or
+    in the last work-group of each (run, kv head)."""
+    f16 = dtype == torch.float16
+    NB = 1200
+    cached = [0, 15, 16, 511, 512, 1000, 2049, 3, 700]
+    new = [1, 1, 5, 1, 5, 1, 4, 5, 1]
+    step = make_step(rng, [c + n for c, n in zip(cached, new)], new, NB)
+    k, v = _random_pools(rng, step, NB, f16=f16)
+    for s, (c0, n) in enumerate(zip(cached, new)):  # new slots hold stale garbage before the step
+        for p_ in range(c0, c0 + n):
+            k[step.tables[s, p_ // PAGE], :, p_ % PAGE] = 7.0
+            v[step.tables[s, p_ // PAGE], :, p_ % PAGE] = -3.0
+    qkv = rng.standard_normal((step.T, W)).astype(np.float16 if f16 else np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    inv = torch.from_numpy(oracle.inv_freq(THETA, D)).to(device)
+    dv = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    runs = (step.query_start[:-1], np.diff(step.query_start))
+    # unfused
+    ka, va = dv(k), dv(v)
+    q_out = torch.empty((step.T, H, D), dtype=dtype, device=device)
+    out_a = torch.full((step.T, H, D), float("nan"), dtype=dtype, device=device)
+    K.qk_norm_rope_store(dv(qkv), q_out, ka, va, ints, n_heads=H, n_kv=KVH, inv_freq_dev=inv, q_norm=dv(qn), k_norm=dv(kn))
+    K.paged_attention(q_out, ka, va, out_a, ints, n_heads=H, n_kv=KVH, runs=runs, use_work_list=work, merge_in_kernel=merge)
+    # fused
+    kb, vb = dv(k), dv(v)
+    out_b = torch.full((step.T, H, D), float("nan"), dtype=dtype, device=device)
+    K.decode_step(dv(qkv), kb, vb, out_b, ints, n_heads=H, n_kv=KVH, inv_freq_dev=inv, q_norm=dv(qn), k_norm=dv(kn),
+                  runs=runs, use_work_list=work, merge_in_kernel=merge)
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().numpy().view(np.uint16 if f16 else np.uint32)  # noqa: E731
+    assert np.array_equal(bits(ka), bits(kb)) and np.array_equal(bits(va), bits(vb)), "pools differ"
+    assert np.array_equal(bits(out_a), bits(out_b)), "attention differs"
+    # and both against the oracle
+    ko, vo = np.nan_to_num(k.astype(np.float32)), np.nan_to_num(v.astype(np.float32))
+    q_ref = oracle.append_layer(qkv.astype(np.float32), step.positions, step.query_start, step.tables, ko, vo, n_heads=H,
+                                n_kv=KVH, inv_freq_=oracle.inv_freq(THETA, D), q_norm=qn, k_norm=kn, num_blocks=NB,
+                                kv_f16=False)
+    want = oracle.attention_layer(q_ref, step.positions, step.query_start, step.tables, ko, vo, n_heads=H, n_kv=KVH,
+                                  num_blocks=NB, kv_f16=False, threads=8)
+    assert rel_err(out_b.float().cpu().numpy(), want) < (2e-3 if f16 else 1e-5)
+
+
+def test_in_kernel_merge_leaves_counters_zero_and_matches(rng, device):
+    """The last-arriving work-group merges; counters come back to zero for the next launch, and repeated
+    launches on the same counters give the same bits as the two-launch form."""
+    NB = 1500
+    ctxs = [4096, 3000, 513, 512, 100, 1]
+    step = make_step(rng, ctxs, [1] * len(ctxs), NB)
+    k, v = _random_pools(rng, step, NB, f16=True)
+    kp, vp = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float16)
+    two = _run_decode(q, kp, vp, step, NB, device, use_work_list=True).cpu().numpy().view(np.uint16)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    qd = torch.from_numpy(q).to(device)
+    a, keep = K._attn_args(qd, kp, vp, torch.empty((step.T, H, D), dtype=torch.float16, device=device), ints,
+                           n_heads=H, n_kv=KVH, token_list=None, runs=None, split_len=512, num_splits=None, scratch=None,
+                           use_work_list=True, merge_in_kernel=True)
+    out = torch.empty((step.T, H, D), dtype=torch.float16, device=device)
+    a.out = out.data_ptr()
+    from ember_amd import _lib
+    for _ in range(3):
+        out.fill_(float("nan"))
+        _lib.check(_lib.lib().ember_hip_paged_decode(a, torch.cuda.current_stream().cuda_stream), "paged_decode")
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), two)
+        assert int(keep[-1].abs().sum()) == 0, "merge counters not reset"
