@@ -228,6 +228,18 @@ __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8],
     m = M;
 }
 
+// Split partials are written and read with device-scope (agent) relaxed
+// atomics: on gfx950 these are global_store / global_load with sc1, coherent
+// across the XCDs' L2s by themselves, so the in-kernel merge needs no
+// cache-wide write-back or invalidate (an agent-scope fence is buffer_wbl2 of
+// the whole L2 per work-group, which serializes).
+__device__ __forceinline__ void put_partial(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_partial(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // The split merge of one output element (token list entry li, head, dim d):
 // out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the splits that
 // hold the token's keys, in split order; splits without a visible key skipped.
@@ -240,14 +252,15 @@ __device__ __forceinline__ void merge_one(const DecodeParams &p, int li, int hea
     const int ns = min(p.num_splits, max(1, (ctx + p.split_len - 1) / p.split_len));
     const int64_t base = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits;
     float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, p.part_ml[(base + s) * 2]);
+    for (int s = 0; s < ns; s++) M = fmaxf(M, get_partial(p.part_ml + (base + s) * 2));
     float L = 0.0f, O = 0.0f;
     bool any = false;
     for (int s = 0; s < ns; s++) {
-        const float ms = p.part_ml[(base + s) * 2];
+        const float ms = get_partial(p.part_ml + (base + s) * 2);
         if (ms == -INFINITY) continue;
         const float f = ms == M ? 1.0f : exp2_hw(ms - M);  // one split: exactly O / L, as a direct write
-        const float ls = p.part_ml[(base + s) * 2 + 1] * f, os = p.part_acc[(base + s) * D + d] * f;
+        const float ls = get_partial(p.part_ml + (base + s) * 2 + 1) * f;
+        const float os = get_partial(p.part_acc + (base + s) * D + d) * f;
         L = any ? L + ls : ls;
         O = any ? O + os : os;
         any = true;
@@ -290,7 +303,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     // The run: list entries first .. first + nq - 1, one sequence.
     const int first = p.run_first ? uniform_load(p.run_first + run) : run;
     int nq = p.run_count ? uniform_load(p.run_count + run) : 1;
-    nq = max(1, min(nq, ROWS / G));
+    nq = max(1, min(min(nq, ROWS / G), FUSED ? NEW : ROWS));  // FUSED: new_k / new_v hold NEW tokens
     const int nrows = nq * G;
     const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
     const int32_t *table = p.tables + static_cast<int64_t>(uniform_load(p.token_seq + t0)) * p.max_blocks;
@@ -554,30 +567,30 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
         } else {
             const int64_t slot = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits + split;
-            p.part_acc[slot * D + d] = O;
+            put_partial(p.part_acc + slot * D + d, O);
             if (d == 0) {
-                p.part_ml[slot * 2] = M;
-                p.part_ml[slot * 2 + 1] = L;
+                put_partial(p.part_ml + slot * 2, M);
+                put_partial(p.part_ml + slot * 2 + 1, L);
             }
         }
     }
     if (direct || !p.counters) return;
 
     // In-kernel split merge: every work-group of this (run, kv head) counts in
-    // after its partial is visible device-wide (agent-scope release: the write
-    // back of this XCD's L2); the last one merges, after an acquire, and resets
-    // the counter for the next launch. Nothing waits.
-    __threadfence();
+    // once its partial stores have completed (they are device-coherent sc1
+    // stores, so completion is visibility); the last one merges, reading the
+    // partials with device-coherent loads, and resets the counter for the next
+    // launch. Nothing waits on another work-group.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t *counter = p.counters + static_cast<int64_t>(run) * p.n_kv + kvh;
-        const uint32_t before = atomicAdd(counter, 1u);
+        const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_here = before + 1 == static_cast<uint32_t>(run_splits);
-        if (merge_here) atomicExch(counter, 0u);
+        if (merge_here) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
     if (!merge_here) return;
-    __threadfence();
     for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
         const int row = idx / D, d = idx % D;
         merge_one<T>(p, first + row / G, kvh * G + row % G, d);
