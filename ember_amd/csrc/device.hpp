@@ -60,23 +60,41 @@ __device__ __forceinline__ float clamp_half(float x) { return fminf(fmaxf(x, -kH
 // squares is taken in double (f32 products are exact there), sine and cosine
 // in double rounded once to f32, and the rest in f32 as the CPU writes it.
 // Every lane of the wave must call it (the sum is a wave reduction).
-__device__ __forceinline__ void qk_norm_rope(float &x0, float &x1, const float *w, float eps, int pos,
-                                             const float *inv_freq, int lane) {
-    constexpr int HALF = kHeadDim / 2;
-    if (w) {
+// The lane's operands from memory, loadable ahead of the arithmetic: its two
+// norm weights (unused without a norm) and its rotary frequency.
+struct NormRopeLane {
+    float w0, w1, inv_freq;
+};
+
+__device__ __forceinline__ NormRopeLane norm_rope_lane(const float *w, const float *inv_freq, int lane) {
+    NormRopeLane n;
+    n.w0 = w ? w[lane] : 1.0f;
+    n.w1 = w ? w[lane + kHeadDim / 2] : 1.0f;
+    n.inv_freq = inv_freq[lane];
+    return n;
+}
+
+__device__ __forceinline__ void qk_norm_rope(float &x0, float &x1, bool norm, const NormRopeLane &n, float eps,
+                                             int pos) {
+    if (norm) {
         double ss = static_cast<double>(x0) * x0 + static_cast<double>(x1) * x1;
         ss = wave_sum_f64(ss);
         const float scale = static_cast<float>(1.0 / sqrt(ss / kHeadDim + static_cast<double>(eps)));
-        x0 = w[lane] * (x0 * scale);
-        x1 = w[lane + HALF] * (x1 * scale);
+        x0 = n.w0 * (x0 * scale);
+        x1 = n.w1 * (x1 * scale);
     }
-    const float angle = static_cast<float>(pos) * inv_freq[lane];
+    const float angle = static_cast<float>(pos) * n.inv_freq;
     double sd, cd;
     sincos(static_cast<double>(angle), &sd, &cd);
     const float s = static_cast<float>(sd), c = static_cast<float>(cd);
     const float lo = x0, hi = x1;
     x0 = lo * c - hi * s;
     x1 = hi * c + lo * s;
+}
+
+__device__ __forceinline__ void qk_norm_rope(float &x0, float &x1, const float *w, float eps, int pos,
+                                             const float *inv_freq, int lane) {
+    qk_norm_rope(x0, x1, w != nullptr, norm_rope_lane(w, inv_freq, lane), eps, pos);
 }
 
 // The value a K/V element is stored as: f16 pages clamp to the finite range

@@ -332,59 +332,20 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
     const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
 
-    if constexpr (FUSED) {
-        // q of every row and the new K/V in this split, one head vector per
-        // wave at a time; lane l holds dims l and l + 64 (a rotary pair).
-        const int n_total = p.n_heads + 2 * p.n_kv;
-        const T *qkv = static_cast<const T *>(p.qkv);
-        for (int row = wave; row < nrows; row += kWaves) {
-            const int li = first + row / G;
-            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-            const int head = kvh * G + row % G;
-            const T *src = qkv + (static_cast<int64_t>(t) * n_total + head) * D;
-            float x0 = to_f32(src[lane]), x1 = to_f32(src[lane + D / 2]);
-            if (p.bias) {
-                x0 = x0 + p.bias[head * D + lane];
-                x1 = x1 + p.bias[head * D + lane + D / 2];
-            }
-            qk_norm_rope(x0, x1, p.q_norm, p.eps, uniform_load(p.positions + t), p.inv_freq, lane);
-            q_lds[row][lane] = from_f32<T>(x0);
-            q_lds[row][lane + D / 2] = from_f32<T>(x1);
-        }
-        for (int i = wave; i < nq; i += kWaves) {
-            const int t = p.token_index ? uniform_load(p.token_index + first + i) : first + i;
-            const int pos = uniform_load(p.positions + t);
-            if (pos < begin || pos >= end) continue;  // another split's work-group appends it
-            const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
-            const T *ks = qkv + (static_cast<int64_t>(t) * n_total + kh) * D;
-            const T *vs = qkv + (static_cast<int64_t>(t) * n_total + vh) * D;
-            float k0 = to_f32(ks[lane]), k1 = to_f32(ks[lane + D / 2]);
-            float v0 = to_f32(vs[lane]), v1 = to_f32(vs[lane + D / 2]);
-            if (p.bias) {
-                k0 = k0 + p.bias[kh * D + lane];
-                k1 = k1 + p.bias[kh * D + lane + D / 2];
-                v0 = v0 + p.bias[vh * D + lane];
-                v1 = v1 + p.bias[vh * D + lane + D / 2];
-            }
-            qk_norm_rope(k0, k1, p.k_norm, p.eps, pos, p.inv_freq, lane);
-            const T ek0 = to_page<T>(k0), ek1 = to_page<T>(k1), ev0 = to_page<T>(v0), ev1 = to_page<T>(v1);
-            new_k[i][lane] = ek0;
-            new_k[i][lane + D / 2] = ek1;
-            new_v[i][lane] = ev0;
-            new_v[i][lane + D / 2] = ev1;
-            const int blk = uniform_load(table + pos / kPage);
-            if (blk >= 0 && blk < p.num_blocks) {
-                const int64_t off = static_cast<int64_t>(blk) * block_stride + head_off + (pos % kPage) * D;
-                T *kd = const_cast<T *>(kbase) + off;
-                T *vd = const_cast<T *>(vbase) + off;
-                kd[lane] = ek0;
-                kd[lane + D / 2] = ek1;
-                vd[lane] = ev0;
-                vd[lane + D / 2] = ev1;
-            }
-        }
-        __syncthreads();
-    }
+    // The page walk: wave w takes pages first_page + w, first_page + w + 4, ...
+    // (n of them). Loads are unconditional: past the wave's last page (or with
+    // none) they re-read the split's last page, from cache, so every page is
+    // used with the same number of page loads issued after it and its wait is a
+    // fixed vmcnt that never drains those.
+    const int first_page = begin / kPage, last_page = (end - 1) / kPage;
+    const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
+    auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
+    auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
+    auto fetch = [&](PageRegs<T> &pr, int j) {
+        const int blk = uniform_load(table + min(page_of(j), last_page));  // a scalar load
+        load_page(pr, kbase, vbase, static_cast<int64_t>(in_pool(blk) ? blk : 0) * block_stride + head_off, lane);
+        return blk;
+    };
 
     QSlice<T> q[ROWS];
     float m[ROWS], l[ROWS], acc[ROWS][8];
@@ -394,16 +355,101 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         l[row] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
-        if (row < nrows) {
-            if constexpr (FUSED) {
-                load_q(q[row], &q_lds[row][8 * c]);
-            } else {
-                const int li = first + row / G;
-                const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-                const int head = kvh * G + row % G;
-                load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
-            }
+    }
+    PageRegs<T> A, B;
+    int ba, bb;
+
+    if constexpr (!FUSED) {
+#pragma unroll
+        for (int row = 0; row < ROWS; row++) {
+            if (row >= nrows) continue;
+            const int li = first + row / G;
+            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+            const int head = kvh * G + row % G;
+            load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
         }
+        ba = fetch(A, 0);
+        bb = STAGES == 3 ? fetch(B, 1) : 0;
+    } else {
+        // q of every row and the new K/V in this split, one head vector per
+        // wave at a time; lane l holds dims l and l + 64 (a rotary pair). The
+        // wave's first q row and new token are loaded before its first pages,
+        // so their arithmetic overlaps those page loads, and the barrier after
+        // it waits for LDS only, not for the pages.
+        const int n_total = p.n_heads + 2 * p.n_kv;
+        const T *qkv = static_cast<const T *>(p.qkv);
+        auto token = [&](int i) { return p.token_index ? uniform_load(p.token_index + first + i) : first + i; };
+        auto vec = [&](int t, int head) { return qkv + (static_cast<int64_t>(t) * n_total + head) * D; };
+        const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
+
+        const int row0 = min(wave, nrows - 1), i0 = min(wave, nq - 1);
+        const int qt0 = token(row0 / G), kt0 = token(i0);
+        const int qpos0 = uniform_load(p.positions + qt0), kpos0 = uniform_load(p.positions + kt0);
+        const T *qs0 = vec(qt0, kvh * G + row0 % G), *ks0 = vec(kt0, kh), *vs0 = vec(kt0, vh);
+        const T q0a = qs0[lane], q0b = qs0[lane + D / 2];
+        const T k0a = ks0[lane], k0b = ks0[lane + D / 2], v0a = vs0[lane], v0b = vs0[lane + D / 2];
+        const NormRopeLane qn = norm_rope_lane(p.q_norm, p.inv_freq, lane);
+        const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
+
+        ba = fetch(A, 0);
+        bb = STAGES == 3 ? fetch(B, 1) : 0;
+
+        auto put_q = [&](int row, float x0, float x1, int pos) {
+            const int head = kvh * G + row % G;
+            if (p.bias) {
+                x0 = x0 + p.bias[head * D + lane];
+                x1 = x1 + p.bias[head * D + lane + D / 2];
+            }
+            qk_norm_rope(x0, x1, p.q_norm != nullptr, qn, p.eps, pos);
+            q_lds[row][lane] = from_f32<T>(x0);
+            q_lds[row][lane + D / 2] = from_f32<T>(x1);
+        };
+        auto put_kv = [&](int i, float k0, float k1, float v0, float v1, int pos) {
+            if (p.bias) {
+                k0 = k0 + p.bias[kh * D + lane];
+                k1 = k1 + p.bias[kh * D + lane + D / 2];
+                v0 = v0 + p.bias[vh * D + lane];
+                v1 = v1 + p.bias[vh * D + lane + D / 2];
+            }
+            qk_norm_rope(k0, k1, p.k_norm != nullptr, kn, p.eps, pos);
+            const T ek0 = to_page<T>(k0), ek1 = to_page<T>(k1), ev0 = to_page<T>(v0), ev1 = to_page<T>(v1);
+            new_k[i][lane] = ek0;
+            new_k[i][lane + D / 2] = ek1;
+            new_v[i][lane] = ev0;
+            new_v[i][lane + D / 2] = ev1;
+            const int blk = uniform_load(table + pos / kPage);
+            if (in_pool(blk)) {
+                const int64_t off = static_cast<int64_t>(blk) * block_stride + head_off + (pos % kPage) * D;
+                T *kd = const_cast<T *>(kbase) + off;
+                T *vd = const_cast<T *>(vbase) + off;
+                kd[lane] = ek0;
+                kd[lane + D / 2] = ek1;
+                vd[lane] = ev0;
+                vd[lane + D / 2] = ev1;
+            }
+        };
+        // A new token is appended by the work-group whose split holds its position.
+        auto in_split = [&](int pos) { return pos >= begin && pos < end; };
+
+        if (wave < nrows) put_q(row0, to_f32(q0a), to_f32(q0b), qpos0);
+        for (int row = wave + kWaves; row < nrows; row += kWaves) {
+            const int t = token(row / G);
+            const T *s = vec(t, kvh * G + row % G);
+            put_q(row, to_f32(s[lane]), to_f32(s[lane + D / 2]), uniform_load(p.positions + t));
+        }
+        if (wave < nq && in_split(kpos0)) put_kv(i0, to_f32(k0a), to_f32(k0b), to_f32(v0a), to_f32(v0b), kpos0);
+        for (int i = wave + kWaves; i < nq; i += kWaves) {
+            const int t = token(i), pos = uniform_load(p.positions + t);
+            if (!in_split(pos)) continue;
+            const T *ks = vec(t, kh), *vs = vec(t, vh);
+            put_kv(i, to_f32(ks[lane]), to_f32(ks[lane + D / 2]), to_f32(vs[lane]), to_f32(vs[lane + D / 2]), pos);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+        for (int row = 0; row < ROWS; row++)
+            if (row < nrows) load_q(q[row], &q_lds[row][8 * c]);
     }
 
     // One page: scores and online softmax for every row, then the values key by
@@ -467,62 +513,26 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         process(pr, page, ok);
     };
 
-    {
-        const int first_page = begin / kPage, last_page = (end - 1) / kPage;
-        const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
-        // Block id of this wave's j-th page (a scalar load) and whether it lies in the pool.
-        auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
-        auto block_of = [&](int j) { return uniform_load(table + page_of(j)); };
-        auto offset_of = [&](int blk) {
-            const bool ok = blk >= 0 && blk < p.num_blocks;
-            return static_cast<int64_t>(ok ? blk : 0) * block_stride + head_off;
-        };
-        auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
-        if constexpr (STAGES == 3) {
-            // Loads are unconditional (past the wave's last page they re-read it,
-            // from cache), so every page is used with exactly two pages' loads
-            // issued after it and the wait before it is vmcnt(16), never vmcnt(0).
-            auto fetch = [&](PageRegs<T> &pr, int j) {
-                const int blk = block_of(min(j, n - 1));
-                load_page(pr, kbase, vbase, offset_of(blk), lane);
-                return blk;
-            };
-            PageRegs<T> A, B, C;
-            if (n > 0) {
-                int ba = fetch(A, 0);
-                int bb = fetch(B, 1);
-                for (int j = 0;; j += 3) {
-                    const int bc = fetch(C, j + 2);
-                    consume(A, page_of(j), in_pool(ba));
-                    if (j + 1 >= n) break;
-                    ba = fetch(A, j + 3);
-                    consume(B, page_of(j + 1), in_pool(bb));
-                    if (j + 2 >= n) break;
-                    bb = fetch(B, j + 4);
-                    consume(C, page_of(j + 2), in_pool(bc));
-                    if (j + 3 >= n) break;
-                }
-            }
-        } else {
-            PageRegs<T> A, B;
-            int ba = 0, bb = 0;
-            if (n > 0) {
-                ba = block_of(0);
-                load_page(A, kbase, vbase, offset_of(ba), lane);
-            }
-            for (int j = 0; j < n; j += 2) {
-                if (j + 1 < n) {
-                    bb = block_of(j + 1);
-                    load_page(B, kbase, vbase, offset_of(bb), lane);
-                }
-                consume(A, page_of(j), in_pool(ba));
-                if (j + 1 >= n) break;
-                if (j + 2 < n) {
-                    ba = block_of(j + 2);
-                    load_page(A, kbase, vbase, offset_of(ba), lane);
-                }
-                consume(B, page_of(j + 1), in_pool(bb));
-            }
+    if constexpr (STAGES == 3) {
+        // Two pages in flight while one is used: page j waits at vmcnt(16).
+        PageRegs<T> C;
+        for (int j = 0; j < n; j += 3) {
+            const int bc = fetch(C, j + 2);
+            consume(A, page_of(j), in_pool(ba));
+            if (j + 1 >= n) break;
+            ba = fetch(A, j + 3);
+            consume(B, page_of(j + 1), in_pool(bb));
+            if (j + 2 >= n) break;
+            bb = fetch(B, j + 4);
+            consume(C, page_of(j + 2), in_pool(bc));
+        }
+    } else {
+        for (int j = 0; j < n; j += 2) {
+            bb = fetch(B, j + 1);
+            consume(A, page_of(j), in_pool(ba));
+            if (j + 1 >= n) break;
+            ba = fetch(A, j + 2);
+            consume(B, page_of(j + 1), in_pool(bb));
         }
     }
 
