@@ -44,6 +44,7 @@
 // factor 1 exactly, zero weights). Hence verify of k + 1 tokens equals k + 1
 // single-token decode steps bit-exactly.
 #include <climits>
+#include <type_traits>
 
 #include <hip/hip_ext.h>
 
@@ -94,35 +95,66 @@ struct PageRegs<float> {
     float4 k[4][2], v[4][2];
 };
 
+// Page data is read once per launch and never again before it leaves the
+// caches, so it is loaded non-temporally (nt): on MI355X a page gather of this
+// shape then reaches about 6.2 TB/s instead of about 5.6 TB/s with ordinary
+// loads, which fill the caches with dead lines.
+// Loads one page of one kv head through a buffer descriptor built from the
+// wave-uniform page address (scalar registers): each load is
+// buffer_load_dwordx4 v, v_lane_off, s[desc] offen offset:imm nt, with no
+// per-page vector address arithmetic. A descriptor with no records (live =
+// false) makes the loads return 0 without touching memory.
+constexpr int kDescWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+constexpr int kNonTemporal = 2;         // cache-policy bit nt of a gfx950 buffer load
+
+__device__ __forceinline__ uint4 load_desc(__amdgpu_buffer_rsrc_t d, uint32_t off) {
+    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+    const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(d, off, 0, kNonTemporal);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <typename T>
-__device__ __forceinline__ void load_page(PageRegs<T> &pr, const T *kbase, const T *vbase, int64_t page_off, int lane) {
-    const T *kp = kbase + page_off + 8 * lane;
-    const T *vp = vbase + page_off + 8 * lane;
+__device__ __forceinline__ void load_page(PageRegs<T> &pr, const T *kp, const T *vp, uint32_t lane_off, bool live) {
+    constexpr uint32_t kStep = 512 * sizeof(T);        // bytes between a lane's four slices of the page
+    constexpr int kBytes = kPage * kHeadDim * sizeof(T);  // one page of one kv head
+    const __amdgpu_buffer_rsrc_t dk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(kp), 0, live ? kBytes : 0, kDescWord3);
+    const __amdgpu_buffer_rsrc_t dv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(vp), 0, live ? kBytes : 0, kDescWord3);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (sizeof(T) == 2) {
-            pr.k[i] = *reinterpret_cast<const uint4 *>(kp + 512 * i);
-            pr.v[i] = *reinterpret_cast<const uint4 *>(vp + 512 * i);
+            pr.k[i] = load_desc(dk, lane_off + kStep * i);
+            pr.v[i] = load_desc(dv, lane_off + kStep * i);
         } else {
-            pr.k[i][0] = *reinterpret_cast<const float4 *>(kp + 512 * i);
-            pr.k[i][1] = *reinterpret_cast<const float4 *>(kp + 512 * i + 4);
-            pr.v[i][0] = *reinterpret_cast<const float4 *>(vp + 512 * i);
-            pr.v[i][1] = *reinterpret_cast<const float4 *>(vp + 512 * i + 4);
+            const uint4 k0 = load_desc(dk, lane_off + kStep * i), k1 = load_desc(dk, lane_off + kStep * i + 16);
+            const uint4 v0 = load_desc(dv, lane_off + kStep * i), v1 = load_desc(dv, lane_off + kStep * i + 16);
+            pr.k[i][0] = make_float4(__uint_as_float(k0.x), __uint_as_float(k0.y), __uint_as_float(k0.z), __uint_as_float(k0.w));
+            pr.k[i][1] = make_float4(__uint_as_float(k1.x), __uint_as_float(k1.y), __uint_as_float(k1.z), __uint_as_float(k1.w));
+            pr.v[i][0] = make_float4(__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w));
+            pr.v[i][1] = make_float4(__uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w));
         }
     }
 }
 
-// Replaces key i of a page with the 8 dims this lane holds, read from LDS.
+// Replaces key i of a page with the 8 dims this lane holds, read from LDS, in
+// the lanes where `take` holds: the LDS rows are read by every lane (the
+// caller passes an in-range row) and kept by selects, with no divergent branch.
+__device__ __forceinline__ uint4 select4(bool take, const uint4 &a, const uint4 &b) {
+    return make_uint4(take ? a.x : b.x, take ? a.y : b.y, take ? a.z : b.z, take ? a.w : b.w);
+}
+__device__ __forceinline__ float4 select4(bool take, const float4 &a, const float4 &b) {
+    return make_float4(take ? a.x : b.x, take ? a.y : b.y, take ? a.z : b.z, take ? a.w : b.w);
+}
+
 template <typename T>
-__device__ __forceinline__ void put_key(PageRegs<T> &pr, int i, const T *k8, const T *v8) {
+__device__ __forceinline__ void put_key(PageRegs<T> &pr, int i, bool take, const T *k8, const T *v8) {
     if constexpr (sizeof(T) == 2) {
-        pr.k[i] = *reinterpret_cast<const uint4 *>(k8);
-        pr.v[i] = *reinterpret_cast<const uint4 *>(v8);
+        pr.k[i] = select4(take, *reinterpret_cast<const uint4 *>(k8), pr.k[i]);
+        pr.v[i] = select4(take, *reinterpret_cast<const uint4 *>(v8), pr.v[i]);
     } else {
-        pr.k[i][0] = *reinterpret_cast<const float4 *>(k8);
-        pr.k[i][1] = *reinterpret_cast<const float4 *>(k8 + 4);
-        pr.v[i][0] = *reinterpret_cast<const float4 *>(v8);
-        pr.v[i][1] = *reinterpret_cast<const float4 *>(v8 + 4);
+        pr.k[i][0] = select4(take, *reinterpret_cast<const float4 *>(k8), pr.k[i][0]);
+        pr.k[i][1] = select4(take, *reinterpret_cast<const float4 *>(k8 + 4), pr.k[i][1]);
+        pr.v[i][0] = select4(take, *reinterpret_cast<const float4 *>(v8), pr.v[i][0]);
+        pr.v[i][1] = select4(take, *reinterpret_cast<const float4 *>(v8 + 4), pr.v[i][1]);
     }
 }
 
@@ -241,33 +273,65 @@ __device__ __forceinline__ float get_partial(const float *p) {
 }
 
 // The split merge of one output element (token list entry li, head, dim d):
-// out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the splits that
+// out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the ns splits that
 // hold the token's keys, in split order; splits without a visible key skipped.
-// Used by the merge kernel and by the in-kernel merge alike.
+// Used by the merge kernel and by the in-kernel merge alike. The partials of
+// up to kMergeChunk splits are requested together and waited for once: a
+// merge costs one memory round trip per chunk instead of one per split.
+constexpr int kMergeChunk = 8;
+
 template <typename T>
-__device__ __forceinline__ void merge_one(const DecodeParams &p, int li, int head, int d) {
+__device__ __forceinline__ void merge_one(const DecodeParams &p, int li, int head, int d, int ctx, T *out) {
     constexpr int D = kHeadDim;
-    const int t = p.token_index ? p.token_index[li] : li;
-    const int ctx = min(p.positions[t] + 1, p.max_blocks * kPage);
     const int ns = min(p.num_splits, max(1, (ctx + p.split_len - 1) / p.split_len));
     const int64_t base = (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits;
+    const float *ml = p.part_ml + base * 2;
+    const float *acc = p.part_acc + base * D + d;
     float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, get_partial(p.part_ml + (base + s) * 2));
+    float mv[kMergeChunk], lv[kMergeChunk], ov[kMergeChunk];
+    // Pass 1 (only when there are more splits than one chunk holds): the max.
+    if (ns > kMergeChunk) {
+        for (int s0 = 0; s0 < ns; s0 += kMergeChunk) {
+#pragma unroll
+            for (int k = 0; k < kMergeChunk; k++) mv[k] = get_partial(ml + 2 * min(s0 + k, ns - 1));
+#pragma unroll
+            for (int k = 0; k < kMergeChunk; k++) M = fmaxf(M, mv[k]);  // repeats of the last split change nothing
+        }
+    }
+    // Pass 2: the sums, in split order.
     float L = 0.0f, O = 0.0f;
     bool any = false;
-    for (int s = 0; s < ns; s++) {
-        const float ms = get_partial(p.part_ml + (base + s) * 2);
-        if (ms == -INFINITY) continue;
-        const float f = ms == M ? 1.0f : exp2_hw(ms - M);  // one split: exactly O / L, as a direct write
-        const float ls = get_partial(p.part_ml + (base + s) * 2 + 1) * f;
-        const float os = get_partial(p.part_acc + (base + s) * D + d) * f;
-        L = any ? L + ls : ls;
-        O = any ? O + os : os;
-        any = true;
+    for (int s0 = 0; s0 < ns; s0 += kMergeChunk) {
+#pragma unroll
+        for (int k = 0; k < kMergeChunk; k++) {
+            const int s = min(s0 + k, ns - 1);
+            mv[k] = get_partial(ml + 2 * s);
+            lv[k] = get_partial(ml + 2 * s + 1);
+            ov[k] = get_partial(acc + static_cast<int64_t>(s) * D);
+        }
+        if (ns <= kMergeChunk) {
+#pragma unroll
+            for (int k = 0; k < kMergeChunk; k++) M = fmaxf(M, mv[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kMergeChunk; k++) {
+            if (s0 + k >= ns || mv[k] == -INFINITY) continue;
+            const float f = mv[k] == M ? 1.0f : exp2_hw(mv[k] - M);  // one split: exactly O / L, as a direct write
+            const float ls = lv[k] * f;
+            const float os = ov[k] * f;
+            L = any ? L + ls : ls;
+            O = any ? O + os : os;
+            any = true;
+        }
     }
-    T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
-    o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
+    out[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
 }
+
+// Keeps the compiler's scheduler from moving instructions across this point:
+// the page loop is written as load-next / use-current phases, and letting the
+// scheduler hoist a phase's arithmetic above the next page's loads would leave
+// fewer pages in flight.
+__device__ __forceinline__ void phase_break() { __builtin_amdgcn_sched_barrier(0); }
 
 template <typename T, int ROWS, bool FUSED>
 __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
@@ -300,11 +364,15 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     __shared__ __align__(16) T new_k[NEW][D], new_v[NEW][D];
     __shared__ int merge_here;
 
-    // The run: list entries first .. first + nq - 1, one sequence.
+    // The run: list entries first .. first + nq - 1, one sequence. Its rows are
+    // (token i, head kvh * G + g) for row = i * G + g < nrows; rows nrows ..
+    // ROWS - 1 repeat the last real row, so the page loop always computes ROWS
+    // rows with no per-row tests (their results are never stored).
     const int first = p.run_first ? uniform_load(p.run_first + run) : run;
     int nq = p.run_count ? uniform_load(p.run_count + run) : 1;
     nq = max(1, min(min(nq, ROWS / G), FUSED ? NEW : ROWS));  // FUSED: new_k / new_v hold NEW tokens
     const int nrows = nq * G;
+    auto src_row = [&](int row) { return min(row, nrows - 1); };
     const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
     const int32_t *table = p.tables + static_cast<int64_t>(uniform_load(p.token_seq + t0)) * p.max_blocks;
 
@@ -312,14 +380,11 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     int min_pos = INT_MAX, max_pos = -1;
 #pragma unroll
     for (int row = 0; row < ROWS; row++) {
-        row_pos[row] = -1;
-        if (row < nrows) {
-            const int li = first + row / G;
-            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-            row_pos[row] = uniform_load(p.positions + t);
-            min_pos = min(min_pos, row_pos[row]);
-            max_pos = max(max_pos, row_pos[row]);
-        }
+        const int li = first + src_row(row) / G;
+        const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+        row_pos[row] = uniform_load(p.positions + t);
+        min_pos = min(min_pos, row_pos[row]);
+        max_pos = max(max_pos, row_pos[row]);
     }
     const int ctx_max = min(max_pos + 1, p.max_blocks * kPage);
     const int begin = split * p.split_len;
@@ -333,18 +398,21 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
 
     // The page walk: wave w takes pages first_page + w, first_page + w + 4, ...
-    // (n of them). Loads are unconditional: past the wave's last page (or with
-    // none) they re-read the split's last page, from cache, so every page is
-    // used with the same number of page loads issued after it and its wait is a
-    // fixed vmcnt that never drains those.
+    // (n of them). Every page of the loop is fetched the same way, so each use
+    // waits at a fixed vmcnt: a fetch past the wave's last page gets a
+    // descriptor with no records (its loads return 0 and touch no memory), and
+    // a block id outside the pool is read as a page of zeros the same way (the
+    // host plan never hands such an id to the kernel).
     const int first_page = begin / kPage, last_page = (end - 1) / kPage;
     const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
     auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
     auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
+    const uint32_t lane_off = 8u * sizeof(T) * static_cast<uint32_t>(lane);
     auto fetch = [&](PageRegs<T> &pr, int j) {
         const int blk = uniform_load(table + min(page_of(j), last_page));  // a scalar load
-        load_page(pr, kbase, vbase, static_cast<int64_t>(in_pool(blk) ? blk : 0) * block_stride + head_off, lane);
-        return blk;
+        const bool live = j < n && in_pool(blk);
+        const int64_t off = static_cast<int64_t>(live ? blk : 0) * block_stride + head_off;
+        load_page(pr, kbase + off, vbase + off, lane_off, live);
     };
 
     QSlice<T> q[ROWS];
@@ -357,19 +425,17 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
     }
     PageRegs<T> A, B;
-    int ba, bb;
 
     if constexpr (!FUSED) {
 #pragma unroll
         for (int row = 0; row < ROWS; row++) {
-            if (row >= nrows) continue;
-            const int li = first + row / G;
+            const int li = first + src_row(row) / G;
             const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-            const int head = kvh * G + row % G;
+            const int head = kvh * G + src_row(row) % G;
             load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
         }
-        ba = fetch(A, 0);
-        bb = STAGES == 3 ? fetch(B, 1) : 0;
+        fetch(A, 0);
+        if constexpr (STAGES == 3) fetch(B, 1);
     } else {
         // q of every row and the new K/V in this split, one head vector per
         // wave at a time; lane l holds dims l and l + 64 (a rotary pair). The
@@ -391,8 +457,8 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         const NormRopeLane qn = norm_rope_lane(p.q_norm, p.inv_freq, lane);
         const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
 
-        ba = fetch(A, 0);
-        bb = STAGES == 3 ? fetch(B, 1) : 0;
+        fetch(A, 0);
+        if constexpr (STAGES == 3) fetch(B, 1);
 
         auto put_q = [&](int row, float x0, float x1, int pos) {
             const int head = kvh * G + row % G;
@@ -448,27 +514,31 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-        for (int row = 0; row < ROWS; row++)
-            if (row < nrows) load_q(q[row], &q_lds[row][8 * c]);
+        for (int row = 0; row < ROWS; row++) load_q(q[row], &q_lds[src_row(row)][8 * c]);
     }
 
     // One page: scores and online softmax for every row, then the values key by
     // key (each key's 8 dims converted once, used by every row). Per row the
     // operations and their order are: rescale by corr, then fma over keys 0..3.
-    auto process = [&](const PageRegs<T> &pr, int page, bool ok) {
+    // MASKED = false: every key of the page is visible to every row (the page
+    // lies below the run's lowest position). MASKED = true: per-row visibility,
+    // with selects, so a hidden key leaves a row's state bit-for-bit unchanged;
+    // for a fully visible page both forms compute the same bits.
+    auto process = [&](const PageRegs<T> &pr, int page, auto masked_tag) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
-        const bool fast = ok && (page + 1) * kPage <= min_pos + 1;  // every key visible to every row
         float pj[ROWS][4];
         bool vis[ROWS][4];
 #pragma unroll
         for (int row = 0; row < ROWS; row++) {
-            if (row >= nrows) continue;
             float s[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 s[i] = row16_sum(dot8(q[row], pr.k[i])) * p.scale_log2;
-                vis[row][i] = fast || (ok && key0 + 4 * i <= row_pos[row]);
-                if (!vis[row][i]) s[i] = -INFINITY;
+                if constexpr (MASKED) {
+                    vis[row][i] = key0 + 4 * i <= row_pos[row];
+                    if (!vis[row][i]) s[i] = -INFINITY;
+                }
             }
             const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
             const float ref = mn == -INFINITY ? 0.0f : mn;
@@ -486,8 +556,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             unpack8(pr.v[i], vf);
 #pragma unroll
             for (int row = 0; row < ROWS; row++) {
-                if (row >= nrows) continue;
-                if (fast) {
+                if constexpr (!MASKED) {
 #pragma unroll
                     for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[row][i], vf[e], acc[row][e]);
                 } else {
@@ -498,42 +567,82 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             }
         }
     };
-    // The fused form first puts this launch's new keys into the page they land
-    // in (in place: the registers are reloaded after use anyway).
-    auto consume = [&](PageRegs<T> &pr, int page, bool ok) {
+    using Fast = std::false_type;
+    using Masked = std::true_type;
+    // A page of the masked part: the fused form first puts this launch's new
+    // keys into the page they land in (in place: the registers are reloaded
+    // after use anyway).
+    auto consume = [&](PageRegs<T> &pr, int page) {
         if constexpr (FUSED) {
             if (page * kPage <= max_pos && (page + 1) * kPage > min_pos) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int j = page * kPage + r + 4 * i - min_pos;  // the run's positions are consecutive
-                    if (j >= 0 && j < nq) put_key(pr, i, &new_k[j][8 * c], &new_v[j][8 * c]);
+                    const int jc = min(max(j, 0), nq - 1);
+                    put_key(pr, i, j >= 0 && j < nq, &new_k[jc][8 * c], &new_v[jc][8 * c]);
                 }
             }
         }
-        process(pr, page, ok);
+        process(pr, page, Masked{});
     };
 
+    // The wave's fast pages come first (pages below min_pos / 16 hold no new key
+    // and only keys every row sees); they run through a loop with no masking.
+    // What is left is short: the loop stops with fewer than STAGES fast pages
+    // to go, and the run's positions (at most EMBER_MAX_RUN, consecutive) lie
+    // in at most two adjacent pages, of which a wave (stride 4 pages) gets at
+    // most one. So at most STAGES pages remain, already in flight or fetched
+    // once more, and they go through the masked path as straight-line code;
+    // the loop after it only serves runs that break that bound.
+    const int fast_end = min_pos / kPage;
+    const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
+    int j = 0;
     if constexpr (STAGES == 3) {
         // Two pages in flight while one is used: page j waits at vmcnt(16).
         PageRegs<T> C;
-        for (int j = 0; j < n; j += 3) {
-            const int bc = fetch(C, j + 2);
-            consume(A, page_of(j), in_pool(ba));
-            if (j + 1 >= n) break;
-            ba = fetch(A, j + 3);
-            consume(B, page_of(j + 1), in_pool(bb));
-            if (j + 2 >= n) break;
-            bb = fetch(B, j + 4);
-            consume(C, page_of(j + 2), in_pool(bc));
+        for (; j + 3 <= n_fast; j += 3) {
+            fetch(C, j + 2);
+            phase_break();
+            process(A, page_of(j), Fast{});
+            phase_break();
+            fetch(A, j + 3);
+            phase_break();
+            process(B, page_of(j + 1), Fast{});
+            phase_break();
+            fetch(B, j + 4);
+            phase_break();
+            process(C, page_of(j + 2), Fast{});
+            phase_break();
         }
+        fetch(C, j + 2);
+        phase_break();
+        if (j < n) consume(A, page_of(j));
+        phase_break();
+        if (j + 1 < n) consume(B, page_of(j + 1));
+        phase_break();
+        if (j + 2 < n) consume(C, page_of(j + 2));
+        j += 3;
     } else {
-        for (int j = 0; j < n; j += 2) {
-            bb = fetch(B, j + 1);
-            consume(A, page_of(j), in_pool(ba));
-            if (j + 1 >= n) break;
-            ba = fetch(A, j + 2);
-            consume(B, page_of(j + 1), in_pool(bb));
+        for (; j + 2 <= n_fast; j += 2) {
+            fetch(B, j + 1);
+            phase_break();
+            process(A, page_of(j), Fast{});
+            phase_break();
+            fetch(A, j + 2);
+            phase_break();
+            process(B, page_of(j + 1), Fast{});
+            phase_break();
         }
+        fetch(B, j + 1);
+        phase_break();
+        if (j < n) consume(A, page_of(j));
+        phase_break();
+        if (j + 1 < n) consume(B, page_of(j + 1));
+        j += 2;
+    }
+    for (; j < n; j++) {
+        fetch(A, j);
+        consume(A, page_of(j));
     }
 
     // Merge the four DPP rows of the wave (rows 0+1 and 2+3, then the pairs).
@@ -603,14 +712,24 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     if (!merge_here) return;
     for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
         const int row = idx / D, d = idx % D;
-        merge_one<T>(p, first + row / G, kvh * G + row % G, d);
+        const int li = first + row / G, head = kvh * G + row % G;
+        int pos = row_pos[0];
+#pragma unroll
+        for (int k = 1; k < ROWS; k++) pos = row == k ? row_pos[k] : pos;
+        const int t = p.token_index ? p.token_index[li] : li;
+        T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
+        merge_one<T>(p, li, head, d, min(pos + 1, p.max_blocks * kPage), o);
     }
 }
 
 // The split merge as its own launch: one work-group per (token, head).
 template <typename T>
 __global__ void __launch_bounds__(kHeadDim) merge_splits_kernel(DecodeParams p) {
-    merge_one<T>(p, blockIdx.x, blockIdx.y, static_cast<int>(threadIdx.x));
+    const int li = static_cast<int>(blockIdx.x), head = static_cast<int>(blockIdx.y);
+    const int t = p.token_index ? p.token_index[li] : li;
+    const int ctx = min(p.positions[t] + 1, p.max_blocks * kPage);
+    T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * kHeadDim;
+    merge_one<T>(p, li, head, static_cast<int>(threadIdx.x), ctx, o);
 }
 
 template <typename T, int ROWS, bool FUSED>

@@ -89,7 +89,8 @@ typedef struct EmberAttnArgs {
     float *part_acc;              /* [T, n_heads, num_splits, head_dim], indexed by list position 0..T-1 */
     float *part_ml;               /* [T, n_heads, num_splits, 2] */
     /* additions */
-    int32_t num_blocks;           /* blocks in this layer's pool; pages outside it are skipped */
+    int32_t num_blocks;           /* blocks in this layer's pool; a table entry outside it reads as a page of
+                                   * zeros (its loads are bounds-checked and touch no memory) */
     int32_t dtype;                /* EMBER_DTYPE_* of q, out and the pools */
     /* Query runs: list entries [run_first[r], run_first[r] + run_count[r]) are
      * consecutive tokens of one sequence; one work-group reads each page once
