@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 1
+ABI_VERSION = 2
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
@@ -45,7 +45,7 @@ class AttnArgs(ctypes.Structure):
         ("scale", c_float), ("out", c_void_p), ("num_splits", c_int32), ("split_len", c_int32),
         ("part_acc", c_void_p), ("part_ml", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
         ("run_first", c_void_p), ("run_count", c_void_p), ("num_runs", c_int32), ("max_run", c_int32),
-        ("work", c_void_p), ("num_work", c_int32), ("merge_counters", c_void_p),
+        ("work", c_void_p), ("num_work", c_int32), ("merge_counters", c_void_p), ("work_desc", c_void_p),
     ]
 
 

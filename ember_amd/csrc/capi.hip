@@ -95,6 +95,12 @@ int ember_hip_decode_step(const EmberQkvArgs *qkv, const EmberAttnArgs *attn, vo
 
 }  // extern "C"
 
+int ember::hip::decode_rows(int G, int max_run) {
+    for (int r : kDecodeRowInstances)
+        if (r >= G * max_run) return r;
+    return 0;
+}
+
 int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
                              const EmberQkvArgs *qkv) {
     g_last_error.clear();
@@ -139,14 +145,8 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
             static_cast<long long>(a->num_work) * a->n_kv > 0x7fffffffLL)
             return set_error(EMBER_ERR_INVALID, "paged_decode: num_work %d out of range", a->num_work);
     }
-    const int need = G * max_run;
-    int rows = 0;
-    for (int r : kDecodeRowInstances)
-        if (r >= need) {
-            rows = r;
-            break;
-        }
-    if (!rows) return set_error(EMBER_ERR_INVALID, "paged_decode: %d query rows per work-group exceed 16", need);
+    const int rows = decode_rows(G, max_run);
+    if (!rows) return set_error(EMBER_ERR_INVALID, "paged_decode: %d query rows per work-group exceed 16", G * max_run);
     if (qkv) return hip_status(launch_decode_step(*qkv, *a, rows, stream, start, stop), "decode_step");
     return hip_status(launch_paged_decode(*a, rows, stream, start, stop), "paged_decode");
 }

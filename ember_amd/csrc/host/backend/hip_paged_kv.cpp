@@ -4,6 +4,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 
 #include "common/error.hpp"
@@ -74,9 +75,11 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     inv_freq_ = device_alloc<float>(inv.size());
     EMBER_HIP_CHECK(hipMemcpyAsync(inv_freq_, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice, stream_));
 
-    // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables, work items.
+    // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables, work items and their
+    // descriptors (8 ints each, 128-byte aligned like every array here).
     ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
-                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) + 64;
+                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) +
+                     pad32(8 * T * max_splits_) + 64;
     dev_ints_ = device_alloc<int32_t>(ints_capacity_);
     for (int i = 0; i < 2; i++) {
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
@@ -195,6 +198,27 @@ void HipPagedKv::plan(const StepBatch &b) {
         work_.push_back(run_ctx_[static_cast<size_t>(r)] / opt_.split_len);
     }
     num_work_ = static_cast<int>(work_.size() / 2);
+    // The kernel's view of each item (EmberAttnArgs::work_desc): everything it
+    // would otherwise look up in a chain before its first page load.
+    work_desc_.assign(static_cast<size_t>(num_work_) * 8, 0);
+    for (int i = 0; i < num_work_; i++) {
+        const int r = work_[2 * static_cast<size_t>(i)];
+        const int first = run_first_[static_cast<size_t>(r)], count = run_count_[static_cast<size_t>(r)];
+        int lo = INT32_MAX, hi = -1;
+        for (int k = 0; k < count; k++) {
+            const int pos = b.positions[static_cast<size_t>(decode_[static_cast<size_t>(first + k)])];
+            lo = std::min(lo, pos);
+            hi = std::max(hi, pos);
+        }
+        int32_t *d = &work_desc_[8 * static_cast<size_t>(i)];
+        d[0] = r;
+        d[1] = work_[2 * static_cast<size_t>(i) + 1];
+        d[2] = first;
+        d[3] = count;
+        d[4] = token_seq_[static_cast<size_t>(decode_[static_cast<size_t>(first)])];
+        d[5] = lo;
+        d[6] = hi;
+    }
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.
     stage_ ^= 1;
@@ -217,6 +241,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     put(tile_end_.data(), tile_end_.size());
     put(tile_seq_.data(), tile_seq_.size());
     put(work_.data(), work_.size());
+    put(work_desc_.data(), work_desc_.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
     EMBER_HIP_CHECK(hipMemcpyAsync(dev_ints_, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
     EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], stream_));
@@ -230,6 +255,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     d_tile_end_ = dev_ints_ + at[7];
     d_tile_seq_ = dev_ints_ + at[8];
     d_work_ = dev_ints_ + at[9];
+    d_work_desc_ = dev_ints_ + at[10];
 }
 
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {
@@ -288,6 +314,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         at.max_run = max_run_;
         at.work = d_work_;
         at.num_work = num_work_;
+        at.work_desc = d_work_desc_;
         at.merge_counters = merge_counters_;
         hipEvent_t start = nullptr, stop = nullptr;
         if (timing_) {  // the kernel's own dispatch is timed (hipExtLaunchKernel), not the gap before it

@@ -92,8 +92,9 @@ private:
     bool fused_ = false;  // every sequence's new tokens form one run: append + attention in one launch
     const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
                   *d_run_first_ = nullptr, *d_run_count_ = nullptr, *d_tile_start_ = nullptr, *d_tile_end_ = nullptr,
-                  *d_tile_seq_ = nullptr, *d_work_ = nullptr;
-    std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, run_ctx_, tile_start_, tile_end_, tile_seq_, work_;
+                  *d_tile_seq_ = nullptr, *d_work_ = nullptr, *d_work_desc_ = nullptr;
+    std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, run_ctx_, tile_start_, tile_end_, tile_seq_, work_,
+        work_desc_;
     int num_work_ = 0;
 
     bool timing_ = false;

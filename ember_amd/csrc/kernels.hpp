@@ -35,4 +35,8 @@ hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
 // Row capacities with a built decode kernel, ascending.
 constexpr int kDecodeRowInstances[] = {1, 2, 4, 8, 10, 16};
 
+// The built row capacity that serves G query heads per kv head and runs of up
+// to max_run tokens; 0 if none does.
+int decode_rows(int G, int max_run);
+
 }  // namespace ember::hip

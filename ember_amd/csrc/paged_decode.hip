@@ -24,8 +24,8 @@
 //           holds (no cross-row traffic in the loop);
 //   values: each lane accumulates its 8 dims over its 4 keys.
 // Latency: block ids are wave-uniform scalar loads (they never wait on the
-// page loads), and each wave keeps the next two pages in flight in registers
-// while it works on the current one.
+// page loads), and each wave keeps its next page in flight in registers while
+// it works on the current one.
 // At the end: rows merge through two lane exchanges, waves through LDS, and
 // splits either in the separate merge kernel or, with merge counters, in the
 // last work-group of the (run, kv head) to finish - all in one fixed order.
@@ -57,9 +57,13 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 
+// A work item as the host plan describes it (EmberAttnArgs::work_desc): run,
+// split, first list entry, count, sequence, lowest position, highest position, 0.
+typedef int32_t WorkDesc __attribute__((ext_vector_type(8)));
+
 struct DecodeParams {
     const void *q, *k, *v;
-    const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count, *work;
+    const int32_t *positions, *token_seq, *tables, *token_index, *run_first, *run_count, *work, *work_desc;
     void *out;
     float *part_acc, *part_ml;
     uint32_t *counters;
@@ -336,9 +340,6 @@ __device__ __forceinline__ void phase_break() { __builtin_amdgcn_sched_barrier(0
 template <typename T, int ROWS, bool FUSED>
 __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
     constexpr int D = kHeadDim;
-    // Two pages in flight per wave while it works on a third, unless the
-    // query rows already need the registers.
-    constexpr int STAGES = ROWS <= 4 ? 3 : 2;
     constexpr int NEW = FUSED ? EMBER_MAX_RUN : 1;
     const int lane = static_cast<int>(threadIdx.x) % kWave;
     const int wave = uniform(static_cast<int>(threadIdx.x) / kWave);
@@ -346,11 +347,19 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     const int G = p.G;
 
     int run, kvh, split;
+    WorkDesc desc = {};
+    const bool have_desc = p.work && p.work_desc;
     if (p.work) {
         const int item = static_cast<int>(blockIdx.x) / p.n_kv;
         kvh = static_cast<int>(blockIdx.x) % p.n_kv;
-        run = uniform_load(p.work + 2 * item);
-        split = uniform_load(p.work + 2 * item + 1);
+        if (have_desc) {
+            desc = uniform_load(reinterpret_cast<const WorkDesc *>(p.work_desc) + item);  // one s_load_dwordx8
+            run = desc[0];
+            split = desc[1];
+        } else {
+            run = uniform_load(p.work + 2 * item);
+            split = uniform_load(p.work + 2 * item + 1);
+        }
         if (run < 0 || run >= p.num_runs || split < 0 || split >= p.num_splits) return;  // whole work-group
     } else {
         run = blockIdx.x;
@@ -368,14 +377,22 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     // (token i, head kvh * G + g) for row = i * G + g < nrows; rows nrows ..
     // ROWS - 1 repeat the last real row, so the page loop always computes ROWS
     // rows with no per-row tests (their results are never stored).
-    const int first = p.run_first ? uniform_load(p.run_first + run) : run;
-    int nq = p.run_count ? uniform_load(p.run_count + run) : 1;
+    const int first = have_desc ? desc[2] : p.run_first ? uniform_load(p.run_first + run) : run;
+    int nq = have_desc ? desc[3] : p.run_count ? uniform_load(p.run_count + run) : 1;
     nq = max(1, min(min(nq, ROWS / G), FUSED ? NEW : ROWS));  // FUSED: new_k / new_v hold NEW tokens
     const int nrows = nq * G;
     auto src_row = [&](int row) { return min(row, nrows - 1); };
-    const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
-    const int32_t *table = p.tables + static_cast<int64_t>(uniform_load(p.token_seq + t0)) * p.max_blocks;
+    int seq;
+    if (have_desc) {
+        seq = desc[4];
+    } else {
+        const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
+        seq = uniform_load(p.token_seq + t0);
+    }
+    const int32_t *table = p.tables + static_cast<int64_t>(seq) * p.max_blocks;
 
+    // Per-row positions (for masking and RoPE); the page range needs only the
+    // lowest and highest, which the descriptor already holds.
     int row_pos[ROWS];
     int min_pos = INT_MAX, max_pos = -1;
 #pragma unroll
@@ -385,6 +402,10 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         row_pos[row] = uniform_load(p.positions + t);
         min_pos = min(min_pos, row_pos[row]);
         max_pos = max(max_pos, row_pos[row]);
+    }
+    if (have_desc) {
+        min_pos = desc[5];
+        max_pos = desc[6];
     }
     const int ctx_max = min(max_pos + 1, p.max_blocks * kPage);
     const int begin = split * p.split_len;
@@ -435,7 +456,6 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
         }
         fetch(A, 0);
-        if constexpr (STAGES == 3) fetch(B, 1);
     } else {
         // q of every row and the new K/V in this split, one head vector per
         // wave at a time; lane l holds dims l and l + 64 (a rotary pair). The
@@ -458,7 +478,6 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
 
         fetch(A, 0);
-        if constexpr (STAGES == 3) fetch(B, 1);
 
         auto put_q = [&](int row, float x0, float x1, int pos) {
             const int head = kvh * G + row % G;
@@ -586,60 +605,37 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         process(pr, page, Masked{});
     };
 
+    // The page walk is a two-stage pipeline: each wave loads its next page
+    // while it computes on the current one. (At 115 VGPRs the kernel keeps
+    // four work-groups per CU, and 16 waves with one page in flight each
+    // stream as fast as 12 waves with two, which cost 32 more VGPRs.)
     // The wave's fast pages come first (pages below min_pos / 16 hold no new key
     // and only keys every row sees); they run through a loop with no masking.
-    // What is left is short: the loop stops with fewer than STAGES fast pages
-    // to go, and the run's positions (at most EMBER_MAX_RUN, consecutive) lie
-    // in at most two adjacent pages, of which a wave (stride 4 pages) gets at
-    // most one. So at most STAGES pages remain, already in flight or fetched
-    // once more, and they go through the masked path as straight-line code;
-    // the loop after it only serves runs that break that bound.
+    // What is left is short: the loop stops with at most one fast page to go,
+    // and the run's positions (at most EMBER_MAX_RUN, consecutive) lie in at
+    // most two adjacent pages, of which a wave (stride 4 pages) gets at most
+    // one. So at most two pages remain, one already in flight, and they go
+    // through the masked path as straight-line code; the loop after it only
+    // serves runs that break that bound.
     const int fast_end = min_pos / kPage;
     const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
     int j = 0;
-    if constexpr (STAGES == 3) {
-        // Two pages in flight while one is used: page j waits at vmcnt(16).
-        PageRegs<T> C;
-        for (; j + 3 <= n_fast; j += 3) {
-            fetch(C, j + 2);
-            phase_break();
-            process(A, page_of(j), Fast{});
-            phase_break();
-            fetch(A, j + 3);
-            phase_break();
-            process(B, page_of(j + 1), Fast{});
-            phase_break();
-            fetch(B, j + 4);
-            phase_break();
-            process(C, page_of(j + 2), Fast{});
-            phase_break();
-        }
-        fetch(C, j + 2);
-        phase_break();
-        if (j < n) consume(A, page_of(j));
-        phase_break();
-        if (j + 1 < n) consume(B, page_of(j + 1));
-        phase_break();
-        if (j + 2 < n) consume(C, page_of(j + 2));
-        j += 3;
-    } else {
-        for (; j + 2 <= n_fast; j += 2) {
-            fetch(B, j + 1);
-            phase_break();
-            process(A, page_of(j), Fast{});
-            phase_break();
-            fetch(A, j + 2);
-            phase_break();
-            process(B, page_of(j + 1), Fast{});
-            phase_break();
-        }
+    for (; j + 2 <= n_fast; j += 2) {
         fetch(B, j + 1);
         phase_break();
-        if (j < n) consume(A, page_of(j));
+        process(A, page_of(j), Fast{});
         phase_break();
-        if (j + 1 < n) consume(B, page_of(j + 1));
-        j += 2;
+        fetch(A, j + 2);
+        phase_break();
+        process(B, page_of(j + 1), Fast{});
+        phase_break();
     }
+    fetch(B, j + 1);
+    phase_break();
+    if (j < n) consume(A, page_of(j));
+    phase_break();
+    if (j + 1 < n) consume(B, page_of(j + 1));
+    j += 2;
     for (; j < n; j++) {
         fetch(A, j);
         consume(A, page_of(j));
@@ -771,6 +767,7 @@ DecodeParams params_of(const EmberAttnArgs &a) {
     p.run_first = a.run_first;
     p.run_count = a.run_count;
     p.work = a.work;
+    p.work_desc = a.work_desc;
     p.out = a.out;
     p.part_acc = a.part_acc;
     p.part_ml = a.part_ml;

@@ -151,7 +151,7 @@ def work_list(run_ctx, split_len: int) -> np.ndarray:
 
 def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list=None, runs=None,
                     split_len=512, num_splits=None, scratch=None, use_work_list=False, merge_in_kernel=False,
-                    stream=None):
+                    work_desc=True, stream=None):
     """Paged decode attention (≙ cuda::paged_attention).
 
     token_list: tokens to process (None = all). runs: (run_first, run_count) over
@@ -159,11 +159,12 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
     what the longest context needs at split_len keys per split. use_work_list:
     dispatch through a sorted (run, split) list instead of the dense grid.
     merge_in_kernel: merge the splits in the last work-group of each (run, kv
-    head) instead of a second launch.
+    head) instead of a second launch. work_desc: with the work list, also pass
+    the per-item descriptors the C++ plan uploads (EmberAttnArgs::work_desc).
     """
     a, keep = _attn_args(q, k_pool, v_pool, out, ints, n_heads=n_heads, n_kv=n_kv, token_list=token_list, runs=runs,
                          split_len=split_len, num_splits=num_splits, scratch=scratch, use_work_list=use_work_list,
-                         merge_in_kernel=merge_in_kernel)
+                         merge_in_kernel=merge_in_kernel, work_desc=work_desc)
     if a is None:
         return keep
     check(_lib.lib().ember_hip_paged_decode(a, _stream_handle(stream)), "paged_decode")
@@ -172,7 +173,7 @@ def paged_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, to
 
 def decode_step(qkv, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, inv_freq_dev, q_norm=None, k_norm=None,
                 bias=None, eps=1e-6, runs=None, split_len=512, num_splits=None, use_work_list=False,
-                merge_in_kernel=False, stream=None):
+                merge_in_kernel=False, work_desc=True, stream=None):
     """Append + attention in one launch (ember_hip_decode_step); every token of the step is listed, each
     sequence's tokens forming one run of consecutive positions."""
     T = ints.T
@@ -181,7 +182,7 @@ def decode_step(qkv, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, inv_
         raise EmberError("qkv does not match the step")
     a, keep = _attn_args(None, k_pool, v_pool, out, ints, n_heads=n_heads, n_kv=n_kv, token_list=None, runs=runs,
                          split_len=split_len, num_splits=num_splits, scratch=None, use_work_list=use_work_list,
-                         merge_in_kernel=merge_in_kernel, dtype_of=qkv)
+                         merge_in_kernel=merge_in_kernel, work_desc=work_desc, dtype_of=qkv)
     seqs = ints.token_seq.tolist()
     if runs is None and len(set(seqs)) != len(seqs):
         raise EmberError("a sequence with several tokens needs them as one run")
@@ -206,7 +207,7 @@ def decode_step(qkv, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, inv_
 
 
 def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_list, runs, split_len, num_splits,
-               scratch, use_work_list, merge_in_kernel, dtype_of=None):
+               scratch, use_work_list, merge_in_kernel, work_desc=True, dtype_of=None):
     tl = np.arange(ints.T, dtype=np.int32) if token_list is None else np.asarray(token_list, np.int32)
     n = int(tl.size)
     if n == 0:
@@ -257,6 +258,7 @@ def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_l
         a.run_first, a.run_count, a.num_runs, a.max_run = rf_dev.data_ptr(), rc_dev.data_ptr(), int(rf.size), int(rc.max())
         run_ctx = [int(ints.positions[tl[f:f + c]].max()) + 1 for f, c in zip(rf, rc)]
     else:
+        rf, rc = np.arange(n, dtype=np.int32), np.ones(n, np.int32)
         run_ctx = [int(ints.positions[t]) + 1 for t in tl]
     if use_work_list:
         items = work_list(run_ctx, split_len)
@@ -265,6 +267,15 @@ def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_l
         w_dev = _ints(items.reshape(-1), dev)
         keep.append(w_dev)
         a.work, a.num_work = w_dev.data_ptr(), int(items.shape[0])
+        if work_desc:
+            desc = np.zeros((items.shape[0], 8), np.int32)
+            for i, (r, sp) in enumerate(items.tolist()):
+                toks = tl[rf[r]:rf[r] + rc[r]]
+                desc[i, :7] = (r, sp, rf[r], rc[r], ints.token_seq[toks[0]], ints.positions[toks].min(),
+                               ints.positions[toks].max())
+            d_dev = _ints(desc.reshape(-1), dev)
+            keep.append(d_dev)
+            a.work_desc = d_dev.data_ptr()
     if merge_in_kernel:
         counters = torch.zeros(len(run_ctx) * n_kv, dtype=torch.int32, device=dev)
         keep.append(counters)

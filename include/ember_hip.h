@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 1
+#define EMBER_ABI_VERSION 2
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
@@ -113,6 +113,14 @@ typedef struct EmberAttnArgs {
      * the merge kernel, so no second launch is needed. NULL = a separate
      * merge kernel when num_splits > 1. */
     uint32_t *merge_counters;
+    /* Optional, with `work`: what the plan already knows of each item, 8 ints
+     * per item {run, split, run_first[run], run_count[run], sequence of the
+     * run, lowest position, highest position, 0}, [8 * num_work]. A
+     * work-group then reaches its first page load after one descriptor load
+     * and one block-table load, instead of the chain run -> run_first ->
+     * token_index -> token_seq / positions -> table. It must agree with the
+     * other arrays (not checked). NULL = looked up as above. */
+    const int32_t *work_desc;
 } EmberAttnArgs;
 
 /* Paged attention for short runs (decode, speculative verify): one work-group

@@ -141,15 +141,18 @@ def _run_decode(q, kp, vp, step, NB, device, **kw):
     return out
 
 
-@pytest.mark.parametrize("split_len,work", [(16, False), (64, True), (512, False), (512, True), (8192, False)])
+@pytest.mark.parametrize("split_len,work", [(16, False), (64, True), (512, False), (512, True), (512, "pairs"),
+                                            (8192, False)])
 def test_decode_f32_matches_oracle(rng, device, split_len, work):
+    """work: False = dense grid; True = sorted work list with the plan's per-item descriptors; "pairs" = the
+    work list alone (the kernel looks each item up)."""
     NB = 1200
     ctxs = [1, 15, 16, 17, 100, 511, 512, 513, 1500, 4096]
     step = make_step(rng, ctxs, [1] * len(ctxs), NB)
     k, v = _random_pools(rng, step, NB, f16=False)
     q = rng.standard_normal((step.T, H, D)).astype(np.float32)
     out = _run_decode(q, torch.from_numpy(k).to(device), torch.from_numpy(v).to(device), step, NB, device,
-                      split_len=split_len, use_work_list=work).cpu().numpy()
+                      split_len=split_len, use_work_list=bool(work), work_desc=work is True).cpu().numpy()
     want = oracle.attention_layer(q, step.positions, step.query_start, step.tables, np.nan_to_num(k), np.nan_to_num(v),
                                   n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=False, threads=8)
     assert np.isfinite(out).all()
