@@ -65,9 +65,13 @@ class Workload:
         self.bm = BlockManager(POOL_PAGES, False)
         every = [self.bm.allocate() for _ in range(POOL_PAGES)]
         self.bm.release_all([every[i] for i in rng.permutation(POOL_PAGES)])
-        self.blocks = [[] for _ in range(BATCH)]
+        # The engine's block tables, kept as one array and extended in place as pages are allocated.
+        self.tables = np.zeros((BATCH, self.max_blocks), np.int32)
+        self.n_blocks = [0] * BATCH
         for s in range(BATCH):
             self._ensure(s, int(self.ctx[s]))
+        self.tokens = np.zeros(BATCH, np.int32)
+        self.query_start = np.arange(BATCH + 1, dtype=np.int32)
         self.stream = torch.cuda.Stream()
         self.kv = PagedKv(n_layers=N_LAYERS, n_heads=H, n_kv_heads=KVH, rms_eps=1e-6, rope_theta=1e6,
                           max_position=self.max_blocks * PAGE, num_blocks=POOL_PAGES, max_batch_tokens=BATCH,
@@ -83,34 +87,40 @@ class Workload:
             self.kn = 1 + 0.1 * torch.randn((N_LAYERS, D), generator=g, device="cuda")
             self.out = torch.empty((BATCH, H, D), device="cuda", dtype=torch.float16)
         self.stream.synchronize()
+        # Per-layer device addresses, checked once here: the timed loop calls the C ABI directly, as a C++
+        # engine's layer loop would, without per-call Python tensor checks.
+        for t in (self.qkv, self.qn, self.kn, self.out):
+            assert t.is_cuda and t.is_contiguous()
+        self.layer_args = [(self.qkv[layer].data_ptr(), self.qn[layer].data_ptr(), self.kn[layer].data_ptr())
+                           for layer in range(N_LAYERS)]
         self.sum_ctx_timed = 0
         self.alloc_s = 0.0
 
     def _ensure(self, s: int, upto: int) -> None:
         need = (upto + PAGE - 1) // PAGE
-        while len(self.blocks[s]) < need:
+        while self.n_blocks[s] < need:
             b = self.bm.allocate()
             if b < 0:
                 raise RuntimeError("the page pool is exhausted")
-            self.blocks[s].append(b)
+            self.tables[s, self.n_blocks[s]] = b
+            self.n_blocks[s] += 1
 
     def step(self) -> int:
+        from ember_amd import _lib
         from ember_amd.paged_kv import StepBatch
 
         t0 = time.perf_counter()
         for s in range(BATCH):
             self._ensure(s, int(self.ctx[s]) + 1)
         self.alloc_s += time.perf_counter() - t0
-        tables = np.zeros((BATCH, self.max_blocks), np.int32)
-        for s in range(BATCH):
-            tables[s, :len(self.blocks[s])] = self.blocks[s]
         pos = self.ctx.astype(np.int32)
-        b = StepBatch(tokens=[0] * BATCH, positions=pos.tolist(), query_start=list(range(BATCH + 1)),
-                      context_len=(pos + 1).tolist(), block_tables=tables.reshape(-1).tolist(),
-                      max_blocks=self.max_blocks)
+        b = StepBatch(tokens=self.tokens, positions=pos, query_start=self.query_start, context_len=pos + 1,
+                      block_tables=self.tables.reshape(-1), max_blocks=self.max_blocks)
         self.kv.plan(b)
-        for layer in range(N_LAYERS):
-            self.kv.layer(layer, self.qkv[layer], self.out, q_norm=self.qn[layer], k_norm=self.kn[layer])
+        layer_fn, h, out = _lib.lib().ember_kv_layer, self.kv._h, self.out.data_ptr()
+        for layer, (qkv, qn, kn) in enumerate(self.layer_args):
+            if layer_fn(h, layer, qkv, qn, kn, None, out) != _lib.OK:
+                _lib.check(-1, "kv_layer")
         self.ctx += 1
         return int(pos.sum() + BATCH)  # sum of contexts after this step's append
 

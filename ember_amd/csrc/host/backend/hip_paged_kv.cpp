@@ -80,23 +80,35 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
                      static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) +
                      pad32(8 * T * max_splits_) + 64;
-    dev_ints_ = device_alloc<int32_t>(ints_capacity_);
     for (int i = 0; i < 2; i++) {
+        dev_ints_[i] = device_alloc<int32_t>(ints_capacity_);
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming));
+        EMBER_HIP_CHECK(hipEventCreateWithFlags(&consumed_[i], hipEventDisableTiming));
+    }
+    EMBER_HIP_CHECK(hipStreamCreateWithFlags(&upload_stream_, hipStreamNonBlocking));  // default priority
+    for (int i = 0; i < 2; i++) {  // every event starts out recorded, so the first plans wait on nothing pending
+        EMBER_HIP_CHECK(hipEventRecord(staged_[i], stream_));
+        EMBER_HIP_CHECK(hipEventRecord(consumed_[i], stream_));
     }
     EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
 HipPagedKv::~HipPagedKv() {
     (void)hipStreamSynchronize(stream_);
+    if (upload_stream_) {
+        (void)hipStreamSynchronize(upload_stream_);
+        (void)hipStreamDestroy(upload_stream_);
+    }
     for (hipEvent_t e : timing_events_) (void)hipEventDestroy(e);
     for (int i = 0; i < 2; i++) {
         if (staged_[i]) (void)hipEventDestroy(staged_[i]);
+        if (consumed_[i]) (void)hipEventDestroy(consumed_[i]);
         if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
+        if (dev_ints_[i]) (void)hipFree(dev_ints_[i]);
     }
     for (void *p : {k_, v_, q_, static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
-                    static_cast<void *>(part_ml_), static_cast<void *>(merge_counters_), static_cast<void *>(dev_ints_)})
+                    static_cast<void *>(part_ml_), static_cast<void *>(merge_counters_)})
         if (p) (void)hipFree(p);
 }
 
@@ -221,9 +233,13 @@ void HipPagedKv::plan(const StepBatch &b) {
     }
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.
+    // Everything enqueued on stream_ so far reads the previous plan's buffer;
+    // that buffer is reused two plans from now, after this event.
+    EMBER_HIP_CHECK(hipEventRecord(consumed_[stage_], stream_));
     stage_ ^= 1;
-    EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));
+    EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));  // its staging buffer is free again
     int32_t *hp = host_ints_[stage_];
+    int32_t *dp = dev_ints_[stage_];
     size_t off = 0;
     std::vector<size_t> at;
     auto put = [&](const int32_t *src, size_t n) {
@@ -243,19 +259,23 @@ void HipPagedKv::plan(const StepBatch &b) {
     put(work_.data(), work_.size());
     put(work_desc_.data(), work_desc_.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
-    EMBER_HIP_CHECK(hipMemcpyAsync(dev_ints_, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
-    EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], stream_));
-    d_positions_ = dev_ints_ + at[0];
-    d_token_seq_ = dev_ints_ + at[1];
-    d_tables_ = dev_ints_ + at[2];
-    d_decode_ = dev_ints_ + at[3];
-    d_run_first_ = dev_ints_ + at[4];
-    d_run_count_ = dev_ints_ + at[5];
-    d_tile_start_ = dev_ints_ + at[6];
-    d_tile_end_ = dev_ints_ + at[7];
-    d_tile_seq_ = dev_ints_ + at[8];
-    d_work_ = dev_ints_ + at[9];
-    d_work_desc_ = dev_ints_ + at[10];
+    // The copy waits for the kernels that last read this buffer (two plans ago),
+    // then runs beside stream_'s work; this step's kernels wait for the copy.
+    EMBER_HIP_CHECK(hipStreamWaitEvent(upload_stream_, consumed_[stage_], 0));
+    EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, upload_stream_));
+    EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], upload_stream_));
+    EMBER_HIP_CHECK(hipStreamWaitEvent(stream_, staged_[stage_], 0));
+    d_positions_ = dp + at[0];
+    d_token_seq_ = dp + at[1];
+    d_tables_ = dp + at[2];
+    d_decode_ = dp + at[3];
+    d_run_first_ = dp + at[4];
+    d_run_count_ = dp + at[5];
+    d_tile_start_ = dp + at[6];
+    d_tile_end_ = dp + at[7];
+    d_tile_seq_ = dp + at[8];
+    d_work_ = dp + at[9];
+    d_work_desc_ = dp + at[10];
 }
 
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {

@@ -81,13 +81,18 @@ private:
     void *k_ = nullptr, *v_ = nullptr, *q_ = nullptr;
     float *inv_freq_ = nullptr, *part_acc_ = nullptr, *part_ml_ = nullptr;
     uint32_t *merge_counters_ = nullptr;  // [max_batch_tokens * n_kv], zero between launches
-    int32_t *dev_ints_ = nullptr;   // this step's integers
-    int32_t *host_ints_[2] = {nullptr, nullptr};  // pinned staging, alternating
-    hipEvent_t staged_[2] = {nullptr, nullptr};   // the upload from each staging buffer has run
+    // A step's integers, double-buffered: plan() packs them into pinned staging
+    // and copies them up on upload_stream_, so the copy overlaps the previous
+    // step's kernels instead of sitting between the steps on stream_.
+    int32_t *dev_ints_[2] = {nullptr, nullptr};
+    int32_t *host_ints_[2] = {nullptr, nullptr};  // pinned staging, alternating with dev_ints_
+    hipEvent_t staged_[2] = {nullptr, nullptr};   // the upload into each buffer has run
+    hipEvent_t consumed_[2] = {nullptr, nullptr}; // the kernels that read each buffer have run
+    hipStream_t upload_stream_ = nullptr;
     int stage_ = 0;
     size_t ints_capacity_ = 0;
 
-    // The current plan (device addresses into dev_ints_).
+    // The current plan (device addresses into dev_ints_[stage_]).
     int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;
     bool fused_ = false;  // every sequence's new tokens form one run: append + attention in one launch
     const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
