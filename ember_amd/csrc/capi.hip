@@ -158,8 +158,7 @@ int ember_hip_prefill_attn(const EmberPrefillArgs *a, void *stream) {
     if (!a) return set_error(EMBER_ERR_INVALID, "prefill_attn: null arguments");
     if (int e = check_heads("prefill_attn", a->head_dim, a->n_heads, a->n_kv)) return e;
     const int G = a->n_heads / a->n_kv;
-    if (G > 4) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1, 2 or 4 (got %d)", G);
-    if (G == 3) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1, 2 or 4 (got 3)");
+    if (G > 8) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1..8 (got %d)", G);
     if (a->dtype != EMBER_DTYPE_F16) return set_error(EMBER_ERR_INVALID, "prefill_attn: the MFMA path takes f16 only");
     if (a->num_tiles < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
         return set_error(EMBER_ERR_INVALID, "prefill_attn: bad sizes");

@@ -162,7 +162,7 @@ void HipPagedKv::plan(const StepBatch &b) {
         for (int p = 0; p * kBlockSize < ctx; p++)
             EMBER_CHECK(row[p] >= 0 && row[p] <= opt_.num_blocks, "sequence {} page {} names block {} (pool of {})", s, p,
                         row[p], opt_.num_blocks);
-        if (q1 - q0 >= kFlashMinTokens && opt_.use_prefill_kernel) {
+        if (q1 - q0 >= kFlashMinTokens && opt_.use_prefill_kernel && opt_.dtype == EMBER_DTYPE_F16) {
             for (int t = q0; t < q1; t += EMBER_PREFILL_TILE) {
                 tile_start_.push_back(t);
                 tile_end_.push_back(std::min(q1, t + EMBER_PREFILL_TILE));

@@ -9,9 +9,9 @@
 // Pools are zeroed at creation, so slots never written read as 0.
 //
 // Routing: a sequence with >= 16 new tokens goes to 64-token MFMA prefill
-// tiles when that kernel is available; every other run is cut into runs of at
-// most 8 tokens for the paged decode kernel, which reads each page once per
-// run. Decode splits are fixed 512-key chunks ([0, 512), [512, 1024), ...)
+// tiles (f16 pools: the MFMA path); every other run, and every run of an f32
+// pool, is cut into runs of at most 8 tokens for the paged decode kernel,
+// which reads each page once per run. Decode splits are fixed 512-key chunks ([0, 512), [512, 1024), ...)
 // at every batch size, so a token's result never depends on its batch.
 #pragma once
 
@@ -32,7 +32,7 @@ struct PagedKvOptions {
     int max_seqs = 64;
     int dtype = EMBER_DTYPE_F16;
     int split_len = 512;
-    bool use_prefill_kernel = false;  // route runs of >= 16 tokens to MFMA tiles
+    bool use_prefill_kernel = true;   // route runs of >= 16 tokens to MFMA tiles (f16 pools; f32 always decodes)
 };
 
 class HipPagedKv {

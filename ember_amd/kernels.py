@@ -17,7 +17,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import BLOCK_SIZE, MAX_RUN, AttnArgs, CopyArgs, EmberError, PrefillArgs, QkvArgs, check
+from ._lib import BLOCK_SIZE, MAX_RUN, PREFILL_TILE, AttnArgs, CopyArgs, EmberError, PrefillArgs, QkvArgs, check
 
 HEAD_DIM = 128
 
@@ -281,6 +281,41 @@ def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_l
         keep.append(counters)
         a.merge_counters = counters.data_ptr()
     return a, keep
+
+
+def prefill_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, tiles, stream=None):
+    """Causal prefill attention of query tiles on MFMA (≙ cuda::prefill_attention).
+
+    tiles: (start, end, seq) triples, each up to PREFILL_TILE consecutive tokens start..end-1 of
+    sequence seq; every token attends to its sequence's keys 0..its position, which must already be in
+    the pools. f16 only.
+    """
+    if not tiles:
+        return []
+    t = np.asarray(tiles, np.int32).reshape(-1, 3)
+    if (t[:, 1] <= t[:, 0]).any() or (t[:, 1] - t[:, 0] > PREFILL_TILE).any() or t[:, 0].min() < 0 \
+            or t[:, 1].max() > ints.T:
+        raise EmberError("malformed tiles")
+    for s0, e0, sq in t.tolist():
+        if (ints.token_seq[s0:e0] != sq).any():
+            raise EmberError("a tile spans tokens of another sequence")
+    if q.numel() < ints.T * n_heads * HEAD_DIM or out.numel() < ints.T * n_heads * HEAD_DIM:
+        raise EmberError("q / out are smaller than the step")
+    if k_pool.numel() < ints.num_blocks * n_kv * BLOCK_SIZE * HEAD_DIM:
+        raise EmberError("pools are smaller than num_blocks pages")
+    dev = k_pool.device
+    pos, seq, tab = ints.device(dev)
+    ts, te, tq = (_ints(np.ascontiguousarray(t[:, i]), dev) for i in range(3))
+    a = PrefillArgs()
+    a.q, a.k_cache, a.v_cache = _dev(q, "q"), _dev(k_pool, "k_pool"), _dev(v_pool, "v_pool")
+    a.tile_start, a.tile_end, a.tile_seq = ts.data_ptr(), te.data_ptr(), tq.data_ptr()
+    a.positions, a.block_tables = pos.data_ptr(), tab.data_ptr()
+    a.num_tiles, a.max_blocks, a.n_heads, a.n_kv, a.head_dim = int(t.shape[0]), ints.max_blocks, n_heads, n_kv, HEAD_DIM
+    a.scale = 1.0 / math.sqrt(HEAD_DIM)
+    a.out = _dev(out, "out")
+    a.num_blocks, a.dtype = ints.num_blocks, _dtype_code(q)
+    check(_lib.lib().ember_hip_prefill_attn(a, _stream_handle(stream)), "prefill_attn")
+    return [ts, te, tq]
 
 
 def copy_pages(k_pool, v_pool, src, dst, *, n_layers, layer_stride, n_kv, num_blocks, stream=None):

@@ -159,9 +159,12 @@ typedef struct EmberPrefillArgs {
     int32_t dtype;                /* must be EMBER_DTYPE_F16 (MFMA path) */
 } EmberPrefillArgs;
 
-/* Causal attention of 64-token query tiles over the paged cache on MFMA
- * (v_mfma_f32_32x32x16_f16), all G query heads of a kv head per work-group.
- * Replaces cuda::prefill_attention (kernels.cuh:120; k_attention.cu:390-399). */
+/* Causal attention of query tiles (up to 64 consecutive tokens of one
+ * sequence, each attending to keys 0..its position) over the paged cache on
+ * MFMA (v_mfma_f32_16x16x32_f16), two query heads of a kv head per work-group
+ * (one when G is odd), so a K/V block is read once for both. f16 only; head_dim
+ * 128, G 1..8. Replaces cuda::prefill_attention (kernels.cuh:120;
+ * k_attention.cu:390-399). */
 int ember_hip_prefill_attn(const EmberPrefillArgs *args, void *stream);
 
 /* No counterpart in the reference: the device half of copy-on-write. */

@@ -337,3 +337,68 @@ def test_in_kernel_merge_leaves_counters_zero_and_matches(rng, device):
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy().view(np.uint16), two)
         assert int(keep[-1].abs().sum()) == 0, "merge counters not reset"
+
+
+# ---- MFMA prefill tiles ----
+
+def _tiles_of(step, tile=64):
+    """Each sequence's new tokens cut into tiles of up to `tile` consecutive tokens."""
+    out = []
+    for s in range(step.S):
+        for a in range(int(step.query_start[s]), int(step.query_start[s + 1]), tile):
+            out.append((a, min(a + tile, int(step.query_start[s + 1])), s))
+    return out
+
+
+@pytest.mark.parametrize("n_kv", [8, 16, 4])
+def test_prefill_matches_oracle(rng, device, n_kv):
+    """Chunked-prefill tiles on MFMA (causal within the chunk, over cached context before it) against the
+    f32 CPU path on the same f16 inputs and a float64 textbook reference: within 2e-3. G = 2, 1, 4."""
+    NB = 1500
+    ctxs = [16, 64, 65, 100, 700, 1040, 2000, 17]
+    new = [16, 64, 65, 100, 128, 16, 64, 17]  # the chunk: positions ctx - new .. ctx - 1
+    step = make_step(rng, ctxs, new, NB)
+    k = np.full((NB, n_kv, PAGE, D), np.nan, np.float32)
+    v = k.copy()
+    for s, c in enumerate(ctxs):
+        for p0 in range(0, c, PAGE):
+            n = min(PAGE, c - p0)
+            k[step.tables[s, p0 // PAGE], :, :n] = rng.standard_normal((n_kv, n, D)) * 0.35
+            v[step.tables[s, p0 // PAGE], :, :n] = rng.standard_normal((n_kv, n, D))
+    k16, v16 = k.astype(np.float16), v.astype(np.float16)
+    q16 = rng.standard_normal((step.T, H, D)).astype(np.float16)
+    out = torch.full((step.T, H, D), float("nan"), dtype=torch.float16, device=device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    K.prefill_attention(torch.from_numpy(q16).to(device), torch.from_numpy(k16).to(device),
+                        torch.from_numpy(v16).to(device), out, ints, n_heads=H, n_kv=n_kv, tiles=_tiles_of(step))
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    kf, vf = np.nan_to_num(k16.astype(np.float32)), np.nan_to_num(v16.astype(np.float32))
+    want = oracle.attention_layer(q16.astype(np.float32), step.positions, step.query_start, step.tables, kf, vf,
+                                  n_heads=H, n_kv=n_kv, num_blocks=NB, kv_f16=False, threads=8)
+    assert rel_err(got, want) < 2e-3
+    assert rel_err(got, attention_f64(q16.astype(np.float32), step, kf, vf, H, n_kv)) < 2e-3
+
+
+def test_prefill_tile_is_independent_of_its_neighbours(rng, device):
+    """A tile's output is bit-identical launched alone or with other tiles, and tokens past a tile's end
+    are not written."""
+    NB = 400
+    step = make_step(rng, [300, 130], [100, 70], NB)
+    k, v = _random_pools(rng, step, NB, f16=True)
+    kp, vp = torch.from_numpy(np.nan_to_num(k)).to(device), torch.from_numpy(np.nan_to_num(v)).to(device)
+    q = torch.from_numpy(rng.standard_normal((step.T, H, D)).astype(np.float16)).to(device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    tiles = _tiles_of(step)
+    both = torch.full((step.T, H, D), float("nan"), dtype=torch.float16, device=device)
+    K.prefill_attention(q, kp, vp, both, ints, n_heads=H, n_kv=KVH, tiles=tiles)
+    for t in tiles:
+        one = torch.full((step.T, H, D), float("nan"), dtype=torch.float16, device=device)
+        K.prefill_attention(q, kp, vp, one, ints, n_heads=H, n_kv=KVH, tiles=[t])
+        torch.cuda.synchronize()
+        a, b = one.cpu().numpy().view(np.uint16), both.cpu().numpy().view(np.uint16)
+        assert np.array_equal(a[t[0]:t[1]], b[t[0]:t[1]])
+        rest = np.ones(step.T, bool)
+        rest[t[0]:t[1]] = False
+        assert np.isnan(one.float().cpu().numpy()[rest]).all(), "a tile wrote outside its tokens"
