@@ -83,7 +83,11 @@ class StepBatchC(ctypes.Structure):
     ]
 
 
-STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC]
+class LayerIo(ctypes.Structure):
+    _fields_ = [("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("bias", c_void_p), ("out", c_void_p)]
+
+
+STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, LayerIo]
 
 # name -> (restype, argtypes); every extern "C" symbol of include/ember_hip.h.
 PROTOTYPES = {
@@ -119,6 +123,7 @@ PROTOTYPES = {
     "ember_kv_destroy": (None, [c_void_p]),
     "ember_kv_plan": (c_int32, [c_void_p, POINTER(StepBatchC)]),
     "ember_kv_layer": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ember_kv_decode_graph": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(LayerIo), c_int32]),
     "ember_kv_copy_blocks": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), c_int32]),
     "ember_kv_k_pool": (c_void_p, [c_void_p, c_int32]),
     "ember_kv_v_pool": (c_void_p, [c_void_p, c_int32]),

@@ -61,6 +61,7 @@ int32_t ember_hip_sizeof(int32_t which) {
         case 3: return sizeof(EmberCopyArgs);
         case 4: return sizeof(EmberKvConfig);
         case 5: return sizeof(EmberStepBatch);
+        case 6: return sizeof(EmberLayerIo);
         default: return -1;
     }
 }

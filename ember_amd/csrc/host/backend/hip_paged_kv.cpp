@@ -96,6 +96,8 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
 
 HipPagedKv::~HipPagedKv() {
     (void)hipStreamSynchronize(stream_);
+    for (auto &[key, g] : graphs_) (void)hipGraphExecDestroy(g.exec);
+    if (capture_stream_) (void)hipStreamDestroy(capture_stream_);
     if (upload_stream_) {
         (void)hipStreamSynchronize(upload_stream_);
         (void)hipStreamDestroy(upload_stream_);
@@ -122,7 +124,7 @@ void *HipPagedKv::v_pool(int layer) const {
     return static_cast<char *>(v_) + static_cast<size_t>(layer) * layer_elems_ * elem_;
 }
 
-void HipPagedKv::plan(const StepBatch &b) {
+void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     const int T = b.num_tokens(), S = b.num_seqs();
     EMBER_CHECK(T > 0 && T <= opt_.max_batch_tokens, "batch of {} tokens (limit {})", T, opt_.max_batch_tokens);
     EMBER_CHECK(S > 0 && S <= opt_.max_seqs, "batch of {} sequences (limit {})", S, opt_.max_seqs);
@@ -188,7 +190,7 @@ void HipPagedKv::plan(const StepBatch &b) {
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
     fused_ = fused_ && tiles_ == 0 && decode_count_ == T;
-    splits_ = std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
+    splits_ = graph_splits > 0 ? graph_splits : std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
 
     // Decode work items (run, split), dispatched in list order: every full
     // split first, then the partial last splits, longest first, so the short
@@ -209,12 +211,20 @@ void HipPagedKv::plan(const StepBatch &b) {
         work_.push_back(r);
         work_.push_back(run_ctx_[static_cast<size_t>(r)] / opt_.split_len);
     }
+    if (graph_splits > 0) {  // the graph's fixed-length list: padding items name no run
+        EMBER_CHECK(static_cast<int>(work_.size() / 2) <= decode_runs_ * graph_splits, "internal: graph work list");
+        work_.resize(2 * static_cast<size_t>(decode_runs_) * graph_splits, -1);
+    }
     num_work_ = static_cast<int>(work_.size() / 2);
     // The kernel's view of each item (EmberAttnArgs::work_desc): everything it
     // would otherwise look up in a chain before its first page load.
     work_desc_.assign(static_cast<size_t>(num_work_) * 8, 0);
     for (int i = 0; i < num_work_; i++) {
         const int r = work_[2 * static_cast<size_t>(i)];
+        if (r < 0) {
+            work_desc_[8 * static_cast<size_t>(i)] = -1;
+            continue;
+        }
         const int first = run_first_[static_cast<size_t>(r)], count = run_count_[static_cast<size_t>(r)];
         int lo = INT32_MAX, hi = -1;
         for (int k = 0; k < count; k++) {
@@ -385,6 +395,98 @@ int HipPagedKv::collect_timing(double *total_ms) {
     timing_used_ = 0;
     if (total_ms) *total_ms = ms;
     return launches;
+}
+
+int HipPagedKv::token_bucket(int T) {
+    static const int buckets[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 40, 48, 56, 64};
+    for (int b : buckets)
+        if (T <= b) return b;
+    return kGraphMaxTokens;
+}
+
+int HipPagedKv::width_bucket(int w) const {
+    int b = 16;
+    while (b < w) b *= 4;
+    return std::min(b, max_blocks_per_seq_);
+}
+
+bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
+    const int T = b.num_tokens(), S = b.num_seqs();
+    if (T < 1 || T > kGraphMaxTokens || S != T || static_cast<int>(b.query_start.size()) != S + 1) return false;
+    for (int s = 0; s <= S; s++)
+        if (b.query_start[static_cast<size_t>(s)] != s) return false;  // one new token per sequence
+    const int TB = token_bucket(T), WB = width_bucket(std::max(b.max_blocks, 1));
+    if (TB > opt_.max_batch_tokens || TB > opt_.max_seqs || b.max_blocks > WB) return false;
+    EMBER_CHECK(static_cast<int>(io.size()) == cfg_.n_layers, "decode_graph: {} layer buffers for {} layers", io.size(),
+                cfg_.n_layers);
+    EMBER_CHECK(!timing_, "decode_graph: kernel timing is not available inside a graph");
+    EMBER_CHECK(static_cast<int64_t>(b.block_tables.size()) == static_cast<int64_t>(S) * b.max_blocks &&
+                    static_cast<int>(b.positions.size()) == T,
+                "decode_graph: malformed batch");
+
+    // The padded step: real rows keep their table and continue with the spare
+    // block; padding rows are sequences of one token at position 0 whose whole
+    // table is the spare block.
+    StepBatch p;
+    p.max_blocks = WB;
+    p.tokens.assign(static_cast<size_t>(TB), 0);
+    p.positions.assign(static_cast<size_t>(TB), 0);
+    p.query_start.resize(static_cast<size_t>(TB) + 1);
+    p.context_len.assign(static_cast<size_t>(TB), 1);
+    p.block_tables.assign(static_cast<size_t>(TB) * WB, spare_block());
+    for (int t = 0; t <= TB; t++) p.query_start[static_cast<size_t>(t)] = t;
+    for (int t = 0; t < T; t++) {
+        p.tokens[static_cast<size_t>(t)] = b.tokens.empty() ? 0 : b.tokens[static_cast<size_t>(t)];
+        p.positions[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)];
+        p.context_len[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)] + 1;
+        std::copy_n(b.block_tables.begin() + static_cast<ptrdiff_t>(t) * b.max_blocks, b.max_blocks,
+                    p.block_tables.begin() + static_cast<ptrdiff_t>(t) * WB);
+    }
+    const int splits = (WB * kBlockSize + opt_.split_len - 1) / opt_.split_len;
+    plan(p, splits);
+
+    const uint64_t key = (static_cast<uint64_t>(TB) << 33) | (static_cast<uint64_t>(WB) << 1) | static_cast<uint64_t>(stage_);
+    auto it = graphs_.find(key);
+    auto same_io = [&](const std::vector<LayerIo> &kept) {
+        for (size_t l = 0; l < io.size(); l++)
+            if (std::memcmp(&kept[l], &io[l], sizeof(LayerIo)) != 0) return false;
+        return true;
+    };
+    if (it == graphs_.end() || !same_io(it->second.io)) {
+        if (it != graphs_.end()) {
+            EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
+            (void)hipGraphExecDestroy(it->second.exec);
+            graphs_.erase(it);
+        }
+        GraphEntry e;
+        e.io.assign(io.begin(), io.end());
+        // Capture on a private stream (the path's stream may be the legacy null
+        // stream, which cannot capture); the graph is launched on stream_.
+        if (!capture_stream_) EMBER_HIP_CHECK(hipStreamCreateWithFlags(&capture_stream_, hipStreamNonBlocking));
+        hipGraph_t graph = nullptr;
+        const hipStream_t path_stream = stream_;
+        EMBER_HIP_CHECK(hipStreamBeginCapture(capture_stream_, hipStreamCaptureModeThreadLocal));
+        stream_ = capture_stream_;
+        try {
+            for (int l = 0; l < cfg_.n_layers; l++) {
+                const LayerIo &x = io[static_cast<size_t>(l)];
+                layer(l, x.qkv, x.q_norm, x.k_norm, x.bias, x.out);
+            }
+        } catch (...) {
+            stream_ = path_stream;
+            (void)hipStreamEndCapture(capture_stream_, &graph);
+            if (graph) (void)hipGraphDestroy(graph);
+            throw;
+        }
+        stream_ = path_stream;
+        EMBER_HIP_CHECK(hipStreamEndCapture(capture_stream_, &graph));
+        const hipError_t inst = hipGraphInstantiate(&e.exec, graph, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(graph);
+        EMBER_HIP_CHECK(inst);
+        it = graphs_.emplace(key, std::move(e)).first;
+    }
+    EMBER_HIP_CHECK(hipGraphLaunch(it->second.exec, stream_));
+    return true;
 }
 
 void HipPagedKv::copy_blocks(std::span<const int32_t> src, std::span<const int32_t> dst) {

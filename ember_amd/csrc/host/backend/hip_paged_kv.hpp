@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <map>
 #include <span>
 #include <vector>
 
@@ -45,10 +46,30 @@ public:
     HipPagedKv &operator=(const HipPagedKv &) = delete;
 
     // Packs and uploads the step's integers and decides the launches.
-    void plan(const StepBatch &b);
+    void plan(const StepBatch &b) { plan(b, 0); }
     // Layer `layer` of the planned step: K/V of every new token into the
     // pools, then attention of every token into out [T, n_heads, head_dim].
     void layer(int layer, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out);
+    // Per-layer buffers of a captured decode step.
+    struct LayerIo {
+        const void *qkv;
+        const float *q_norm, *k_norm, *bias;
+        void *out;
+    };
+    static constexpr int kGraphMaxTokens = 64;
+    // A pure decode step (every sequence one new token, at most 64) as one
+    // replayed hipGraph of all layers' launches (cuda_backend.cu:376-454): the
+    // step is padded to a token bucket and a block-table width bucket, padding
+    // tokens are sequences of length 1 at position 0 on the spare block, and the
+    // splits follow the width bucket, so a replay always matches its capture.
+    // qkv and out of every layer must hold token_bucket(T) rows (64 suffice);
+    // rows past T are padding. Graphs are kept per (bucket pair, staging buffer)
+    // and captured again when the layer buffers change. Returns false, with
+    // nothing enqueued, when the step is not a pure decode step of <= 64 tokens.
+    bool decode_graph(const StepBatch &b, std::span<const LayerIo> io);
+    static int token_bucket(int T);
+    int width_bucket(int w) const;
+
     // Device copies of whole pages, src[i] -> dst[i], all layers, K and V.
     void copy_blocks(std::span<const int32_t> src, std::span<const int32_t> dst);
 
@@ -68,7 +89,17 @@ public:
     int collect_timing(double *total_ms);
 
 private:
-    int32_t *upload(size_t count);  // copies host_ints_[0, count) to the device, returns its device address
+    // graph_splits > 0: a graph step's plan, with num_splits fixed to it and the
+    // work list padded to T * graph_splits items (padding items do nothing), so
+    // every array has the same size for the same buckets.
+    void plan(const StepBatch &b, int graph_splits);
+
+    struct GraphEntry {
+        hipGraphExec_t exec = nullptr;
+        std::vector<LayerIo> io;
+    };
+    std::map<uint64_t, GraphEntry> graphs_;
+    hipStream_t capture_stream_ = nullptr;  // graphs are captured here (the path's stream may be the null stream)
 
     ModelConfig cfg_;
     PagedKvOptions opt_;

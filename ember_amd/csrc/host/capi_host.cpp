@@ -169,19 +169,36 @@ EmberPagedKv *ember_kv_create(const EmberKvConfig *cfg, void *stream) {
 
 void ember_kv_destroy(EmberPagedKv *h) { delete h; }
 
+static ember::StepBatch step_batch(const EmberStepBatch *b) {
+    EMBER_CHECK(b && b->num_tokens > 0 && b->num_seqs > 0 && b->max_blocks > 0, "empty or malformed batch");
+    ember::StepBatch sb;
+    const size_t T = static_cast<size_t>(b->num_tokens), S = static_cast<size_t>(b->num_seqs);
+    sb.tokens.assign(b->tokens, b->tokens + T);
+    sb.positions.assign(b->positions, b->positions + T);
+    sb.query_start.assign(b->query_start, b->query_start + S + 1);
+    sb.context_len.assign(b->context_len, b->context_len + S);
+    sb.max_blocks = b->max_blocks;
+    sb.block_tables.assign(b->block_tables, b->block_tables + S * static_cast<size_t>(b->max_blocks));
+    return sb;
+}
+
 int32_t ember_kv_plan(EmberPagedKv *h, const EmberStepBatch *b) {
     return guarded("kv_plan", [&] {
-        EMBER_CHECK(b && b->num_tokens > 0 && b->num_seqs > 0 && b->max_blocks > 0, "empty or malformed batch");
-        ember::StepBatch sb;
-        const size_t T = static_cast<size_t>(b->num_tokens), S = static_cast<size_t>(b->num_seqs);
-        sb.tokens.assign(b->tokens, b->tokens + T);
-        sb.positions.assign(b->positions, b->positions + T);
-        sb.query_start.assign(b->query_start, b->query_start + S + 1);
-        sb.context_len.assign(b->context_len, b->context_len + S);
-        sb.max_blocks = b->max_blocks;
-        sb.block_tables.assign(b->block_tables, b->block_tables + S * static_cast<size_t>(b->max_blocks));
-        h->kv.plan(sb);
+        h->kv.plan(step_batch(b));
         return EMBER_OK;
+    });
+}
+
+int32_t ember_kv_decode_graph(EmberPagedKv *h, const EmberStepBatch *b, const EmberLayerIo *layers, int32_t n_layers) {
+    return guarded("kv_decode_graph", [&] {
+        EMBER_CHECK(layers && n_layers > 0, "no layer buffers");
+        std::vector<ember::HipPagedKv::LayerIo> io(static_cast<size_t>(n_layers));
+        for (int l = 0; l < n_layers; l++) {
+            const EmberLayerIo &x = layers[l];
+            EMBER_CHECK(x.qkv && x.out, "layer {}: null qkv or out", l);
+            io[static_cast<size_t>(l)] = {x.qkv, x.q_norm, x.k_norm, x.bias, x.out};
+        }
+        return h->kv.decode_graph(step_batch(b), io) ? EMBER_OK : 1;
     });
 }
 

@@ -66,12 +66,33 @@ class PagedKv:
     def __del__(self):
         self.close()
 
-    def plan(self, b: StepBatch) -> None:
+    @staticmethod
+    def _batch(b: StepBatch):
         arrs = [_arr(b.tokens), _arr(b.positions), _arr(b.query_start), _arr(b.context_len), _arr(b.block_tables)]
         sb = StepBatchC()
         sb.tokens, sb.positions, sb.query_start, sb.context_len, sb.block_tables = (a.ctypes.data for a in arrs)
         sb.num_tokens, sb.num_seqs, sb.max_blocks = len(b.tokens), len(b.context_len), b.max_blocks
+        return sb, arrs
+
+    def plan(self, b: StepBatch) -> None:
+        sb, _keep = self._batch(b)
         check(_lib.lib().ember_kv_plan(self._h, sb), "kv_plan")
+
+    def decode_graph(self, b: StepBatch, layers) -> bool:
+        """A pure decode step of <= 64 tokens, planned and run for every layer as one replayed hipGraph.
+        layers: per layer (qkv, out, q_norm, k_norm, bias) device tensors (or None for the optional ones),
+        qkv and out holding token_bucket(T) rows; they must stay the same between steps to reuse a graph.
+        Returns False (nothing enqueued) when the step does not qualify."""
+        sb, _keep = self._batch(b)
+        io = (_lib.LayerIo * len(layers))()
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        for i, (qkv, out, qn, kn, bias) in enumerate(layers):
+            io[i].qkv, io[i].out, io[i].q_norm, io[i].k_norm, io[i].bias = ptr(qkv), ptr(out), ptr(qn), ptr(kn), ptr(bias)
+        code = _lib.lib().ember_kv_decode_graph(self._h, sb, io, len(layers))
+        if code == 1:
+            return False
+        check(code, "kv_decode_graph")
+        return True
 
     def layer(self, layer: int, qkv: torch.Tensor, out: torch.Tensor, q_norm=None, k_norm=None, bias=None) -> None:
         for t in (qkv, out):

@@ -188,7 +188,7 @@ const char *ember_hip_last_error(void);
 int ember_hip_abi_version(void);
 /* sizeof of each argument struct, for FFI bindings to check their layouts:
  * 0 EmberQkvArgs, 1 EmberAttnArgs, 2 EmberPrefillArgs, 3 EmberCopyArgs,
- * 4 EmberKvConfig, 5 EmberStepBatch; -1 otherwise. */
+ * 4 EmberKvConfig, 5 EmberStepBatch, 6 EmberLayerIo; -1 otherwise. */
 int32_t ember_hip_sizeof(int32_t which);
 
 /* ---- 2. KV block manager ------------------------------------------------- */
@@ -272,6 +272,27 @@ int32_t ember_kv_plan(EmberPagedKv *kv, const EmberStepBatch *batch);
  * for every token into out [num_tokens, n_heads, head_dim] (cuda_backend.cu:357-361). */
 int32_t ember_kv_layer(EmberPagedKv *kv, int32_t layer, const void *qkv, const float *q_norm, const float *k_norm,
                        const float *bias, void *out);
+/* One layer's buffers for a decode step replayed as a graph. */
+typedef struct EmberLayerIo {
+    const void *qkv;              /* [token_bucket(T), (n_heads + 2 * n_kv) * head_dim]; rows past T are padding */
+    const float *q_norm, *k_norm; /* [head_dim], or NULL */
+    const float *bias;            /* or NULL */
+    void *out;                    /* [token_bucket(T), n_heads, head_dim] */
+} EmberLayerIo;
+
+/* A pure decode step (every sequence one new token, at most 64 tokens) planned
+ * and run for all n_layers layers as one replayed hipGraph, as the reference's
+ * decode graphs do (src/backend/cuda/cuda_backend.cu:376-454). The step is
+ * padded to a token bucket {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 40, 48, 56, 64}
+ * and a block-table width bucket (16 * 4^k blocks); padding tokens are
+ * sequences of one token at position 0 whose table is the spare block, so they
+ * write only there, and the splits follow the width bucket. Graphs are kept per
+ * bucket pair and captured again when the layer buffers change; the buffers
+ * must hold token_bucket(T) rows (64 suffice). Results equal plan + layer
+ * bit for bit. Returns EMBER_OK, 1 when the step does not qualify (nothing was
+ * enqueued: use ember_kv_plan + ember_kv_layer), or an error. */
+int32_t ember_kv_decode_graph(EmberPagedKv *kv, const EmberStepBatch *batch, const EmberLayerIo *layers,
+                              int32_t n_layers);
 /* Device copies of whole pages, src[i] -> dst[i] (host arrays of n blocks), all layers. */
 int32_t ember_kv_copy_blocks(EmberPagedKv *kv, const int32_t *src, const int32_t *dst, int32_t n);
 void *ember_kv_k_pool(EmberPagedKv *kv, int32_t layer);

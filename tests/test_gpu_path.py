@@ -254,3 +254,62 @@ def test_fork_copy_on_write(rng, device, dtype):
     for blocks in seqs:
         bm.release_all(blocks)
     assert bm.check() == "" and bm.used() == 0 and bm.cached() == 4
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
+    """Decode steps run as replayed hipGraphs (padded to a token bucket and a block-table width bucket,
+    padding tokens on the spare block) leave the same outputs and pools, to the bit, as plan + layer: the
+    same graph replayed step after step with eager work in between, and new graphs when the batch moves
+    to another bucket. Only the spare block differs (the padding writes there and nowhere else)."""
+    L, NB, maxpos = 2, 700, 2048
+    mk = lambda: PagedKv(n_layers=L, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,  # noqa: E731
+                         max_position=maxpos, num_blocks=NB, max_batch_tokens=64, max_seqs=64, dtype=dtype)
+    ga, eb = mk(), mk()
+    qn = [torch.from_numpy((1 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(device) for _ in range(L)]
+    kn = [torch.from_numpy((1 + 0.1 * rng.standard_normal(D)).astype(np.float32)).to(device) for _ in range(L)]
+    qkv = [torch.zeros((64, W), dtype=dtype, device=device) for _ in range(L)]  # fixed buffers: graphs keep them
+    out_g = [torch.zeros((64, H, D), dtype=dtype, device=device) for _ in range(L)]
+    out_e = [torch.zeros((64, H, D), dtype=dtype, device=device) for _ in range(L)]
+    io = [(qkv[l], out_g[l], qn[l], kn[l], None) for l in range(L)]
+    ctx = [int(c) for c in rng.integers(1, 240, 9)]  # tokens cached per sequence
+    blocks = [[] for _ in ctx]
+    free = list(rng.permutation(NB))
+    # active sequences per step: same bucket (replays), then 7 -> bucket 8, 3 -> bucket 3; contexts grow past
+    # 256 tokens (width bucket 16 -> 64 blocks) on the way
+    active_per_step = [5, 5, 5, 7, 7, 3, 3, 9]
+    for step, n_act in enumerate(active_per_step):
+        seqs = list(range(n_act))
+        if step == 4:
+            for s in seqs:
+                ctx[s] += 200  # jump: as if many steps had passed
+        for s in seqs:
+            while len(blocks[s]) * PAGE < ctx[s] + 1:
+                blocks[s].append(int(free.pop()))
+        mb = max(len(blocks[s]) for s in seqs)
+        tables = np.zeros((n_act, mb), np.int32)
+        for i, s in enumerate(seqs):
+            tables[i, :len(blocks[s])] = blocks[s]
+        pos = np.array([ctx[s] for s in seqs], np.int32)
+        batch = StepBatch(tokens=[0] * n_act, positions=pos, query_start=np.arange(n_act + 1, dtype=np.int32),
+                          context_len=pos + 1, block_tables=tables.reshape(-1), max_blocks=mb)
+        acts = _acts(rng, n_act, L, dtype == torch.float16)
+        for l in range(L):
+            qkv[l][:n_act] = torch.from_numpy(acts[l]).to(device, dtype)
+        assert ga.decode_graph(batch, io)
+        eb.plan(batch)
+        for l in range(L):
+            eb.layer(l, qkv[l][:n_act], out_e[l][:n_act], q_norm=qn[l], k_norm=kn[l])
+        torch.cuda.synchronize()
+        bits = lambda t: t.cpu().numpy().view(np.uint16 if dtype == torch.float16 else np.uint32)  # noqa: E731
+        for l in range(L):
+            assert np.array_equal(bits(out_g[l][:n_act]), bits(out_e[l][:n_act])), f"step {step} layer {l} output"
+            for which in ("k", "v"):
+                a, b = bits(ga.pool_view(l, which)), bits(eb.pool_view(l, which))
+                assert np.array_equal(a[:NB], b[:NB]), f"step {step} layer {l} {which} pool"
+        for s in seqs:
+            ctx[s] += 1
+    # a step that is not pure decode is refused with nothing enqueued
+    two = StepBatch(tokens=[0, 0], positions=np.array([5, 6], np.int32), query_start=np.array([0, 2], np.int32),
+                    context_len=np.array([7], np.int32), block_tables=np.array(blocks[0][:1], np.int32), max_blocks=1)
+    assert not ga.decode_graph(two, io)
