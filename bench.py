@@ -231,6 +231,341 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+# ---- BASELINE configs 3, 4 and 5 (reported beside the metric; `--config N`) ----
+
+class Path:
+    """The GPU path plus the engine-side bookkeeping a config needs: a BlockManager over the pool, block
+    tables kept as one array, pools filled with random f16 K/V, per-layer q/k/v activations."""
+
+    def __init__(self, *, pool_pages, max_seqs, max_blocks, max_tokens, split_len, prefix_caching=False, seed,
+                 qkv_tokens=None, shared_qkv=False):
+        import torch
+
+        from ember_amd import BlockManager
+        from ember_amd.paged_kv import PagedKv
+
+        self.torch = torch
+        self.rng = np.random.default_rng(seed)
+        self.bm = BlockManager(pool_pages, prefix_caching)
+        every = [self.bm.allocate() for _ in range(pool_pages)]  # pages handed out in a seeded random order
+        self.bm.release_all([every[i] for i in self.rng.permutation(pool_pages)])
+        self.max_blocks = max_blocks
+        self.tables = np.zeros((max_seqs, max_blocks), np.int32)
+        self.blocks = [[] for _ in range(max_seqs)]
+        self.stream = torch.cuda.Stream()
+        self.kv = PagedKv(n_layers=N_LAYERS, n_heads=H, n_kv_heads=KVH, rms_eps=1e-6, rope_theta=1e6,
+                          max_position=max_blocks * PAGE, num_blocks=pool_pages, max_batch_tokens=max_tokens,
+                          max_seqs=max_seqs, dtype=torch.float16, split_len=split_len, stream=self.stream)
+        g = torch.Generator(device="cuda").manual_seed(seed)
+        with torch.cuda.stream(self.stream):
+            for layer in range(N_LAYERS):
+                self.kv.pool_view(layer, "k").normal_(generator=g)
+                self.kv.pool_view(layer, "v").normal_(generator=g)
+            rows = qkv_tokens or max_tokens
+            if shared_qkv:  # one buffer read by every layer (the values are synthetic either way)
+                self.qkv = torch.randn((rows, (H + 2 * KVH) * D), generator=g, device="cuda",
+                                       dtype=torch.float16).expand(N_LAYERS, -1, -1)
+            else:
+                self.qkv = torch.randn((N_LAYERS, rows, (H + 2 * KVH) * D), generator=g, device="cuda",
+                                       dtype=torch.float16)
+            self.qn = 1 + 0.1 * torch.randn((N_LAYERS, D), generator=g, device="cuda")
+            self.kn = 1 + 0.1 * torch.randn((N_LAYERS, D), generator=g, device="cuda")
+            self.out = torch.empty((max_tokens, H, D), device="cuda", dtype=torch.float16)
+        self.stream.synchronize()
+        self.alloc_s = 0.0
+
+    def ensure(self, s: int, upto: int) -> None:
+        t0 = time.perf_counter()
+        while len(self.blocks[s]) * PAGE < upto:
+            b = self.bm.allocate()
+            if b < 0:
+                raise RuntimeError("the page pool is exhausted")
+            self.tables[s, len(self.blocks[s])] = b
+            self.blocks[s].append(b)
+        self.alloc_s += time.perf_counter() - t0
+
+    def release(self, s: int) -> None:
+        t0 = time.perf_counter()
+        self.bm.release_all(self.blocks[s])
+        self.blocks[s] = []
+        self.alloc_s += time.perf_counter() - t0
+
+    def run(self, seqs, positions, query_start) -> None:
+        """Plans and runs one step of all layers for the sequences `seqs` (rows of the block tables)."""
+        from ember_amd import _lib
+        from ember_amd.paged_kv import StepBatch
+
+        positions = np.asarray(positions, np.int32)
+        qs = np.asarray(query_start, np.int32)
+        tab = self.tables[np.asarray(seqs)]
+        ctx = np.array([positions[qs[i + 1] - 1] + 1 for i in range(len(seqs))], np.int32)
+        mb = int(max(1, (ctx.max() + PAGE - 1) // PAGE))
+        b = StepBatch(tokens=np.zeros(positions.size, np.int32), positions=positions, query_start=qs,
+                      context_len=ctx, block_tables=np.ascontiguousarray(tab[:, :mb]).reshape(-1), max_blocks=mb)
+        self.kv.plan(b)
+        fn, h, out = _lib.lib().ember_kv_layer, self.kv._h, self.out.data_ptr()
+        for layer in range(N_LAYERS):
+            if fn(h, layer, self.qkv[layer].data_ptr(), self.qn[layer].data_ptr(), self.kn[layer].data_ptr(), None,
+                  out) != _lib.OK:
+                _lib.check(-1, "kv_layer")
+
+
+def _timed(path, step, steps, warmup):
+    """Bare pass (the step time), then a pass with HIP events around every paged-decode launch."""
+    for _ in range(warmup):
+        step()
+    path.stream.synchronize()
+    path.alloc_s = 0.0
+    bytes_ = 0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        bytes_ += step()
+    path.stream.synchronize()
+    wall = time.perf_counter() - t0
+    alloc_us = path.alloc_s / steps * 1e6
+    path.kv.set_timing(True)
+    path.kv.timing()
+    for _ in range(steps):
+        step()
+    path.stream.synchronize()
+    launches, kernel_ms = path.kv.timing()
+    path.kv.set_timing(False)
+    return wall / steps, bytes_ / steps, alloc_us, launches, kernel_ms
+
+
+def run_config5(args) -> dict:
+    """speculative verify on the paged cache at Qwen3-1.7B shape. 64 sequences with
+    contexts U[512, 4096]; each step appends the last accepted token and 4 draft tokens per sequence and
+    attends with q_len 5 (causal inside the window: one 5-token run per sequence through the fused
+    append + attention kernel), then rolls back to a seeded accepted count U{0..4}: the context grows by
+    1 + accepted, and the rejected slots are overwritten by the next step. Bytes count each sequence's
+    K/V once per layer."""
+    B5, Q = 64, 5
+    rng = np.random.default_rng(SEED + 5)
+    ctx = rng.integers(512, 4097, B5).astype(np.int64)
+    total = args.warmup + 2 * args.steps
+    max_ctx = int(ctx.max()) + Q * total + PAGE
+    mb = (max_ctx + PAGE - 1) // PAGE
+    pages = int(((ctx + Q * total) // PAGE + 2).sum())
+    path = Path(pool_pages=pages, max_seqs=B5, max_blocks=mb, max_tokens=B5 * Q, split_len=args.split_len, seed=SEED + 5)
+    acc_rng = np.random.default_rng(SEED + 55)
+    qs = np.arange(B5 + 1, dtype=np.int32) * Q
+
+    def step():
+        for s in range(B5):
+            path.ensure(s, int(ctx[s]) + Q)
+        pos = (ctx[:, None] + np.arange(Q)[None, :]).reshape(-1)
+        path.run(range(B5), pos, qs)
+        kv_bytes = KV_BYTES_PER_TOKEN * int((ctx + Q).sum())
+        ctx[:] += 1 + acc_rng.integers(0, Q, B5)
+        return N_LAYERS * (kv_bytes + TOKEN_BYTES * B5 * Q)
+
+    step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
+    gbs = step_bytes / step_s / 1e9
+    return {
+        "metric": "speculative verify rows/s and % HBM peak (Qwen3-1.7B shape, batch 64, q_len 5)",
+        "value": round(B5 * Q / step_s, 1), "unit": "query rows/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "host_blockmanager_us_per_step": round(alloc_us, 2),
+        "config": {"workload": "BASELINE configs[4]: 64 sequences, context U[512,4096], 4 drafts + 1 per sequence "
+                               "verified in one fused launch per layer, rollback to accepted U{0..4}, 28 layers",
+                   "split_len": args.split_len},
+    }
+
+
+def run_config3(args) -> dict:
+    """a continuous-batching mixed step at Qwen3-1.7B shape. 64 sequences share one
+    1024-token system prefix held in 64 sealed, refcounted pages (prefix cache: match_prefix). 4 of them
+    prefill their own 2048-token prompts in 512-token chunks (MFMA tiles), staggered so one finishes and a
+    new one is admitted every step; 60 decode one token each, with own context U[128, 2048] after the
+    prefix. Two decode sequences are a fork sharing every page, the partial last one included, so their
+    first step copies that page on write. Bytes count each sequence's context once per layer."""
+    NSEQ, NPRE, PREFIX, CHUNK, NCHUNK = 64, 4, 1024, 512, 4
+    rng = np.random.default_rng(SEED + 3)
+    total = args.warmup + 2 * args.steps
+    own = rng.integers(128, 2049, NSEQ - NPRE)
+    max_ctx = PREFIX + max(CHUNK * NCHUNK, int(own.max()) + total) + PAGE
+    mb = (max_ctx + PAGE - 1) // PAGE
+    pages = PREFIX // PAGE + int((own + total).sum()) // PAGE + 2 * NSEQ + (NPRE + 2) * CHUNK * NCHUNK // PAGE + 64
+    path = Path(pool_pages=pages, max_seqs=NSEQ, max_blocks=mb, max_tokens=NPRE * CHUNK + NSEQ, split_len=args.split_len,
+                prefix_caching=True, seed=SEED + 3)
+    bm = path.bm
+    prefix = rng.integers(0, 150000, PREFIX).astype(np.int32)
+    # The prefix, computed once (its K/V are already in the pools) and sealed into the prefix cache.
+    path.ensure(0, PREFIX)
+    parent = 0
+    for i, b in enumerate(path.blocks[0]):
+        parent = bm.seal(b, parent, prefix[i * PAGE:(i + 1) * PAGE])
+    prefix_blocks = list(path.blocks[0])
+    path.release(0)  # sealed and unreferenced: held by the prefix cache until a sequence matches it
+
+    def admit(s, n_own):  # a sequence starting with the prefix: the cache hands out the shared pages
+        got = bm.match_prefix(np.concatenate([prefix, np.zeros(1, np.int32)]))
+        assert got == prefix_blocks, "the prefix cache missed"
+        path.blocks[s] = list(got)
+        path.tables[s, :len(got)] = got
+        path.ensure(s, PREFIX + n_own)
+
+    ctx = np.zeros(NSEQ, np.int64)
+    for s in range(NPRE, NSEQ - 1):
+        admit(s, int(own[s - NPRE]))
+        ctx[s] = PREFIX + int(own[s - NPRE])
+    # the fork: sequence NSEQ-1 shares every page of sequence NSEQ-2, partial last page included
+    src = NSEQ - 2
+    bm.share(path.blocks[src])
+    path.blocks[NSEQ - 1] = list(path.blocks[src])
+    path.tables[NSEQ - 1, :len(path.blocks[src])] = path.blocks[src]
+    ctx[NSEQ - 1] = ctx[src]
+    assert ctx[src] % PAGE, "the fork's last page must be partial"
+    shared_last = path.blocks[src][-1]
+    assert bm.refcount(shared_last) == 2 and bm.refcount(prefix_blocks[0]) == NSEQ - NPRE
+    chunk_of = list(range(NPRE))  # staggered prompts: sequence i starts at chunk i
+    for s in range(NPRE):
+        admit(s, CHUNK * NCHUNK)
+    cow = {"copies": 0}
+
+    def step():
+        # copy-on-write before any write into a shared page
+        for s in range(NPRE, NSEQ):
+            last = path.blocks[s][-1] if ctx[s] % PAGE else None
+            if last is not None and bm.refcount(last) > 1:
+                nb = bm.copy_on_write(last)
+                if nb < 0:
+                    raise RuntimeError("no block for copy-on-write")
+                if nb != last:
+                    path.kv.copy_blocks([last], [nb])
+                    path.blocks[s][-1] = nb
+                    path.tables[s, len(path.blocks[s]) - 1] = nb
+                    cow["copies"] += 1
+        pos, qs = [], [0]
+        kv_tokens = 0
+        for s in range(NPRE):
+            c0 = PREFIX + CHUNK * chunk_of[s]
+            pos.append(np.arange(c0, c0 + CHUNK))
+            qs.append(qs[-1] + CHUNK)
+            kv_tokens += c0 + CHUNK
+        for s in range(NPRE, NSEQ):
+            path.ensure(s, int(ctx[s]) + 1)
+            pos.append(np.array([ctx[s]]))
+            qs.append(qs[-1] + 1)
+            kv_tokens += int(ctx[s]) + 1
+        path.run(range(NSEQ), np.concatenate(pos), qs)
+        ctx[NPRE:] += 1
+        for s in range(NPRE):  # the next chunk; a finished prompt makes room for a new one
+            chunk_of[s] += 1
+            if chunk_of[s] == NCHUNK:
+                path.release(s)
+                admit(s, CHUNK * NCHUNK)
+                chunk_of[s] = 0
+        return N_LAYERS * (KV_BYTES_PER_TOKEN * kv_tokens + TOKEN_BYTES * (NPRE * CHUNK + NSEQ - NPRE))
+
+    step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
+    assert cow["copies"] == 1, f"expected one copy-on-write, saw {cow['copies']}"
+    assert bm.refcount(prefix_blocks[0]) == NSEQ and bm.check() == "", bm.check()
+    gbs = step_bytes / step_s / 1e9
+    T = NPRE * CHUNK + NSEQ - NPRE
+    return {
+        "metric": "continuous-batching mixed step tokens/s and % HBM peak (Qwen3-1.7B shape, 4 x 512 prefill + 60 decode)",
+        "value": round(T / step_s, 1), "unit": "tokens/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "host_blockmanager_us_per_step": round(alloc_us, 2), "cow_copies": cow["copies"],
+        "prefix_refcount": bm.refcount(prefix_blocks[0]),
+        "config": {"workload": "BASELINE configs[2]: 64 sequences sharing a 1024-token prefix (64 sealed pages), "
+                               "4 x 512-token prefill chunks (MFMA tiles) + 60 decodes (own context U[128,2048]), "
+                               "one forked pair copying its shared partial page on write, 28 layers",
+                   "split_len": args.split_len},
+    }
+
+
+def run_config4(args) -> dict:
+    """large-pool decode sized for 288 GB of HBM. A 2,097,152-token pool (131,072
+    pages, 112 KiB of f16 K/V per token over 28 layers: 224 GiB) and 256 sequences with contexts
+    log-uniform in [512, 16384]. Each step decodes one token for every running sequence, preempts the
+    newest 8 (their pages go back to the pool) and resumes the 8 preempted the step before: their pages
+    are allocated again and their K/V restored by re-appending every context token through the append
+    kernel (the re-prefill's cache writes; the rest of the model's recompute is outside this path). The
+    decode step and the re-append are timed together; GB/s counts the decode's K/V once per sequence."""
+    import torch
+
+    from ember_amd import _lib
+
+    POOL, NSEQ, PRE = 131072, 256, 8
+    free = torch.cuda.mem_get_info()[0]
+    need = 2 * N_LAYERS * (POOL + 1) * KVH * PAGE * D * 2
+    if need > free * 0.95:
+        raise RuntimeError(f"config 4 needs {need / 2**30:.0f} GiB of pool, {free / 2**30:.0f} GiB free")
+    rng = np.random.default_rng(SEED + 4)
+    ctx = np.exp(rng.uniform(np.log(512), np.log(16384), NSEQ)).astype(np.int64)
+    total = args.warmup + 2 * args.steps
+    mb = (int(ctx.max()) + total + 2 * PAGE) // PAGE
+    resume_rows = PRE * (int(ctx.max()) + total)
+    path = Path(pool_pages=POOL, max_seqs=NSEQ, max_blocks=mb, max_tokens=NSEQ, split_len=args.split_len,
+                seed=SEED + 4, qkv_tokens=max(NSEQ, resume_rows), shared_qkv=True)
+    for s in range(NSEQ):
+        path.ensure(s, int(ctx[s]))
+    order = list(range(NSEQ))  # admission order: the newest are preempted
+    paused = []
+    dev = torch.device("cuda")
+    q_out = torch.empty((resume_rows, H, D), device=dev, dtype=torch.float16)
+    inv = torch.tensor([1.0 / (1e6 ** (2 * i / D)) for i in range(D // 2)], dtype=torch.float32, device=dev)
+    tables_dev = torch.empty(path.tables.shape, dtype=torch.int32, device=dev)
+
+    def reappend(seqs):
+        """The resumed sequences' K/V written again, every context token, through the append kernel."""
+        pos = np.concatenate([np.arange(0, ctx[s]) for s in seqs]).astype(np.int32)
+        tsq = np.concatenate([np.full(ctx[s], s) for s in seqs]).astype(np.int32)
+        with torch.cuda.stream(path.stream):
+            pos_d = torch.from_numpy(pos).to(dev, non_blocking=False)
+            tsq_d = torch.from_numpy(tsq).to(dev, non_blocking=False)
+            tables_dev.copy_(torch.from_numpy(path.tables))
+        a = _lib.QkvArgs()
+        a.q_out, a.inv_freq = q_out.data_ptr(), inv.data_ptr()
+        a.positions, a.token_seq, a.block_tables = pos_d.data_ptr(), tsq_d.data_ptr(), tables_dev.data_ptr()
+        a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = path.tables.shape[1], int(pos.size), H, KVH, D
+        a.eps, a.num_blocks, a.dtype = 1e-6, POOL + 1, _lib.DTYPE_F16
+        for layer in range(N_LAYERS):
+            a.qkv = path.qkv[layer].data_ptr()
+            a.k_cache, a.v_cache = path.kv.pool_view(layer, "k").data_ptr(), path.kv.pool_view(layer, "v").data_ptr()
+            a.q_norm, a.k_norm = path.qn[layer].data_ptr(), path.kn[layer].data_ptr()
+            _lib.check(_lib.lib().ember_hip_kv_append(a, path.stream.cuda_stream), "kv_append")
+        return pos_d, tsq_d  # kept alive until the stream has run them
+
+    def step():
+        nonlocal paused
+        running = [s for s in order if s not in paused]
+        for s in paused:
+            path.ensure(s, int(ctx[s]))
+        keep = reappend(paused) if paused else None
+        for s in running:
+            path.ensure(s, int(ctx[s]) + 1)
+        path.run(running, ctx[running], np.arange(len(running) + 1))
+        kv_bytes = KV_BYTES_PER_TOKEN * int((ctx[running] + 1).sum())
+        ctx[running] += 1
+        # the resumed rejoin at the back; the newest 8 running are preempted and their pages freed
+        newest = running[-PRE:]
+        for s in newest:
+            path.release(s)
+        order[:] = [s for s in order if s not in newest] + newest
+        paused = newest
+        del keep
+        return N_LAYERS * (kv_bytes + TOKEN_BYTES * len(running))
+
+    step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
+    gbs = step_bytes / step_s / 1e9
+    return {
+        "metric": "large-pool decode tokens/s, % HBM peak and page-allocator overhead (2M-token pool, 256 sequences)",
+        "value": round((NSEQ - PRE) / step_s, 1), "unit": "decode tokens/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "host_blockmanager_us_per_step": round(alloc_us, 2),
+        "config": {"workload": "BASELINE configs[3]: 2,097,152-token f16 pool (224 GiB over 28 layers), 256 sequences "
+                               "with context logU[512,16384], each step preempting the newest 8 and re-appending the "
+                               "8 preempted the step before", "split_len": args.split_len},
+    }
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +575,8 @@ def main() -> int:
     ap.add_argument("--split-len", type=int, default=512, help="keys per decode split (a multiple of 16)")
     ap.add_argument("--graph", action="store_true",
                     help="run each step as a replayed hipGraph of all layers (the timing pass stays eager)")
+    ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
+                    help="BASELINE config: 2 = the metric (default); 3, 4, 5 print their own line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size page copy used to scale the HBM byte counters")
     args = ap.parse_args()
@@ -249,6 +586,22 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.steps)
+    if args.config != 2:
+        import torch
+
+        from ember_amd import lib
+
+        lib()
+        assert torch.cuda.is_available(), "bench.py needs a GPU"
+        log(f"[bench] BASELINE config {args.config}")
+        fn = {3: run_config3, 4: run_config4, 5: run_config5}[args.config]
+        line = fn(args)
+        line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+                     "vs_baseline": None, "dtype": "f16", "data": "synthetic, seeded"})
+        log(f"[bench] {line['ms_per_step']:.3f} ms/step, {line['value']:.0f} {line['unit']}, "
+            f"{line['step_hbm_frac']:.1%} of peak HBM")
+        print(json.dumps(line), flush=True)
+        return 0
 
     import torch
 

@@ -61,10 +61,15 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_HIP_CHECK(hipMalloc(&q_, T * cfg_.n_heads * cfg_.head_dim * elem_));
     max_blocks_per_seq_ = (cfg_.max_position + kBlockSize - 1) / kBlockSize;
     max_splits_ = (max_blocks_per_seq_ * kBlockSize + opt_.split_len - 1) / opt_.split_len;
-    const size_t part_rows = T * cfg_.n_heads * static_cast<size_t>(max_splits_);
+    // Split scratch serves decode tokens only. With f16 pools a sequence's run of 16 or more new tokens
+    // goes to prefill tiles, so at most 15 tokens per sequence are decode tokens.
+    decode_cap_ = static_cast<int>(opt_.dtype == EMBER_DTYPE_F16 && opt_.use_prefill_kernel
+                                       ? std::min<size_t>(T, static_cast<size_t>(kFlashMinTokens - 1) * opt_.max_seqs)
+                                       : T);
+    const size_t part_rows = static_cast<size_t>(decode_cap_) * cfg_.n_heads * static_cast<size_t>(max_splits_);
     part_acc_ = device_alloc<float>(part_rows * cfg_.head_dim);
     part_ml_ = device_alloc<float>(part_rows * 2);
-    const size_t counters = T * static_cast<size_t>(cfg_.n_kv_heads);  // one per (run, kv head); runs <= tokens
+    const size_t counters = static_cast<size_t>(decode_cap_) * cfg_.n_kv_heads;  // per (run, kv head); runs <= tokens
     merge_counters_ = device_alloc<uint32_t>(counters);
     EMBER_HIP_CHECK(hipMemsetAsync(merge_counters_, 0, counters * sizeof(uint32_t), stream_));
 
@@ -187,6 +192,8 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     T_ = T;
     max_blocks_ = b.max_blocks;
     decode_count_ = static_cast<int>(decode_.size());
+    EMBER_CHECK(decode_count_ <= decode_cap_, "internal: {} decode tokens exceed the split scratch ({})", decode_count_,
+                decode_cap_);
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
     fused_ = fused_ && tiles_ == 0 && decode_count_ == T;

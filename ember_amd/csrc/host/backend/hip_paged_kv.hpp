@@ -108,6 +108,7 @@ private:
     int64_t layer_elems_ = 0;       // elements of one layer's K (or V) pool
     int max_blocks_per_seq_ = 0;
     int max_splits_ = 0;
+    int decode_cap_ = 0;            // decode tokens a step can hold (the split scratch is sized for it)
 
     void *k_ = nullptr, *v_ = nullptr, *q_ = nullptr;
     float *inv_freq_ = nullptr, *part_acc_ = nullptr, *part_ml_ = nullptr;
