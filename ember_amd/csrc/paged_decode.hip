@@ -369,7 +369,11 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 
     __shared__ float red_acc[ROWS][kWaves][D];
     __shared__ float red_m[ROWS][kWaves], red_l[ROWS][kWaves];
-    __shared__ __align__(16) T q_lds[FUSED ? ROWS : 1][D];
+    // With many rows (a verify run), q stays in LDS and each row's slice is read
+    // again per page: holding every row's q in registers as well would push the
+    // kernel past 256 VGPRs (one wave per SIMD).
+    constexpr bool Q_LDS = ROWS > 4;
+    __shared__ __align__(16) T q_lds[(FUSED || Q_LDS) ? ROWS : 1][D];
     __shared__ __align__(16) T new_k[NEW][D], new_v[NEW][D];
     __shared__ int merge_here;
 
@@ -436,7 +440,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         load_page(pr, kbase + off, vbase + off, lane_off, live);
     };
 
-    QSlice<T> q[ROWS];
+    QSlice<T> q[Q_LDS ? 1 : ROWS];
     float m[ROWS], l[ROWS], acc[ROWS][8];
 #pragma unroll
     for (int row = 0; row < ROWS; row++) {
@@ -448,14 +452,27 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     PageRegs<T> A, B;
 
     if constexpr (!FUSED) {
+        if constexpr (Q_LDS) {
+            // rows' q vectors into LDS, 8 elements per thread at a time
+            for (int idx = static_cast<int>(threadIdx.x); idx < nrows * (D / 8); idx += kThreads) {
+                const int row = idx / (D / 8), d8 = (idx % (D / 8)) * 8;
+                const int li = first + row / G;
+                const int t = p.token_index ? p.token_index[li] : li;
+                const T *src = static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + kvh * G + row % G) * D + d8;
 #pragma unroll
-        for (int row = 0; row < ROWS; row++) {
-            const int li = first + src_row(row) / G;
-            const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-            const int head = kvh * G + src_row(row) % G;
-            load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
+                for (int e = 0; e < 8; e++) q_lds[row][d8 + e] = src[e];
+            }
+        } else {
+#pragma unroll
+            for (int row = 0; row < ROWS; row++) {
+                const int li = first + src_row(row) / G;
+                const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+                const int head = kvh * G + src_row(row) % G;
+                load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
+            }
         }
         fetch(A, 0);
+        if constexpr (Q_LDS) __syncthreads();
     } else {
         // q of every row and the new K/V in this split, one head vector per
         // wave at a time; lane l holds dims l and l + 64 (a rotary pair). The
@@ -532,8 +549,10 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if constexpr (!Q_LDS) {
 #pragma unroll
-        for (int row = 0; row < ROWS; row++) load_q(q[row], &q_lds[src_row(row)][8 * c]);
+            for (int row = 0; row < ROWS; row++) load_q(q[row], &q_lds[src_row(row)][8 * c]);
+        }
     }
 
     // One page: scores and online softmax for every row, then the values key by
@@ -550,10 +569,13 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         bool vis[ROWS][4];
 #pragma unroll
         for (int row = 0; row < ROWS; row++) {
+            QSlice<T> qrow;
+            if constexpr (Q_LDS) load_q(qrow, &q_lds[src_row(row)][8 * c]);
+            else qrow = q[row];
             float s[4];
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                s[i] = row16_sum(dot8(q[row], pr.k[i])) * p.scale_log2;
+                s[i] = row16_sum(dot8(qrow, pr.k[i])) * p.scale_log2;
                 if constexpr (MASKED) {
                     vis[row][i] = key0 + 4 * i <= row_pos[row];
                     if (!vis[row][i]) s[i] = -INFINITY;
