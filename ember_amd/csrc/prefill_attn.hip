@@ -8,11 +8,14 @@
 // keys past a query's position masked, online softmax, f16 in, f32
 // accumulation, f16 out.
 //
-// Shape on MI355X: one work-group of 4 waves per (tile, pair of query heads of
-// one kv head), so each K/V block is read once for both heads of a GQA pair
-// (the reference's block serves one head). Wave w owns tokens 16w .. 16w + 15
-// of the tile. Keys go in blocks of 32 (two pages): the work-group stages the
-// block's K rows and V transposed (dims x keys) in LDS, then every wave runs
+// Shape on MI355X: one work-group per (tile, pair of query heads of one kv
+// head), so each K/V block is read once for both heads of a GQA pair (the
+// reference's block serves one head): 4 waves per head, wave w owning tokens
+// 16 (w % 4) .. + 15 of the tile for head w / 4. Keys go in blocks of 32 (two
+// pages): the work-group stages a block's K rows and V transposed (dims x
+// keys) in LDS, double-buffered (every thread fetches its part of block k + 1
+// into registers while block k computes, then stores it to the other buffer),
+// and every wave runs
 //   S^T = K Q^T   16 keys x 16 queries per v_mfma_f32_16x16x32_f16, four
 //                 32-dim chunks; lane l ends with query l % 16 and keys
 //                 4 (l / 16) + 0..3 of each 16-key half;
@@ -32,7 +35,8 @@ namespace {
 
 constexpr int kTileTokens = EMBER_PREFILL_TILE;  // 64
 constexpr int kKeyBlock = 32;                     // keys per LDS block: two pages
-constexpr int kPThreads = 256;
+template <int HG>
+constexpr int kThreadsFor = 256 * HG;  // 4 waves per query head
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
 constexpr int kVRow = kKeyBlock + 8;              // LDS row of V^T (one dim), halves
 
@@ -43,18 +47,20 @@ typedef float f32x4v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int HG>  // query heads per work-group (1 or 2), all of one kv head
-__global__ void __launch_bounds__(kPThreads) prefill_kernel(EmberPrefillArgs a, float scale_log2) {
-    __shared__ __align__(16) f16 k_lds[kKeyBlock * kKRow];
-    __shared__ __align__(16) f16 v_lds[kHeadDim * kVRow];
-    __shared__ int wave_max[4];
+__global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillArgs a, float scale_log2) {
+    constexpr int kPThreads = kThreadsFor<HG>;
+    constexpr int kWavesP = kPThreads / kWave;         // 4 x HG: wave w takes tokens 16 (w % 4).. and head w / 4
+    __shared__ __align__(16) f16 k_lds[2][kKeyBlock * kKRow];
+    __shared__ __align__(16) f16 v_lds[2][kHeadDim * kVRow];
+    __shared__ int wave_max[kWavesP];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid % kWave, wave = tid / kWave;
     const int ql = lane % 16, g = lane / 16;
     const int tile = static_cast<int>(blockIdx.x);
-    const int head0 = static_cast<int>(blockIdx.y) * HG;
+    const int head = static_cast<int>(blockIdx.y) * HG + wave / 4;
     const int G = a.n_heads / a.n_kv;
-    const int kvh = head0 / G;
+    const int kvh = static_cast<int>(blockIdx.y) * HG / G;
     const int t0 = a.tile_start[tile];
     const int nt = min(a.tile_end[tile] - t0, kTileTokens);
     const int32_t *table = a.block_tables + static_cast<int64_t>(a.tile_seq[tile]) * a.max_blocks;
@@ -62,147 +68,153 @@ __global__ void __launch_bounds__(kPThreads) prefill_kernel(EmberPrefillArgs a, 
     const f16 *kc = static_cast<const f16 *>(a.k_cache);
     const f16 *vc = static_cast<const f16 *>(a.v_cache);
 
-    // This lane's query (token 16 wave + ql of the tile) and the tile's key range.
-    const int my_i = 16 * wave + ql;
+    // This lane's query (token 16 (wave % 4) + ql of the tile) and the tile's key range.
+    const int my_i = 16 * (wave % 4) + ql;
     const bool my_ok = my_i < nt;
     const int my_pos = my_ok ? a.positions[t0 + my_i] : -1;
     int mx = my_pos;
     for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, kWave));
     if (lane == 0) wave_max[wave] = mx;
     __syncthreads();
-    const int max_pos = min(max(max(wave_max[0], wave_max[1]), max(wave_max[2], wave_max[3])),
-                            a.max_blocks * kPage - 1);
+    int max_pos = wave_max[0];
+    for (int w = 1; w < kWavesP; w++) max_pos = max(max_pos, wave_max[w]);
+    max_pos = min(max_pos, a.max_blocks * kPage - 1);
     const int n_blocks = (max_pos + kKeyBlock) / kKeyBlock;
 
-    // Q^T operands: for head h and 32-dim chunk c, dims 32c + 8g .. + 8 of this lane's query.
-    f16x8 qb[HG][4];
+    // Q^T operands: for 32-dim chunk c, dims 32c + 8g .. + 8 of this lane's query.
+    f16x8 qb[4];
 #pragma unroll
-    for (int h = 0; h < HG; h++)
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            f16x8 v = {};
-            if (my_ok)
-                v = *reinterpret_cast<const f16x8 *>(q + (static_cast<int64_t>(t0 + my_i) * a.n_heads + head0 + h) * kHeadDim +
-                                                     32 * c + 8 * g);
-            qb[h][c] = v;
-        }
-
-    float m[HG], l[HG];
-    f32x4v o_acc[HG][8];
-#pragma unroll
-    for (int h = 0; h < HG; h++) {
-        m[h] = -INFINITY;
-        l[h] = 0.0f;
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o_acc[h][dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = 0; c < 4; c++) {
+        f16x8 v = {};
+        if (my_ok)
+            v = *reinterpret_cast<const f16x8 *>(q + (static_cast<int64_t>(t0 + my_i) * a.n_heads + head) * kHeadDim +
+                                                 32 * c + 8 * g);
+        qb[c] = v;
     }
 
-    for (int kb = 0; kb < n_blocks; kb++) {
-        // Stage the block: 32 keys x 128 dims of K (row-major) and of V (transposed),
-        // 512 chunks of 8 halves each; keys past the tile's last position or in a
-        // block outside the pool are zeros.
+    float m = -INFINITY, l = 0.0f;
+    f32x4v o_acc[8];
 #pragma unroll
-        for (int rep = 0; rep < 2; rep++) {
-            const int chunk = tid + rep * kPThreads;
-            const int key = chunk / 16, d8 = (chunk % 16) * 8;
+    for (int dt = 0; dt < 8; dt++) o_acc[dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // A key block's K and V, fetched into registers (512 chunks of 8 halves
+    // each per block: one or two per thread) and later stored to LDS; keys past
+    // the tile's last position or in a block outside the pool are zeros.
+    constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kPThreads;
+    auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vv4)[kChunks]) {
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) {
+            const int chunk = tid + j * kPThreads, key = chunk / 16, d8 = (chunk % 16) * 8;
+            kv4[j] = make_uint4(0, 0, 0, 0);
+            vv4[j] = make_uint4(0, 0, 0, 0);
             const int pos = kb * kKeyBlock + key;
-            uint4 kv4 = make_uint4(0, 0, 0, 0), vv4 = make_uint4(0, 0, 0, 0);
-            if (pos <= max_pos) {
+            if (kb < n_blocks && pos <= max_pos) {
                 const int blk = table[pos / kPage];
                 if (blk >= 0 && blk < a.num_blocks) {
                     const int64_t off = ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos % kPage) * kHeadDim + d8;
-                    kv4 = *reinterpret_cast<const uint4 *>(kc + off);
-                    vv4 = *reinterpret_cast<const uint4 *>(vc + off);
+                    kv4[j] = *reinterpret_cast<const uint4 *>(kc + off);
+                    vv4[j] = *reinterpret_cast<const uint4 *>(vc + off);
                 }
             }
-            *reinterpret_cast<uint4 *>(&k_lds[key * kKRow + d8]) = kv4;
-            const f16x8 vh = __builtin_bit_cast(f16x8, vv4);
-#pragma unroll
-            for (int i = 0; i < 8; i++) v_lds[(d8 + i) * kVRow + key] = vh[i];
         }
-        __syncthreads();
+    };
+    auto stage = [&](int buf, const uint4 (&kv4)[kChunks], const uint4 (&vv4)[kChunks]) {
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) {
+            const int chunk = tid + j * kPThreads, key = chunk / 16, d8 = (chunk % 16) * 8;
+            *reinterpret_cast<uint4 *>(&k_lds[buf][key * kKRow + d8]) = kv4[j];
+            const f16x8 vh = __builtin_bit_cast(f16x8, vv4[j]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v_lds[buf][(d8 + i) * kVRow + key] = vh[i];
+        }
+    };
+
+    uint4 nk[kChunks], nv[kChunks];
+    fetch(0, nk, nv);
+    stage(0, nk, nv);
+    __syncthreads();
+    for (int kb = 0; kb < n_blocks; kb++) {
+        const int buf = kb & 1;
+        fetch(kb + 1, nk, nv);  // in flight while this block computes
 
         // Keys of this lane in the block: 16 st + 4g + r (st = half, r = 0..3).
         const int key_base = kb * kKeyBlock + 4 * g;
         const bool full = kb * kKeyBlock + kKeyBlock - 1 <= my_pos;  // every key of the block visible
+        f32x4v s[2];
 #pragma unroll
-        for (int h = 0; h < HG; h++) {
-            f32x4v s[2];
+        for (int st = 0; st < 2; st++) {
+            f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int st = 0; st < 2; st++) {
-                f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int c = 0; c < 4; c++) {
-                    const f16x8 ka = *reinterpret_cast<const f16x8 *>(&k_lds[(16 * st + ql) * kKRow + 32 * c + 8 * g]);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[h][c], acc, 0, 0, 0);
-                }
-                s[st] = acc;
+            for (int c = 0; c < 4; c++) {
+                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&k_lds[buf][(16 * st + ql) * kKRow + 32 * c + 8 * g]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[c], acc, 0, 0, 0);
             }
-            float sv[8];
-            float bm = -INFINITY;
-#pragma unroll
-            for (int st = 0; st < 2; st++)
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float x = s[st][r] * scale_log2;
-                    if (!full && key_base + 16 * st + r > my_pos) x = -INFINITY;
-                    sv[4 * st + r] = x;
-                    bm = fmaxf(bm, x);
-                }
-            bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-            const float mn = fmaxf(m[h], bm);
-            const float ref = mn == -INFINITY ? 0.0f : mn;
-            const float corr = m[h] == mn ? 1.0f : exp2_fast(m[h] - ref);
-            f16x8 pa;
-            float psum = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const f16 ph = static_cast<f16>(exp2_fast(sv[i] - ref));
-                pa[i] = ph;
-                psum += static_cast<float>(ph);
-            }
-            l[h] = l[h] * corr + psum;
-            m[h] = mn;
-            // O rows are queries 4g + r: their correction factors live in lanes 4g + r.
-            float cq[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
-                const f16 *vrow = &v_lds[(16 * dt + ql) * kVRow];
-                const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
-                const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
-                const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                f32x4v acc = o_acc[h][dt];
-#pragma unroll
-                for (int r = 0; r < 4; r++) acc[r] = acc[r] * cq[r];
-                o_acc[h][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc, 0, 0, 0);
-            }
+            s[st] = acc;
         }
-        __syncthreads();  // the next block overwrites the LDS
+        float sv[8];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; st++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float x = s[st][r] * scale_log2;
+                if (!full && key_base + 16 * st + r > my_pos) x = -INFINITY;
+                sv[4 * st + r] = x;
+                bm = fmaxf(bm, x);
+            }
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        const float mn = fmaxf(m, bm);
+        const float ref = mn == -INFINITY ? 0.0f : mn;
+        const float corr = m == mn ? 1.0f : exp2_fast(m - ref);
+        f16x8 pa;
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const f16 ph = static_cast<f16>(exp2_fast(sv[i] - ref));
+            pa[i] = ph;
+            psum += static_cast<float>(ph);
+        }
+        l = l * corr + psum;
+        m = mn;
+        // O rows are queries 4g + r: their correction factors live in lanes 4g + r.
+        float cq[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) {
+            const f16 *vrow = &v_lds[buf][(16 * dt + ql) * kVRow];
+            const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
+            const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
+            const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            f32x4v acc = o_acc[dt];
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = acc[r] * cq[r];
+            o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc, 0, 0, 0);
+        }
+        // The next block goes into the other buffer, which nobody reads any more:
+        // the barrier that ended the previous block separated its readers.
+        if (kb + 1 < n_blocks) stage(buf ^ 1, nk, nv);
+        __syncthreads();
     }
 
     // Row sums over the four lanes of each query, then out = O / l for the
     // queries 4g + r this lane's O rows hold.
+    float lt = l;
+    lt = lt + __shfl_xor(lt, 16, kWave);
+    lt = lt + __shfl_xor(lt, 32, kWave);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    float iq[4];
 #pragma unroll
-    for (int h = 0; h < HG; h++) {
-        float lt = l[h];
-        lt = lt + __shfl_xor(lt, 16, kWave);
-        lt = lt + __shfl_xor(lt, 32, kWave);
-        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        float iq[4];
+    for (int r = 0; r < 4; r++) iq[r] = __shfl(inv, 4 * g + r, kWave);
+    f16 *out = static_cast<f16 *>(a.out);
 #pragma unroll
-        for (int r = 0; r < 4; r++) iq[r] = __shfl(inv, 4 * g + r, kWave);
-        f16 *out = static_cast<f16 *>(a.out);
+    for (int r = 0; r < 4; r++) {
+        const int i = 16 * (wave % 4) + 4 * g + r;
+        if (i >= nt) continue;
+        f16 *row = out + (static_cast<int64_t>(t0 + i) * a.n_heads + head) * kHeadDim;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = 16 * wave + 4 * g + r;
-            if (i >= nt) continue;
-            f16 *row = out + (static_cast<int64_t>(t0 + i) * a.n_heads + head0 + h) * kHeadDim;
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) row[16 * dt + ql] = static_cast<f16>(o_acc[h][dt][r] * iq[r]);
-        }
+        for (int dt = 0; dt < 8; dt++) row[16 * dt + ql] = static_cast<f16>(o_acc[dt][r] * iq[r]);
     }
 }
 
@@ -214,9 +226,9 @@ hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(a.num_tiles), static_cast<unsigned>(a.n_heads / hg));
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)
-        hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kPThreads), 0, stream, a, scale_log2);
+        hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, a, scale_log2);
     else
-        hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kPThreads), 0, stream, a, scale_log2);
+        hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, a, scale_log2);
     return hipGetLastError();
 }
 
