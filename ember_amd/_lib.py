@@ -13,10 +13,11 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 2
+ABI_VERSION = 3
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
+MAX_SPLIT_LEN = 1024
 OK = 0
 ERR_INVALID = -1
 DTYPE_F16 = 0

@@ -124,9 +124,10 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
     if (!valid_dtype(a->dtype)) return set_error(EMBER_ERR_INVALID, "paged_decode: unknown dtype %d", a->dtype);
     if (a->T < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
         return set_error(EMBER_ERR_INVALID, "paged_decode: bad sizes");
-    if (a->num_splits < 1 || a->num_splits > 65535 || a->split_len < kPage || a->split_len % kPage != 0)
-        return set_error(EMBER_ERR_INVALID, "paged_decode: split_len must be a positive multiple of 16 (got %d x %d)",
-                         a->num_splits, a->split_len);
+    if (a->num_splits < 1 || a->num_splits > 65535 || a->split_len < kPage || a->split_len % kPage != 0 ||
+        a->split_len > EMBER_MAX_SPLIT_LEN)
+        return set_error(EMBER_ERR_INVALID, "paged_decode: split_len must be a multiple of 16 in 16..%d (got %d x %d)",
+                         EMBER_MAX_SPLIT_LEN, a->num_splits, a->split_len);
     if (a->T == 0) return EMBER_OK;
     if ((!a->q && !qkv) || !a->k_cache || !a->v_cache || !a->positions || !a->token_seq || !a->block_tables || !a->out)
         return set_error(EMBER_ERR_INVALID, "paged_decode: a required pointer is null");

@@ -44,7 +44,8 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_CHECK(opt_.num_blocks > 0, "the KV cache has no blocks");
     EMBER_CHECK(opt_.dtype == EMBER_DTYPE_F16 || opt_.dtype == EMBER_DTYPE_F32, "unknown dtype {}", opt_.dtype);
     if (opt_.split_len <= 0) opt_.split_len = 512;
-    EMBER_CHECK(opt_.split_len % kBlockSize == 0, "split_len {} is not a multiple of {}", opt_.split_len, kBlockSize);
+    EMBER_CHECK(opt_.split_len % kBlockSize == 0 && opt_.split_len <= EMBER_MAX_SPLIT_LEN,
+                "split_len {} is not a multiple of {} up to {}", opt_.split_len, kBlockSize, EMBER_MAX_SPLIT_LEN);
     EMBER_CHECK(opt_.max_batch_tokens > 0 && opt_.max_seqs > 0, "bad batch limits");
     EMBER_CHECK(cfg_.max_position > 0, "max_position must be set");
     elem_ = opt_.dtype == EMBER_DTYPE_F16 ? 2 : 4;
@@ -81,10 +82,10 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_HIP_CHECK(hipMemcpyAsync(inv_freq_, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice, stream_));
 
     // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables, work items and their
-    // descriptors (8 ints each, 128-byte aligned like every array here).
+    // descriptors (kDescInts each, 128-byte aligned like every array here).
     ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
                      static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) +
-                     pad32(8 * T * max_splits_) + 64;
+                     pad32(static_cast<size_t>(kDescInts) * T * max_splits_) + 64;
     for (int i = 0; i < 2; i++) {
         dev_ints_[i] = device_alloc<int32_t>(ints_capacity_);
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
@@ -224,29 +225,38 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     }
     num_work_ = static_cast<int>(work_.size() / 2);
     // The kernel's view of each item (EmberAttnArgs::work_desc): everything it
-    // would otherwise look up in a chain before its first page load.
-    work_desc_.assign(static_cast<size_t>(num_work_) * 8, 0);
+    // would otherwise look up in a chain before its first page loads.
+    work_desc_.assign(static_cast<size_t>(num_work_) * kDescInts, -1);
     for (int i = 0; i < num_work_; i++) {
         const int r = work_[2 * static_cast<size_t>(i)];
-        if (r < 0) {
-            work_desc_[8 * static_cast<size_t>(i)] = -1;
-            continue;
-        }
+        if (r < 0) continue;  // padding: run -1
+        const int split = work_[2 * static_cast<size_t>(i) + 1];
         const int first = run_first_[static_cast<size_t>(r)], count = run_count_[static_cast<size_t>(r)];
+        const int t0 = decode_[static_cast<size_t>(first)];
         int lo = INT32_MAX, hi = -1;
+        bool counting = true;
         for (int k = 0; k < count; k++) {
-            const int pos = b.positions[static_cast<size_t>(decode_[static_cast<size_t>(first + k)])];
+            const int t = decode_[static_cast<size_t>(first + k)];
+            const int pos = b.positions[static_cast<size_t>(t)];
             lo = std::min(lo, pos);
             hi = std::max(hi, pos);
+            counting = counting && t == t0 + k && pos == b.positions[static_cast<size_t>(t0)] + k;
         }
-        int32_t *d = &work_desc_[8 * static_cast<size_t>(i)];
+        const int seq = token_seq_[static_cast<size_t>(t0)];
+        int32_t *d = &work_desc_[kDescInts * static_cast<size_t>(i)];
         d[0] = r;
-        d[1] = work_[2 * static_cast<size_t>(i) + 1];
+        d[1] = split;
         d[2] = first;
         d[3] = count;
-        d[4] = token_seq_[static_cast<size_t>(decode_[static_cast<size_t>(first)])];
+        d[4] = seq;
         d[5] = lo;
         d[6] = hi;
+        d[7] = counting ? t0 : -1;
+        const int ctx = std::min(hi + 1, b.max_blocks * kBlockSize);
+        const int p0 = split * opt_.split_len / kBlockSize;
+        const int p_last = (std::min(ctx, (split + 1) * opt_.split_len) - 1) / kBlockSize;
+        const int32_t *row = b.block_tables.data() + static_cast<size_t>(seq) * b.max_blocks;
+        for (int j = 0; j < 8 && p0 + j <= p_last; j++) d[8 + j] = row[p0 + j];
     }
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.

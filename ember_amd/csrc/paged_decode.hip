@@ -23,9 +23,10 @@
 //   softmax: each DPP row keeps its own running max / sum over the keys it
 //           holds (no cross-row traffic in the loop);
 //   values: each lane accumulates its 8 dims over its 4 keys.
-// Latency: block ids are wave-uniform scalar loads (they never wait on the
-// page loads), and each wave keeps its next page in flight in registers while
-// it works on the current one.
+// Latency: a work-group's first page loads depend on one descriptor load only
+// (the descriptor carries the first block ids), the split's other block ids
+// arrive in one vector load next to them, and each wave keeps its next page in
+// flight in registers while it works on the current one.
 // At the end: rows merge through two lane exchanges, waves through LDS, and
 // splits either in the separate merge kernel or, with merge counters, in the
 // last work-group of the (run, kv head) to finish - all in one fixed order.
@@ -58,8 +59,13 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * kWave;
 
 // A work item as the host plan describes it (EmberAttnArgs::work_desc): run,
-// split, first list entry, count, sequence, lowest position, highest position, 0.
-typedef int32_t WorkDesc __attribute__((ext_vector_type(8)));
+// split, first list entry, count, sequence, lowest position, highest position,
+// the first entry's token when the run's tokens and positions both count up by
+// one (else -1), then the block ids of the split's first 8 pages (-1 past its
+// last page). One s_load_dwordx16 gives a work-group everything it needs to
+// issue its first page loads.
+typedef int32_t WorkDesc __attribute__((ext_vector_type(16)));
+constexpr int kDescTok = 7, kDescBlocks = 8;
 
 struct DecodeParams {
     const void *q, *k, *v;
@@ -337,23 +343,30 @@ __device__ __forceinline__ void merge_one(const DecodeParams &p, int li, int hea
 // fewer pages in flight.
 __device__ __forceinline__ void phase_break() { __builtin_amdgcn_sched_barrier(0); }
 
+// One work item: (run, kv head, split) = work-group `bid` of the dense grid or
+// entry `bid` of the work list (item bid / n_kv, kv head bid % n_kv). tid is
+// the thread's index in the work-group.
 template <typename T, int ROWS, bool FUSED>
-__global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
+__device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid, const int tid) {
     constexpr int D = kHeadDim;
     constexpr int NEW = FUSED ? EMBER_MAX_RUN : 1;
-    const int lane = static_cast<int>(threadIdx.x) % kWave;
-    const int wave = uniform(static_cast<int>(threadIdx.x) / kWave);
+    const int lane = tid % kWave;
+    const int wave = uniform(tid / kWave);
     const int r = lane >> 4, c = lane & 15;
     const int G = p.G;
+    // Until its page walk starts, a work-group runs at raised wave priority: a
+    // CU's older waves, streaming pages, otherwise win the issue arbitration
+    // and a late work-group's first loads wait behind them for microseconds.
+    __builtin_amdgcn_s_setprio(3);
 
     int run, kvh, split;
     WorkDesc desc = {};
     const bool have_desc = p.work && p.work_desc;
     if (p.work) {
-        const int item = static_cast<int>(blockIdx.x) / p.n_kv;
-        kvh = static_cast<int>(blockIdx.x) % p.n_kv;
+        const int item = bid / p.n_kv;
+        kvh = bid % p.n_kv;
         if (have_desc) {
-            desc = uniform_load(reinterpret_cast<const WorkDesc *>(p.work_desc) + item);  // one s_load_dwordx8
+            desc = uniform_load(reinterpret_cast<const WorkDesc *>(p.work_desc) + item);  // one s_load_dwordx16
             run = desc[0];
             split = desc[1];
         } else {
@@ -362,7 +375,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         }
         if (run < 0 || run >= p.num_runs || split < 0 || split >= p.num_splits) return;  // whole work-group
     } else {
-        run = blockIdx.x;
+        run = bid;
         kvh = blockIdx.y;
         split = blockIdx.z;
     }
@@ -386,13 +399,15 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     nq = max(1, min(min(nq, ROWS / G), FUSED ? NEW : ROWS));  // FUSED: new_k / new_v hold NEW tokens
     const int nrows = nq * G;
     auto src_row = [&](int row) { return min(row, nrows - 1); };
-    int seq;
-    if (have_desc) {
-        seq = desc[4];
-    } else {
-        const int t0 = p.token_index ? uniform_load(p.token_index + first) : first;
-        seq = uniform_load(p.token_seq + t0);
-    }
+    // Token and position of the run's entry i: with a counting descriptor both
+    // are arithmetic, otherwise two dependent scalar loads.
+    const bool counting = have_desc && desc[kDescTok] >= 0;
+    auto token_of = [&](int i) {
+        if (counting) return desc[kDescTok] + i;
+        return p.token_index ? uniform_load(p.token_index + first + i) : first + i;
+    };
+    auto pos_of = [&](int i) { return counting ? desc[5] + i : uniform_load(p.positions + token_of(i)); };
+    const int seq = have_desc ? desc[4] : uniform_load(p.token_seq + token_of(0));
     const int32_t *table = p.tables + static_cast<int64_t>(seq) * p.max_blocks;
 
     // Per-row positions (for masking and RoPE); the page range needs only the
@@ -401,9 +416,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     int min_pos = INT_MAX, max_pos = -1;
 #pragma unroll
     for (int row = 0; row < ROWS; row++) {
-        const int li = first + src_row(row) / G;
-        const int t = p.token_index ? uniform_load(p.token_index + li) : li;
-        row_pos[row] = uniform_load(p.positions + t);
+        row_pos[row] = pos_of(src_row(row) / G);
         min_pos = min(min_pos, row_pos[row]);
         max_pos = max(max_pos, row_pos[row]);
     }
@@ -433,11 +446,29 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
     auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
     const uint32_t lane_off = 8u * sizeof(T) * static_cast<uint32_t>(lane);
-    auto fetch = [&](PageRegs<T> &pr, int j) {
-        const int blk = uniform_load(table + min(page_of(j), last_page));  // a scalar load
+    // The split's block ids, lane k holding page first_page + k: one vector
+    // load, issued before any page load and read back per page with
+    // v_readlane, so no page load waits on a scalar load of the table (under a
+    // full memory queue each such round trip costs microseconds). A split has
+    // at most 64 pages (split_len <= 1024, checked by the launcher).
+    const int tv = first_page + lane <= last_page ? table[first_page + lane] : -1;
+    auto block_at = [&](int page) { return __builtin_amdgcn_readlane(tv, page - first_page); };  // page in the split
+    auto fetch_block = [&](PageRegs<T> &pr, int j, int blk) {
         const bool live = j < n && in_pool(blk);
         const int64_t off = static_cast<int64_t>(live ? blk : 0) * block_stride + head_off;
         load_page(pr, kbase + off, vbase + off, lane_off, live);
+    };
+    auto fetch = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_at(min(page_of(j), last_page))); };
+    // A wave's first page, whose block id the descriptor holds: the work-group
+    // issues it right after the descriptor load.
+    auto fetch_first = [&](PageRegs<T> &pr) {
+        if (!have_desc) return fetch(pr, 0);
+        const int rel = min(wave, last_page - first_page);
+        int blk = desc[kDescBlocks];
+        blk = rel == 1 ? desc[kDescBlocks + 1] : blk;
+        blk = rel == 2 ? desc[kDescBlocks + 2] : blk;
+        blk = rel == 3 ? desc[kDescBlocks + 3] : blk;
+        fetch_block(pr, 0, blk);
     };
 
     QSlice<T> q[Q_LDS ? 1 : ROWS];
@@ -454,10 +485,10 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     if constexpr (!FUSED) {
         if constexpr (Q_LDS) {
             // rows' q vectors into LDS, 8 elements per thread at a time
-            for (int idx = static_cast<int>(threadIdx.x); idx < nrows * (D / 8); idx += kThreads) {
+            for (int idx = tid; idx < nrows * (D / 8); idx += kThreads) {
                 const int row = idx / (D / 8), d8 = (idx % (D / 8)) * 8;
-                const int li = first + row / G;
-                const int t = p.token_index ? p.token_index[li] : li;
+                const int li = first + row / G;  // per thread: a vector load when looked up
+                const int t = counting ? desc[kDescTok] + row / G : p.token_index ? p.token_index[li] : li;
                 const T *src = static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + kvh * G + row % G) * D + d8;
 #pragma unroll
                 for (int e = 0; e < 8; e++) q_lds[row][d8 + e] = src[e];
@@ -465,13 +496,12 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         } else {
 #pragma unroll
             for (int row = 0; row < ROWS; row++) {
-                const int li = first + src_row(row) / G;
-                const int t = p.token_index ? uniform_load(p.token_index + li) : li;
+                const int t = token_of(src_row(row) / G);
                 const int head = kvh * G + src_row(row) % G;
                 load_q(q[row], static_cast<const T *>(p.q) + (static_cast<int64_t>(t) * p.n_heads + head) * D + 8 * c);
             }
         }
-        fetch(A, 0);
+        fetch_first(A);
         if constexpr (Q_LDS) __syncthreads();
     } else {
         // q of every row and the new K/V in this split, one head vector per
@@ -481,20 +511,19 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         // it waits for LDS only, not for the pages.
         const int n_total = p.n_heads + 2 * p.n_kv;
         const T *qkv = static_cast<const T *>(p.qkv);
-        auto token = [&](int i) { return p.token_index ? uniform_load(p.token_index + first + i) : first + i; };
         auto vec = [&](int t, int head) { return qkv + (static_cast<int64_t>(t) * n_total + head) * D; };
         const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
 
         const int row0 = min(wave, nrows - 1), i0 = min(wave, nq - 1);
-        const int qt0 = token(row0 / G), kt0 = token(i0);
-        const int qpos0 = uniform_load(p.positions + qt0), kpos0 = uniform_load(p.positions + kt0);
+        const int qt0 = token_of(row0 / G), kt0 = token_of(i0);
+        const int qpos0 = pos_of(row0 / G), kpos0 = pos_of(i0);
         const T *qs0 = vec(qt0, kvh * G + row0 % G), *ks0 = vec(kt0, kh), *vs0 = vec(kt0, vh);
         const T q0a = qs0[lane], q0b = qs0[lane + D / 2];
         const T k0a = ks0[lane], k0b = ks0[lane + D / 2], v0a = vs0[lane], v0b = vs0[lane + D / 2];
         const NormRopeLane qn = norm_rope_lane(p.q_norm, p.inv_freq, lane);
         const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
 
-        fetch(A, 0);
+        fetch_first(A);
 
         auto put_q = [&](int row, float x0, float x1, int pos) {
             const int head = kvh * G + row % G;
@@ -519,7 +548,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
             new_k[i][lane + D / 2] = ek1;
             new_v[i][lane] = ev0;
             new_v[i][lane + D / 2] = ev1;
-            const int blk = uniform_load(table + pos / kPage);
+            const int blk = block_at(pos / kPage);  // the token's page lies in this split
             if (in_pool(blk)) {
                 const int64_t off = static_cast<int64_t>(blk) * block_stride + head_off + (pos % kPage) * D;
                 T *kd = const_cast<T *>(kbase) + off;
@@ -535,13 +564,12 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
 
         if (wave < nrows) put_q(row0, to_f32(q0a), to_f32(q0b), qpos0);
         for (int row = wave + kWaves; row < nrows; row += kWaves) {
-            const int t = token(row / G);
-            const T *s = vec(t, kvh * G + row % G);
-            put_q(row, to_f32(s[lane]), to_f32(s[lane + D / 2]), uniform_load(p.positions + t));
+            const T *s = vec(token_of(row / G), kvh * G + row % G);
+            put_q(row, to_f32(s[lane]), to_f32(s[lane + D / 2]), pos_of(row / G));
         }
         if (wave < nq && in_split(kpos0)) put_kv(i0, to_f32(k0a), to_f32(k0b), to_f32(v0a), to_f32(v0b), kpos0);
         for (int i = wave + kWaves; i < nq; i += kWaves) {
-            const int t = token(i), pos = uniform_load(p.positions + t);
+            const int t = token_of(i), pos = pos_of(i);
             if (!in_split(pos)) continue;
             const T *ks = vec(t, kh), *vs = vec(t, vh);
             put_kv(i, to_f32(ks[lane]), to_f32(ks[lane + D / 2]), to_f32(vs[lane]), to_f32(vs[lane + D / 2]), pos);
@@ -641,6 +669,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     // serves runs that break that bound.
     const int fast_end = min_pos / kPage;
     const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
+    __builtin_amdgcn_s_setprio(0);
     int j = 0;
     for (; j + 2 <= n_fast; j += 2) {
         fetch(B, j + 1);
@@ -683,7 +712,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     // Merge the waves in order 0..3, then write the output (a run with one
     // split) or this split's partial.
     const bool direct = p.counters ? run_splits == 1 : p.num_splits == 1;
-    for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
+    for (int idx = tid; idx < nrows * D; idx += kThreads) {
         const int row = idx / D, d = idx % D;
         float M = -INFINITY;
 #pragma unroll
@@ -699,7 +728,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
         const int li = first + row / G;
         const int head = kvh * G + row % G;
         if (direct) {
-            const int t = p.token_index ? p.token_index[li] : li;
+            const int t = counting ? desc[kDescTok] + row / G : p.token_index ? p.token_index[li] : li;
             T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
             o[d] = from_f32<T>(L > 0.0f ? O / L : 0.0f);
         } else {
@@ -720,7 +749,7 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     // launch. Nothing waits on another work-group.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         uint32_t *counter = p.counters + static_cast<int64_t>(run) * p.n_kv + kvh;
         const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_here = before + 1 == static_cast<uint32_t>(run_splits);
@@ -728,16 +757,21 @@ __global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) 
     }
     __syncthreads();
     if (!merge_here) return;
-    for (int idx = static_cast<int>(threadIdx.x); idx < nrows * D; idx += kThreads) {
+    for (int idx = tid; idx < nrows * D; idx += kThreads) {
         const int row = idx / D, d = idx % D;
         const int li = first + row / G, head = kvh * G + row % G;
         int pos = row_pos[0];
 #pragma unroll
         for (int k = 1; k < ROWS; k++) pos = row == k ? row_pos[k] : pos;
-        const int t = p.token_index ? p.token_index[li] : li;
+        const int t = counting ? desc[kDescTok] + row / G : p.token_index ? p.token_index[li] : li;
         T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
         merge_one<T>(p, li, head, d, min(pos + 1, p.max_blocks * kPage), o);
     }
+}
+
+template <typename T, int ROWS, bool FUSED>
+__global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
+    decode_item<T, ROWS, FUSED>(p, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
 }
 
 // The split merge as its own launch: one work-group per (token, head).

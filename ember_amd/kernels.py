@@ -268,11 +268,18 @@ def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_l
         keep.append(w_dev)
         a.work, a.num_work = w_dev.data_ptr(), int(items.shape[0])
         if work_desc:
-            desc = np.zeros((items.shape[0], 8), np.int32)
+            desc = np.full((items.shape[0], 16), -1, np.int32)
             for i, (r, sp) in enumerate(items.tolist()):
                 toks = tl[rf[r]:rf[r] + rc[r]]
-                desc[i, :7] = (r, sp, rf[r], rc[r], ints.token_seq[toks[0]], ints.positions[toks].min(),
-                               ints.positions[toks].max())
+                pos = ints.positions[toks]
+                seq = int(ints.token_seq[toks[0]])
+                counting = (np.diff(toks) == 1).all() and (np.diff(pos) == 1).all()
+                desc[i, :8] = (r, sp, rf[r], rc[r], seq, pos.min(), pos.max(), toks[0] if counting else -1)
+                p0 = sp * split_len // BLOCK_SIZE
+                last = min(int(pos.max()) + 1, (sp + 1) * split_len) - 1
+                for j in range(8):
+                    if p0 + j <= last // BLOCK_SIZE:
+                        desc[i, 8 + j] = ints.block_tables[seq, p0 + j]
             d_dev = _ints(desc.reshape(-1), dev)
             keep.append(d_dev)
             a.work_desc = d_dev.data_ptr()

@@ -37,10 +37,11 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 2
+#define EMBER_ABI_VERSION 3
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
+#define EMBER_MAX_SPLIT_LEN 1024 /* keys per decode split at most: a split's block ids fit one 64-lane register */
 
 #define EMBER_OK 0
 #define EMBER_ERR_INVALID (-1)
@@ -85,7 +86,7 @@ typedef struct EmberAttnArgs {
     float scale;
     void *out;                    /* [*, n_heads, head_dim] */
     int32_t num_splits;           /* context chunks per token: 1 = no split */
-    int32_t split_len;            /* keys per chunk, a multiple of 16 */
+    int32_t split_len;            /* keys per chunk, a multiple of 16, at most EMBER_MAX_SPLIT_LEN */
     float *part_acc;              /* [T, n_heads, num_splits, head_dim], indexed by list position 0..T-1 */
     float *part_ml;               /* [T, n_heads, num_splits, 2] */
     /* additions */
@@ -113,11 +114,16 @@ typedef struct EmberAttnArgs {
      * the merge kernel, so no second launch is needed. NULL = a separate
      * merge kernel when num_splits > 1. */
     uint32_t *merge_counters;
-    /* Optional, with `work`: what the plan already knows of each item, 8 ints
-     * per item {run, split, run_first[run], run_count[run], sequence of the
-     * run, lowest position, highest position, 0}, [8 * num_work]. A
-     * work-group then reaches its first page load after one descriptor load
-     * and one block-table load, instead of the chain run -> run_first ->
+    /* Optional, with `work`: what the plan already knows of each item, 16
+     * ints per item, [16 * num_work]:
+     *   0 run, 1 split, 2 run_first[run], 3 run_count[run], 4 sequence of the
+     *   run, 5 lowest position, 6 highest position,
+     *   7 token_index[run_first[run]] if the run's entries name tokens t, t+1,
+     *     ... at positions lowest, lowest+1, ... (else -1),
+     *   8..15 block ids of the split's pages 0..7 (split * split_len / 16 + i
+     *     of the sequence's table; -1 past the split's last page).
+     * A work-group then issues its first page loads right after one
+     * descriptor load, instead of after the chain run -> run_first ->
      * token_index -> token_seq / positions -> table. It must agree with the
      * other arrays (not checked). NULL = looked up as above. */
     const int32_t *work_desc;
@@ -245,7 +251,7 @@ typedef struct EmberKvConfig {
     int32_t max_seqs;         /* sequences per step */
     int32_t dtype;            /* EMBER_DTYPE_* of activations and pools */
     int32_t qk_norm;          /* nonzero: q_norm / k_norm weights are given per layer */
-    int32_t split_len;        /* keys per decode split, multiple of 16 (0 = 512) */
+    int32_t split_len;        /* keys per decode split, multiple of 16 up to EMBER_MAX_SPLIT_LEN (0 = 512) */
 } EmberKvConfig;
 
 /* Replaces ember::StepBatch (src/backend/backend.hpp:56-76); host arrays. */

@@ -47,6 +47,9 @@ def test_launchers_reject_bad_arguments_without_a_gpu():
     at.n_kv, at.max_blocks, at.num_blocks, at.T, at.num_splits, at.split_len = 8, 4, 4, 1, 1, 24
     assert lib.ember_hip_paged_decode(at, None) == _lib.ERR_INVALID  # split_len not a multiple of 16
     assert "split_len" in _lib.last_error()
+    at.split_len = _lib.MAX_SPLIT_LEN + 16  # a split's block ids must fit one 64-lane register
+    assert lib.ember_hip_paged_decode(at, None) == _lib.ERR_INVALID
+    assert "split_len" in _lib.last_error()
     pf = _lib.PrefillArgs()
     pf.head_dim, pf.n_heads, pf.n_kv, pf.dtype = 128, 16, 8, _lib.DTYPE_F32
     assert lib.ember_hip_prefill_attn(pf, None) == _lib.ERR_INVALID

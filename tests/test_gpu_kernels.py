@@ -142,7 +142,7 @@ def _run_decode(q, kp, vp, step, NB, device, **kw):
 
 
 @pytest.mark.parametrize("split_len,work", [(16, False), (64, True), (512, False), (512, True), (512, "pairs"),
-                                            (8192, False)])
+                                            (1024, False), (1024, True)])
 def test_decode_f32_matches_oracle(rng, device, split_len, work):
     """work: False = dense grid; True = sorted work list with the plan's per-item descriptors; "pairs" = the
     work list alone (the kernel looks each item up)."""
@@ -218,6 +218,15 @@ def test_verify_run_equals_sequential_decode(rng, device, dtype):
     seq = _run_decode(q, kp, vp, step, NB, device).cpu().numpy()  # one run per token
     assert np.array_equal(verify.view(np.uint8), seq.view(np.uint8))
     listed = _run_decode(q, kp, vp, step, NB, device, runs=runs, use_work_list=True).cpu().numpy()
+    assert np.array_equal(listed.view(np.uint8), seq.view(np.uint8))
+    # runs whose entries count down: the descriptors cannot give tokens and positions arithmetically, so the
+    # kernel looks each one up
+    tl = np.concatenate([np.arange(a, b)[::-1] for a, b in zip(step.query_start[:-1], step.query_start[1:])])
+    down = (np.arange(0, step.T, n, dtype=np.int32), np.full(len(base), n, np.int32))
+    listed = _run_decode(q, kp, vp, step, NB, device, token_list=tl, runs=down, use_work_list=True).cpu().numpy()
+    assert np.array_equal(listed.view(np.uint8), seq.view(np.uint8))
+    # the split merge in the last work-group of each (run, kv head)
+    listed = _run_decode(q, kp, vp, step, NB, device, runs=runs, use_work_list=True, merge_in_kernel=True).cpu().numpy()
     assert np.array_equal(listed.view(np.uint8), seq.view(np.uint8))
     # runs of 2 and 3 too
     for m in (2, 3, 8):
