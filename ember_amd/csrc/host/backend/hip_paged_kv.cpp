@@ -287,11 +287,13 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     put(work_desc_.data(), work_desc_.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
     // The copy waits for the kernels that last read this buffer (two plans ago),
-    // then runs beside stream_'s work; this step's kernels wait for the copy.
+    // then runs beside stream_'s work. The host, not stream_, waits for it:
+    // the host is normally a step ahead, so the wait costs it little, while a
+    // cross-stream wait on stream_ idles the GPU for about 10 us per step.
     EMBER_HIP_CHECK(hipStreamWaitEvent(upload_stream_, consumed_[stage_], 0));
     EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, upload_stream_));
     EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], upload_stream_));
-    EMBER_HIP_CHECK(hipStreamWaitEvent(stream_, staged_[stage_], 0));
+    EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));
     d_positions_ = dp + at[0];
     d_token_seq_ = dp + at[1];
     d_tables_ = dp + at[2];

@@ -272,7 +272,10 @@ EmberPagedKv *ember_kv_create(const EmberKvConfig *cfg, void *stream);
 void ember_kv_destroy(EmberPagedKv *kv);
 /* Packs the step's integers, routes runs of >= 16 new tokens to prefill tiles
  * and the rest to decode runs, fixes the splits and uploads the plan with one
- * host-to-device copy (cuda_backend.cu:153-205). */
+ * host-to-device copy (cuda_backend.cu:153-205). The copy runs on a side
+ * stream once the kernels of the plan before the previous one are done; the
+ * call returns when it has landed (so it blocks while the GPU is more than a
+ * step behind), and the stream then needs no cross-stream wait. */
 int32_t ember_kv_plan(EmberPagedKv *kv, const EmberStepBatch *batch);
 /* One layer of the planned step: append K/V of every new token, then attention
  * for every token into out [num_tokens, n_heads, head_dim] (cuda_backend.cu:357-361). */
