@@ -25,8 +25,9 @@
 //   values: each lane accumulates its 8 dims over its 4 keys.
 // Latency: a work-group's first page loads depend on one descriptor load only
 // (the descriptor carries the first block ids), the split's other block ids
-// arrive in one vector load next to them, and each wave keeps its next page in
-// flight in registers while it works on the current one.
+// arrive in one vector load next to them, and each wave loads the next page's
+// keys while it computes the current page's values, and the next page's values
+// while it computes the next page's scores.
 // At the end: rows merge through two lane exchanges, waves through LDS, and
 // splits either in the separate merge kernel or, with merge counters, in the
 // last work-group of the (run, kv head) to finish - all in one fixed order.
@@ -123,24 +124,23 @@ __device__ __forceinline__ uint4 load_desc(__amdgpu_buffer_rsrc_t d, uint32_t of
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <typename T>
-__device__ __forceinline__ void load_page(PageRegs<T> &pr, const T *kp, const T *vp, uint32_t lane_off, bool live) {
-    constexpr uint32_t kStep = 512 * sizeof(T);        // bytes between a lane's four slices of the page
-    constexpr int kBytes = kPage * kHeadDim * sizeof(T);  // one page of one kv head
-    const __amdgpu_buffer_rsrc_t dk = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(kp), 0, live ? kBytes : 0, kDescWord3);
-    const __amdgpu_buffer_rsrc_t dv = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(vp), 0, live ? kBytes : 0, kDescWord3);
+// One half of a page of one kv head (its 16 keys, or its 16 values) into
+// regs[4]: four loads per lane, load i covering bytes [1024 i, 1024 i + 1024)
+// of the half (f16), lane l at offset 16 l.
+template <typename T, typename R>
+__device__ __forceinline__ void load_half(R (&regs)[4], const T *base, uint32_t lane_off, bool live) {
+    constexpr uint32_t kStep = 512 * sizeof(T);        // bytes between a lane's four slices of the half
+    constexpr int kBytes = kPage * kHeadDim * sizeof(T);  // one half-page of one kv head
+    const __amdgpu_buffer_rsrc_t d = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(base), 0, live ? kBytes : 0,
+                                                                       kDescWord3);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (sizeof(T) == 2) {
-            pr.k[i] = load_desc(dk, lane_off + kStep * i);
-            pr.v[i] = load_desc(dv, lane_off + kStep * i);
+            regs[i] = load_desc(d, lane_off + kStep * i);
         } else {
-            const uint4 k0 = load_desc(dk, lane_off + kStep * i), k1 = load_desc(dk, lane_off + kStep * i + 16);
-            const uint4 v0 = load_desc(dv, lane_off + kStep * i), v1 = load_desc(dv, lane_off + kStep * i + 16);
-            pr.k[i][0] = make_float4(__uint_as_float(k0.x), __uint_as_float(k0.y), __uint_as_float(k0.z), __uint_as_float(k0.w));
-            pr.k[i][1] = make_float4(__uint_as_float(k1.x), __uint_as_float(k1.y), __uint_as_float(k1.z), __uint_as_float(k1.w));
-            pr.v[i][0] = make_float4(__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w));
-            pr.v[i][1] = make_float4(__uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w));
+            const uint4 x = load_desc(d, lane_off + kStep * i), y = load_desc(d, lane_off + kStep * i + 16);
+            regs[i][0] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z), __uint_as_float(x.w));
+            regs[i][1] = make_float4(__uint_as_float(y.x), __uint_as_float(y.y), __uint_as_float(y.z), __uint_as_float(y.w));
         }
     }
 }
@@ -453,12 +453,17 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     // at most 64 pages (split_len <= 1024, checked by the launcher).
     const int tv = first_page + lane <= last_page ? table[first_page + lane] : -1;
     auto block_at = [&](int page) { return __builtin_amdgcn_readlane(tv, page - first_page); };  // page in the split
-    auto fetch_block = [&](PageRegs<T> &pr, int j, int blk) {
+    // The wave's page j: its keys, its values, or both, into pr.
+    auto fetch_block = [&](PageRegs<T> &pr, int j, int blk, bool keys, bool values) {
         const bool live = j < n && in_pool(blk);
         const int64_t off = static_cast<int64_t>(live ? blk : 0) * block_stride + head_off;
-        load_page(pr, kbase + off, vbase + off, lane_off, live);
+        if (keys) load_half(pr.k, kbase + off, lane_off, live);
+        if (values) load_half(pr.v, vbase + off, lane_off, live);
     };
-    auto fetch = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_at(min(page_of(j), last_page))); };
+    auto block_of = [&](int j) { return block_at(min(page_of(j), last_page)); };
+    auto fetch = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_of(j), true, true); };
+    auto fetch_keys = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_of(j), true, false); };
+    auto fetch_values = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_of(j), false, true); };
     // A wave's first page, whose block id the descriptor holds: the work-group
     // issues it right after the descriptor load.
     auto fetch_first = [&](PageRegs<T> &pr) {
@@ -468,7 +473,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         blk = rel == 1 ? desc[kDescBlocks + 1] : blk;
         blk = rel == 2 ? desc[kDescBlocks + 2] : blk;
         blk = rel == 3 ? desc[kDescBlocks + 3] : blk;
-        fetch_block(pr, 0, blk);
+        fetch_block(pr, 0, blk, true, true);
     };
 
     QSlice<T> q[Q_LDS ? 1 : ROWS];
@@ -480,7 +485,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
     }
-    PageRegs<T> A, B;
+    PageRegs<T> A;
 
     if constexpr (!FUSED) {
         if constexpr (Q_LDS) {
@@ -589,12 +594,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     // MASKED = false: every key of the page is visible to every row (the page
     // lies below the run's lowest position). MASKED = true: per-row visibility,
     // with selects, so a hidden key leaves a row's state bit-for-bit unchanged;
-    // for a fully visible page both forms compute the same bits.
-    auto process = [&](const PageRegs<T> &pr, int page, auto masked_tag) {
+    // for a fully visible page both forms compute the same bits. The two halves
+    // read only pr.k and only pr.v, so a wave can load the next page's keys
+    // between them.
+    auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, float (&pj)[ROWS][4], bool (&vis)[ROWS][4]) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
-        float pj[ROWS][4];
-        bool vis[ROWS][4];
 #pragma unroll
         for (int row = 0; row < ROWS; row++) {
             QSlice<T> qrow;
@@ -619,6 +624,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
             m[row] = mn;
         }
+    };
+    auto values = [&](const PageRegs<T> &pr, auto masked_tag, const float (&pj)[ROWS][4], const bool (&vis)[ROWS][4]) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             float vf[8];
@@ -652,44 +660,43 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
                 }
             }
         }
-        process(pr, page, Masked{});
+        float pj[ROWS][4];
+        bool vis[ROWS][4];
+        scores(pr, page, Masked{}, pj, vis);
+        values(pr, Masked{}, pj, vis);
     };
 
-    // The page walk is a two-stage pipeline: each wave loads its next page
-    // while it computes on the current one. (At 115 VGPRs the kernel keeps
-    // four work-groups per CU, and 16 waves with one page in flight each
-    // stream as fast as 12 waves with two, which cost 32 more VGPRs.)
+    // The page walk: each wave holds one page in registers and loads the next
+    // page's keys once this page's scores are done, its values once this
+    // page's values are done, so half a page is in flight while the wave
+    // computes. With 16 waves per CU that keeps the memory system as busy as
+    // two whole pages per wave did, with shorter queues (and 32 fewer VGPRs).
     // The wave's fast pages come first (pages below min_pos / 16 hold no new key
     // and only keys every row sees); they run through a loop with no masking.
-    // What is left is short: the loop stops with at most one fast page to go,
-    // and the run's positions (at most EMBER_MAX_RUN, consecutive) lie in at
-    // most two adjacent pages, of which a wave (stride 4 pages) gets at most
-    // one. So at most two pages remain, one already in flight, and they go
-    // through the masked path as straight-line code; the loop after it only
-    // serves runs that break that bound.
+    // The rest (the run's positions, at most EMBER_MAX_RUN and consecutive, lie
+    // in at most two adjacent pages, of which a wave at stride 4 gets at most
+    // one) goes through the masked path.
     const int fast_end = min_pos / kPage;
     const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
     __builtin_amdgcn_s_setprio(0);
     int j = 0;
-    for (; j + 2 <= n_fast; j += 2) {
-        fetch(B, j + 1);
+    for (; j < n_fast; j++) {
+        float pj[ROWS][4];
+        bool vis[ROWS][4];
+        scores(A, page_of(j), Fast{}, pj, vis);
         phase_break();
-        process(A, page_of(j), Fast{});
+        fetch_keys(A, j + 1);
         phase_break();
-        fetch(A, j + 2);
+        values(A, Fast{}, pj, vis);
         phase_break();
-        process(B, page_of(j + 1), Fast{});
+        fetch_values(A, j + 1);
         phase_break();
     }
-    fetch(B, j + 1);
-    phase_break();
-    if (j < n) consume(A, page_of(j));
-    phase_break();
-    if (j + 1 < n) consume(B, page_of(j + 1));
-    j += 2;
     for (; j < n; j++) {
-        fetch(A, j);
         consume(A, page_of(j));
+        phase_break();
+        fetch(A, j + 1);
+        phase_break();
     }
 
     // Merge the four DPP rows of the wave (rows 0+1 and 2+3, then the pairs).
