@@ -38,7 +38,7 @@ constexpr int kKeyBlock = 32;                     // keys per LDS block: two pag
 template <int HG>
 constexpr int kThreadsFor = 256 * HG;  // 4 waves per query head
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
-constexpr int kVRow = kKeyBlock + 8;              // LDS row of V^T (one dim), halves
+constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), halves: 18 dwords, rows 2 apart 4 banks apart
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
@@ -97,35 +97,63 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) o_acc[dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // A key block's K and V, fetched into registers (512 chunks of 8 halves
-    // each per block: one or two per thread) and later stored to LDS; keys past
-    // the tile's last position or in a block outside the pool are zeros.
+    // A key block's K and V, fetched into registers and later stored to LDS;
+    // keys past the tile's last position or in a block outside the pool are
+    // zeros. K: 512 chunks of 8 dims of one key (one or two per thread), stored
+    // as rows. V: 512 pieces of 4 keys x 2 dims (dims 2 dp, 2 dp + 1 of keys
+    // 4 kq .. 4 kq + 3), each one 4-byte load per key - a wave's load reads one
+    // 256-byte key row - regrouped into two 8-byte rows of V^T (dims x keys),
+    // so V is transposed without sub-dword LDS stores.
     constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kPThreads;
-    auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vv4)[kChunks]) {
+    auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-            const int chunk = tid + j * kPThreads, key = chunk / 16, d8 = (chunk % 16) * 8;
-            kv4[j] = make_uint4(0, 0, 0, 0);
-            vv4[j] = make_uint4(0, 0, 0, 0);
-            const int pos = kb * kKeyBlock + key;
-            if (kb < n_blocks && pos <= max_pos) {
-                const int blk = table[pos / kPage];
-                if (blk >= 0 && blk < a.num_blocks) {
-                    const int64_t off = ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos % kPage) * kHeadDim + d8;
-                    kv4[j] = *reinterpret_cast<const uint4 *>(kc + off);
-                    vv4[j] = *reinterpret_cast<const uint4 *>(vc + off);
+            const int chunk = tid + j * kPThreads;
+            {
+                const int key = chunk / 16, d8 = (chunk % 16) * 8;
+                kv4[j] = make_uint4(0, 0, 0, 0);
+                const int pos = kb * kKeyBlock + key;
+                if (kb < n_blocks && pos <= max_pos) {
+                    const int blk = table[pos / kPage];
+                    if (blk >= 0 && blk < a.num_blocks) {
+                        const int64_t off =
+                            ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos % kPage) * kHeadDim + d8;
+                        kv4[j] = *reinterpret_cast<const uint4 *>(kc + off);
+                    }
                 }
+            }
+            {
+                const int kq = chunk / 64, dp = chunk % 64;
+                const int pos0 = kb * kKeyBlock + 4 * kq;  // the quad's 4 keys share a page
+                uint32_t w[4] = {0, 0, 0, 0};
+                if (kb < n_blocks && pos0 <= max_pos) {
+                    const int blk = table[pos0 / kPage];
+                    if (blk >= 0 && blk < a.num_blocks) {
+                        const int64_t off =
+                            ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos0 % kPage) * kHeadDim + 2 * dp;
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            if (pos0 + e <= max_pos) w[e] = *reinterpret_cast<const uint32_t *>(vc + off + e * kHeadDim);
+                    }
+                }
+                vq[j] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
     };
-    auto stage = [&](int buf, const uint4 (&kv4)[kChunks], const uint4 (&vv4)[kChunks]) {
+    auto stage = [&](int buf, const uint4 (&kv4)[kChunks], const uint4 (&vq)[kChunks]) {
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-            const int chunk = tid + j * kPThreads, key = chunk / 16, d8 = (chunk % 16) * 8;
+            const int chunk = tid + j * kPThreads;
+            const int key = chunk / 16, d8 = (chunk % 16) * 8;
             *reinterpret_cast<uint4 *>(&k_lds[buf][key * kKRow + d8]) = kv4[j];
-            const f16x8 vh = __builtin_bit_cast(f16x8, vv4[j]);
-#pragma unroll
-            for (int i = 0; i < 8; i++) v_lds[buf][(d8 + i) * kVRow + key] = vh[i];
+            // vq = (key e: dim 2dp | dim 2dp+1 << 16), e = 0..3; v_perm picks halves.
+            const int kq = chunk / 64, dp = chunk % 64;
+            const uint2 lo = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x05040100u),
+                                        __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x05040100u));
+            const uint2 hi = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x07060302u),
+                                        __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x07060302u));
+            *reinterpret_cast<uint2 *>(&v_lds[buf][(2 * dp) * kVRow + 4 * kq]) = lo;
+            *reinterpret_cast<uint2 *>(&v_lds[buf][(2 * dp + 1) * kVRow + 4 * kq]) = hi;
         }
     };
 
