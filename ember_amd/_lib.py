@@ -22,6 +22,10 @@ OK = 0
 ERR_INVALID = -1
 DTYPE_F16 = 0
 DTYPE_F32 = 1
+EPILOGUE_STORE_F16 = 0
+EPILOGUE_STORE_F32 = 1
+EPILOGUE_ADD_F32 = 2
+EPILOGUE_SILU_MUL = 3
 
 
 class EmberError(RuntimeError):
@@ -88,7 +92,21 @@ class LayerIo(ctypes.Structure):
     _fields_ = [("qkv", c_void_p), ("q_norm", c_void_p), ("k_norm", c_void_p), ("bias", c_void_p), ("out", c_void_p)]
 
 
-STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, LayerIo]
+class GemvArgs(ctypes.Structure):
+    _fields_ = [
+        ("A", c_void_p), ("lda", c_int32), ("W", c_void_p), ("M", c_int32), ("N", c_int32), ("K", c_int32),
+        ("C", c_void_p), ("ldc", c_int32), ("epilogue", c_int32),
+    ]
+
+
+class NormArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", c_void_p), ("rows", c_void_p), ("R", c_int32), ("hidden", c_int32), ("w", c_void_p), ("eps", c_float),
+        ("out", c_void_p),
+    ]
+
+
+STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, LayerIo, GemvArgs, NormArgs]
 
 # name -> (restype, argtypes); every extern "C" symbol of include/ember_hip.h.
 PROTOTYPES = {
@@ -97,6 +115,8 @@ PROTOTYPES = {
     "ember_hip_decode_step": (c_int32, [POINTER(QkvArgs), POINTER(AttnArgs), c_void_p]),
     "ember_hip_prefill_attn": (c_int32, [POINTER(PrefillArgs), c_void_p]),
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
+    "ember_hip_gemv": (c_int32, [POINTER(GemvArgs), c_void_p]),
+    "ember_hip_rmsnorm_rows": (c_int32, [POINTER(NormArgs), c_void_p]),
     "ember_hip_last_error": (c_char_p, []),
     "ember_hip_abi_version": (c_int32, []),
     "ember_hip_sizeof": (c_int32, [c_int32]),

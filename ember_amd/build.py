@@ -26,6 +26,7 @@ SOURCES = [
     CSRC / "paged_decode.hip",
     CSRC / "prefill_attn.hip",
     CSRC / "copy_pages.hip",
+    CSRC / "linear.hip",
     CSRC / "host" / "kvcache" / "block_manager.cpp",
     CSRC / "host" / "backend" / "hip_paged_kv.cpp",
     CSRC / "host" / "capi_host.cpp",

@@ -62,6 +62,8 @@ int32_t ember_hip_sizeof(int32_t which) {
         case 4: return sizeof(EmberKvConfig);
         case 5: return sizeof(EmberStepBatch);
         case 6: return sizeof(EmberLayerIo);
+        case 7: return sizeof(EmberGemvArgs);
+        case 8: return sizeof(EmberNormArgs);
         default: return -1;
     }
 }
@@ -186,6 +188,35 @@ int ember_hip_copy_pages(const EmberCopyArgs *a, void *stream) {
     if (!a->k_cache || !a->v_cache || !a->src_blocks || !a->dst_blocks)
         return set_error(EMBER_ERR_INVALID, "copy_pages: a required pointer is null");
     return hip_status(launch_copy_pages(*a, static_cast<hipStream_t>(stream)), "copy_pages");
+}
+
+int ember_hip_gemv(const EmberGemvArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "gemv: null arguments");
+    if (a->M < 1 || a->M > 64) return set_error(EMBER_ERR_INVALID, "gemv: M must be 1..64 (got %d)", a->M);
+    if (a->N < 1 || a->K < 32 || a->K % 32 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv: N >= 1 and K a positive multiple of 32 (got N %d, K %d)", a->N, a->K);
+    if (a->epilogue < EMBER_EPILOGUE_STORE_F16 || a->epilogue > EMBER_EPILOGUE_SILU_MUL)
+        return set_error(EMBER_ERR_INVALID, "gemv: unknown epilogue %d", a->epilogue);
+    if (a->epilogue == EMBER_EPILOGUE_SILU_MUL && a->N % 2 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv: silu_mul needs an even N (got %d)", a->N);
+    const int cols = a->epilogue == EMBER_EPILOGUE_SILU_MUL ? a->N / 2 : a->N;
+    if (a->lda < a->K || a->lda % 8 != 0 || a->ldc < cols)
+        return set_error(EMBER_ERR_INVALID, "gemv: lda must be >= K and a multiple of 8, ldc >= %d (got %d, %d)", cols,
+                         a->lda, a->ldc);
+    if (!a->A || !a->W || !a->C) return set_error(EMBER_ERR_INVALID, "gemv: a required pointer is null");
+    if (reinterpret_cast<uintptr_t>(a->A) % 16 != 0 || reinterpret_cast<uintptr_t>(a->W) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv: A and W must be 16-byte aligned");
+    return hip_status(launch_gemv(*a, static_cast<hipStream_t>(stream)), "gemv");
+}
+
+int ember_hip_rmsnorm_rows(const EmberNormArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "rmsnorm_rows: null arguments");
+    if (a->R < 0 || a->hidden < 1) return set_error(EMBER_ERR_INVALID, "rmsnorm_rows: bad sizes");
+    if (a->R == 0) return EMBER_OK;
+    if (!a->x || !a->w || !a->out) return set_error(EMBER_ERR_INVALID, "rmsnorm_rows: a required pointer is null");
+    return hip_status(launch_rmsnorm_rows(*a, static_cast<hipStream_t>(stream)), "rmsnorm_rows");
 }
 
 }  // extern "C"

@@ -32,6 +32,10 @@ hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream);
 
 hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
 
+hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream);
+
+hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream);
+
 // Row capacities with a built decode kernel, ascending.
 constexpr int kDecodeRowInstances[] = {1, 2, 4, 8, 10, 16};
 

@@ -345,3 +345,40 @@ def copy_pages(k_pool, v_pool, src, dst, *, n_layers, layer_stride, n_kv, num_bl
     a.num_blocks, a.dtype = num_blocks, _dtype_code(k_pool)
     check(_lib.lib().ember_hip_copy_pages(a, _stream_handle(stream)), "copy_pages")
     return (sd, dd)
+
+
+def gemv(a, w, c, epilogue: int, stream=None):
+    """C = A . W^T for decode-sized batches (≙ cuda::gemm with GemmKernel::gemv_tc, k_gemm.cu:302-425).
+
+    a: f16 [M, K] (M <= 64, K a multiple of 32); w: f16 [N, K]; c: per epilogue, f16 [M, N] (store_f16),
+    f32 [M, N] (store_f32; add_f32 adds into it) or f16 [M, N / 2] (silu_mul, W rows interleaving gate and up).
+    """
+    if a.dtype != torch.float16 or w.dtype != torch.float16 or a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
+        raise EmberError("gemv: a [M, K] and w [N, K] must be f16 with the same K")
+    M, K = a.shape
+    N = w.shape[0]
+    cols = N // 2 if epilogue == _lib.EPILOGUE_SILU_MUL else N
+    want = torch.float32 if epilogue in (_lib.EPILOGUE_STORE_F32, _lib.EPILOGUE_ADD_F32) else torch.float16
+    if c.dtype != want or tuple(c.shape) != (M, cols):
+        raise EmberError(f"gemv: c must be {want} [{M}, {cols}]")
+    g = _lib.GemvArgs()
+    g.A, g.lda, g.W, g.M, g.N, g.K = _dev(a, "a"), K, _dev(w, "w"), M, N, K
+    g.C, g.ldc, g.epilogue = _dev(c, "c"), cols, epilogue
+    check(_lib.lib().ember_hip_gemv(g, _stream_handle(stream)), "gemv")
+
+
+def rmsnorm_rows(x, w, out, eps: float, rows=None, stream=None):
+    """out[r] = rmsnorm(x[rows[r] if rows else r]) * w as f16 (≙ cuda::rmsnorm_rows, kernels.cuh:70-72)."""
+    if x.dtype != torch.float32 or w.dtype != torch.float32 or out.dtype != torch.float16:
+        raise EmberError("rmsnorm_rows: x and w f32, out f16")
+    hidden = x.shape[-1]
+    R = out.shape[0]
+    keep = []
+    n = _lib.NormArgs()
+    n.x, n.w, n.out, n.R, n.hidden, n.eps = _dev(x, "x"), _dev(w, "w"), _dev(out, "out"), R, hidden, eps
+    if rows is not None:
+        r = _ints(np.asarray(rows, np.int32), x.device)
+        keep.append(r)
+        n.rows = r.data_ptr()
+    check(_lib.lib().ember_hip_rmsnorm_rows(n, _stream_handle(stream)), "rmsnorm_rows")
+    return keep

@@ -189,12 +189,57 @@ typedef struct EmberCopyArgs {
 /* Copies whole pages (every layer, K and V, every kv head) from src to dst. */
 int ember_hip_copy_pages(const EmberCopyArgs *args, void *stream);
 
+/* The layer either side of the path: the input RMSNorm and the decode-sized
+ * linear layers (qkv projection into the append, output projection into the
+ * residual), in the reference's order (cuda_backend.cu:350-362). */
+
+/* Epilogues of ember_hip_gemv; the values of cuda::Epilogue (kernels.cuh:25-30). */
+#define EMBER_EPILOGUE_STORE_F16 0 /* C half [M, ldc], clamped to +-65504 */
+#define EMBER_EPILOGUE_STORE_F32 1 /* C float [M, ldc] */
+#define EMBER_EPILOGUE_ADD_F32 2   /* C float [M, ldc] += the product (the residual stream) */
+#define EMBER_EPILOGUE_SILU_MUL 3  /* W rows interleave gate/up; C half [M, ldc], C[m][j] = silu(gate j) * up j */
+
+/* The arguments of cuda::gemm (kernels.cuh:40-41), decode-sized. */
+typedef struct EmberGemvArgs {
+    const void *A;                /* f16 [M, lda] activations; 16-byte aligned rows */
+    int32_t lda;
+    const void *W;                /* f16 [N, K] weights, one output feature per row */
+    int32_t M, N, K;              /* M 1..64; K a multiple of 32 */
+    void *C;                      /* [M, ldc], f16 or f32 by epilogue */
+    int32_t ldc;
+    int32_t epilogue;             /* EMBER_EPILOGUE_* */
+} EmberGemvArgs;
+
+/* C[M, N] = A[M, K] . W[N, K]^T, f16 in, f32 accumulation, then the epilogue
+ * (silu_mul: N even, C has N / 2 columns). MFMA tiles of 16 features x 16
+ * tokens, 8 waves splitting K. Replaces cuda::gemm with GemmKernel::gemv_tc
+ * (kernels.cuh:40-41; k_gemm.cu:302-425, :462-485). */
+int ember_hip_gemv(const EmberGemvArgs *args, void *stream);
+
+/* The arguments of cuda::rmsnorm_rows (kernels.cuh:70-72). */
+typedef struct EmberNormArgs {
+    const float *x;               /* f32 [*, hidden] */
+    const int32_t *rows;          /* [R] rows of x, or NULL = rows 0..R-1 */
+    int32_t R, hidden;
+    const float *w;               /* [hidden] */
+    float eps;
+    void *out;                    /* f16 [R, hidden] */
+} EmberNormArgs;
+
+/* out[r] = w * (x[row r] * scale), scale = 1 / sqrt(sum of squares / hidden +
+ * eps), as f16 clamped to +-65504. The sum of squares is taken in double and
+ * the scale rounded once to f32, as the CPU backend does
+ * (cpu_backend.cpp:34-39). Replaces cuda::rmsnorm_rows (kernels.cuh:70-72;
+ * k_elementwise.cu:52-65). */
+int ember_hip_rmsnorm_rows(const EmberNormArgs *args, void *stream);
+
 /* Description of the last failure on this thread ("" if none). */
 const char *ember_hip_last_error(void);
 int ember_hip_abi_version(void);
 /* sizeof of each argument struct, for FFI bindings to check their layouts:
  * 0 EmberQkvArgs, 1 EmberAttnArgs, 2 EmberPrefillArgs, 3 EmberCopyArgs,
- * 4 EmberKvConfig, 5 EmberStepBatch, 6 EmberLayerIo; -1 otherwise. */
+ * 4 EmberKvConfig, 5 EmberStepBatch, 6 EmberLayerIo, 7 EmberGemvArgs,
+ * 8 EmberNormArgs; -1 otherwise. */
 int32_t ember_hip_sizeof(int32_t which);
 
 /* ---- 2. KV block manager ------------------------------------------------- */

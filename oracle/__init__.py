@@ -28,6 +28,7 @@ _PROTOS = {
     "ember_oracle_inv_freq": (None, [c_double, c_int32, _F32P]),
     "ember_oracle_rmsnorm": (None, [_F32P, _F32P, c_int32, c_float, _F32P]),
     "ember_oracle_rope": (None, [_F32P, c_int32, c_int32, _F32P]),
+    "ember_oracle_linear": (None, [_U16P, _U16P, c_int32, c_int32, c_int32, c_int32, _F32P, c_int32]),
     "ember_oracle_dot": (c_float, [_F32P, _F32P, c_int32]),
     "ember_oracle_cache_offset": (c_int64, [_I32P, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "ember_oracle_append_layer": (c_int32, [_F32P, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
@@ -117,6 +118,18 @@ def rmsnorm(x, w, eps: float) -> np.ndarray:
     x, w = _f32(x), _f32(w)
     out = np.empty_like(x)
     lib().ember_oracle_rmsnorm(_p(x, _F32P), _p(w, _F32P), x.size, eps, _p(out, _F32P))
+    return out
+
+
+def linear(a_f16, w_f16, epilogue: int, c=None) -> np.ndarray:
+    """C = A . W^T (f16 bits in, double sums, f32 out) with an epilogue; c is the f32 C that add_f32 adds to."""
+    a = np.ascontiguousarray(np.asarray(a_f16, np.float16)).view(np.uint16)
+    w = np.ascontiguousarray(np.asarray(w_f16, np.float16)).view(np.uint16)
+    M, K = a.shape
+    N = w.shape[0]
+    cols = N // 2 if epilogue == 3 else N
+    out = np.zeros((M, cols), np.float32) if c is None else np.array(c, np.float32, copy=True)
+    lib().ember_oracle_linear(_p(a, _U16P), _p(w, _U16P), M, N, K, epilogue, _p(out, _F32P), cols)
     return out
 
 

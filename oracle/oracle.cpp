@@ -350,6 +350,33 @@ void ember_oracle_rmsnorm(const float *x, const float *w, int32_t n, float eps, 
 
 void ember_oracle_rope(float *x, int32_t D, int32_t pos, const float *inv_freq) { rope(x, D, pos, inv_freq); }
 
+void ember_oracle_linear(const uint16_t *A, const uint16_t *W, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                         float *C, int32_t ldc) {
+    std::vector<float> a(static_cast<size_t>(K)), w(static_cast<size_t>(K));
+    std::vector<float> v(static_cast<size_t>(N));
+    for (int32_t m = 0; m < M; m++) {
+        for (int32_t k = 0; k < K; k++) a[static_cast<size_t>(k)] = ember_oracle_f16_to_f32(A[static_cast<size_t>(m) * K + k]);
+        for (int32_t n = 0; n < N; n++) {
+            double s = 0.0;
+            for (int32_t k = 0; k < K; k++)
+                s += static_cast<double>(a[static_cast<size_t>(k)]) *
+                     ember_oracle_f16_to_f32(W[static_cast<size_t>(n) * K + k]);
+            v[static_cast<size_t>(n)] = static_cast<float>(s);
+        }
+        float *row = C + static_cast<size_t>(m) * ldc;
+        if (epilogue == 3) {
+            for (int32_t j = 0; j < N / 2; j++) {
+                const float g = v[static_cast<size_t>(2 * j)], u = v[static_cast<size_t>(2 * j + 1)];
+                row[j] = g / (1.0f + std::exp(-g)) * u;
+            }
+        } else if (epilogue == 2) {
+            for (int32_t n = 0; n < N; n++) row[n] += v[static_cast<size_t>(n)];
+        } else {
+            for (int32_t n = 0; n < N; n++) row[n] = v[static_cast<size_t>(n)];
+        }
+    }
+}
+
 float ember_oracle_dot(const float *a, const float *b, int32_t n) { return dot(a, b, n); }
 
 int64_t ember_oracle_cache_offset(const int32_t *tables, int32_t max_blocks, int32_t num_blocks, int32_t n_kv,

@@ -34,6 +34,16 @@ void ember_oracle_inv_freq(double theta, int32_t head_dim, float *out);
  * Pinned: transformers' Qwen3RMSNorm; unit-weight outputs have unit RMS. */
 void ember_oracle_rmsnorm(const float *x, const float *w, int32_t n, float eps, float *out);
 
+/* C[M, N] = A[M, K] . W[N, K]^T from f16 bits, each dot product summed in double,
+ * then an epilogue (0 store: C = v; 1 store f32: C = v; 2 add f32: C += v;
+ * 3 silu_mul: C[m, j] = silu(v[m, 2j]) * v[m, 2j+1], N even), all in f32 after
+ * the double sum. Restates the reference's GEMM test reference
+ * (tests/test_cuda.cpp:27-47) and epilogues (src/backend/cuda/kernels.cuh:25-30).
+ * C is f32 [M, ldc] in every case (the caller rounds f16 outputs).
+ * Pinned: numpy float64 matmul, the identity weight, silu's closed form. */
+void ember_oracle_linear(const uint16_t *A, const uint16_t *W, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                         float *C, int32_t ldc);
+
 /* Rotate-half RoPE of one head vector in place (cpu_backend.cpp:262-272).
  * Pinned: transformers' apply_rotary_pos_emb; pos 0 is the identity; pair norms kept. */
 void ember_oracle_rope(float *x, int32_t head_dim, int32_t pos, const float *inv_freq);

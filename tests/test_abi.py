@@ -54,6 +54,21 @@ def test_launchers_reject_bad_arguments_without_a_gpu():
     pf.head_dim, pf.n_heads, pf.n_kv, pf.dtype = 128, 16, 8, _lib.DTYPE_F32
     assert lib.ember_hip_prefill_attn(pf, None) == _lib.ERR_INVALID
     assert lib.ember_hip_copy_pages(None, None) == _lib.ERR_INVALID
+    g = _lib.GemvArgs()
+    g.M, g.N, g.K, g.lda, g.ldc, g.epilogue = 65, 16, 64, 64, 16, 0  # M above 64
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    assert "M must be 1..64" in _lib.last_error()
+    g.M, g.K, g.lda = 4, 40, 40  # K not a multiple of 32
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    g.K, g.lda, g.N, g.epilogue = 64, 64, 15, _lib.EPILOGUE_SILU_MUL  # silu_mul needs an even N
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    assert "even N" in _lib.last_error()
+    g.N, g.epilogue = 16, 0  # null pointers
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    assert lib.ember_hip_rmsnorm_rows(None, None) == _lib.ERR_INVALID
+    n = _lib.NormArgs()
+    n.R, n.hidden = 2, 0
+    assert lib.ember_hip_rmsnorm_rows(n, None) == _lib.ERR_INVALID
     # T = 0 is a no-op, not an error
     at.split_len, at.T = 512, 0
     assert lib.ember_hip_paged_decode(at, None) == _lib.OK

@@ -411,3 +411,61 @@ def test_prefill_tile_is_independent_of_its_neighbours(rng, device):
         rest = np.ones(step.T, bool)
         rest[t[0]:t[1]] = False
         assert np.isnan(one.float().cpu().numpy()[rest]).all(), "a tile wrote outside its tokens"
+
+
+# ---- the layer either side: decode-sized linear layers and the input RMSNorm ----
+
+def _linear_err(got, want):
+    """The reference's GEMM test metric (tests/test_cuda.cpp:49-54): max |got - want| / max(1e-3, max |want|)."""
+    return float(np.abs(got.astype(np.float64) - want).max() / max(1e-3, float(np.abs(want).max())))
+
+
+@pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (8, 512, 1024), (13, 200, 128), (31, 384, 512),
+                                   (64, 256, 1024), (32, 4096, 2048), (32, 2048, 2048), (17, 48, 32)])
+@pytest.mark.parametrize("ep", [0, 1, 2, 3])
+def test_gemv_matches_oracle(device, M, N, KD, ep):
+    """Every epilogue on the reference test's decode-sized shapes (K a multiple of 32) and the Qwen3-1.7B
+    projections; ragged M and N exercise the clamped rows. Bound 2e-3 as in the reference's test."""
+    from ember_amd import _lib
+    rng = np.random.default_rng(M * 7919 + N * 31 + KD + ep)
+    a = (rng.standard_normal((M, KD))).astype(np.float16)
+    w = (rng.standard_normal((N, KD)) * 0.05).astype(np.float16)
+    cols = N // 2 if ep == _lib.EPILOGUE_SILU_MUL else N
+    f32 = ep in (_lib.EPILOGUE_STORE_F32, _lib.EPILOGUE_ADD_F32)
+    c0 = np.ones((M, cols), np.float32)
+    c = torch.from_numpy(c0).to(device) if f32 else torch.full((M, cols), float("nan"), dtype=torch.float16,
+                                                                 device=device)
+    K.gemv(torch.from_numpy(a).to(device), torch.from_numpy(w).to(device), c, ep)
+    torch.cuda.synchronize()
+    got = c.float().cpu().numpy()
+    want = oracle.linear(a, w, ep, c0 if ep == _lib.EPILOGUE_ADD_F32 else None)
+    assert np.isfinite(got).all()
+    assert _linear_err(got, want) < 2e-3
+
+
+def test_gemv_saturates_f16_outputs(device):
+    """store_f16 clamps to the finite f16 range instead of overflowing to inf (k_gemm.cu's to_half_sat)."""
+    a = np.full((2, 64), 100.0, np.float16)
+    w = np.full((16, 64), 50.0, np.float16)
+    w[1::2] *= -1
+    c = torch.empty((2, 16), dtype=torch.float16, device=device)
+    K.gemv(torch.from_numpy(a).to(device), torch.from_numpy(w).to(device), c, 0)
+    torch.cuda.synchronize()
+    assert c.float().cpu().numpy()[0, :2].tolist() == [65504.0, -65504.0]
+
+
+@pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (3, 4096)])
+def test_rmsnorm_rows_matches_oracle(device, R, hidden):
+    """f16 outputs within one f16 ulp of the oracle's f32 rows (cpu_backend.cpp:34-39; the GPU's double sum of
+    squares runs in another order), through a row list."""
+    rng = np.random.default_rng(R * 100 + hidden)
+    x = rng.standard_normal((R + 2, hidden)).astype(np.float32) * 3
+    w = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
+    rows = list(range(R + 1, 1, -1))[:R]
+    out = torch.full((R, hidden), float("nan"), dtype=torch.float16, device=device)
+    keep = K.rmsnorm_rows(torch.from_numpy(x).to(device), torch.from_numpy(w).to(device), out, 1e-6, rows=rows)
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    want = np.stack([oracle.rmsnorm(x[r], w, 1e-6) for r in rows])
+    np.testing.assert_allclose(got, want, rtol=2.0 ** -10, atol=2.0 ** -24)
+    del keep
