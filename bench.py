@@ -374,6 +374,80 @@ def run_config5(args) -> dict:
     }
 
 
+def run_linear(args) -> dict:
+    """The layer either side of the path at config 2's shape (32 tokens, Qwen3-1.7B: hidden 2048, q 16 x 128,
+    kv 8 x 128): the input RMSNorm, the qkv projection (N 4096, K 2048, f16 out) and the output projection
+    (N 2048, K 2048, added into the f32 residual), in the reference's order (cuda_backend.cu:350-362). Each
+    of the 28 layers has its own random weights (672 MB in all, more than the 256 MB last-level cache), so W
+    streams from HBM as in a real step. Kernels are timed with HIP events on the launching stream."""
+    import torch
+
+    from ember_amd import kernels as K
+
+    M, HID, NQKV = BATCH, H * D, (H + 2 * KVH) * D
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(SEED + 7)
+    w_qkv = [torch.randn((NQKV, HID), generator=g, device=dev, dtype=torch.float16) * 0.02 for _ in range(N_LAYERS)]
+    w_o = [torch.randn((HID, HID), generator=g, device=dev, dtype=torch.float16) * 0.02 for _ in range(N_LAYERS)]
+    norm_w = [torch.ones(HID, device=dev) for _ in range(N_LAYERS)]
+    h = torch.randn((M, HID), generator=g, device=dev)
+    xn = torch.empty((M, HID), device=dev, dtype=torch.float16)
+    qkv = torch.empty((M, NQKV), device=dev, dtype=torch.float16)
+    att = torch.randn((M, HID), generator=g, device=dev).half()
+    torch.cuda.synchronize()
+    names = ["rmsnorm_rows", "gemv qkv (store_f16)", "gemv o (add_f32)"]
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in names]
+          for _ in range(N_LAYERS)]
+
+    def layer(l, timed):
+        ops = [lambda: K.rmsnorm_rows(h, norm_w[l], xn, 1e-6),
+               lambda: K.gemv(xn, w_qkv[l], qkv, 0),
+               lambda: K.gemv(att, w_o[l], h, 2)]
+        for i, op in enumerate(ops):
+            if timed:
+                ev[l][i][0].record()
+            op()
+            if timed:
+                ev[l][i][1].record()
+
+    for _ in range(args.warmup):
+        for l in range(N_LAYERS):
+            layer(l, False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        for l in range(N_LAYERS):
+            layer(l, False)
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    tot = [0.0] * len(names)
+    for _ in range(args.steps):
+        for l in range(N_LAYERS):
+            layer(l, True)
+        torch.cuda.synchronize()
+        for l in range(N_LAYERS):
+            for i in range(len(names)):
+                tot[i] += ev[l][i][0].elapsed_time(ev[l][i][1])
+    us = [t / (args.steps * N_LAYERS) * 1e3 for t in tot]
+    bytes_ = [M * HID * 4 + HID * 4 + M * HID * 2,
+              NQKV * HID * 2 + M * HID * 2 + M * NQKV * 2,
+              HID * HID * 2 + M * HID * 2 + 2 * M * HID * 4]
+    kern = {n: {"avg_us": round(u, 2), "bytes": b_, "gbs": round(b_ / u / 1e3, 1),
+                "hbm_frac": round(b_ / u / 1e3 / HBM_PEAK_GBS, 4)} for n, u, b_ in zip(names, us, bytes_)}
+    gemv_bytes = bytes_[1] + bytes_[2]
+    gemv_gbs = gemv_bytes / (us[1] + us[2]) / 1e3
+    log(f"[bench] linear layers: {step_s * 1e3:.3f} ms per 28-layer pass; " +
+        "; ".join(f"{n} {k['avg_us']} us = {k['gbs']} GB/s" for n, k in kern.items()))
+    return {
+        "metric": "decode-size linear layers either side of the path: GB/s and % HBM peak (Qwen3-1.7B shape, "
+                  "32 tokens)",
+        "value": round(gemv_gbs, 1), "unit": "GB/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_hbm_frac": round(gemv_gbs / HBM_PEAK_GBS, 4), "kernels": kern,
+        "config": {"workload": "28 layers of rmsnorm_rows (32 x 2048) + qkv GEMV (4096 x 2048, f16 out) + "
+                               "o GEMV (2048 x 2048, added into the f32 residual), own random weights per layer"},
+    }
+
+
 def run_config3(args) -> dict:
     """a continuous-batching mixed step at Qwen3-1.7B shape. 64 sequences share one
     1024-token system prefix held in 64 sealed, refcounted pages (prefix cache: match_prefix). 4 of them
@@ -577,6 +651,8 @@ def main() -> int:
                     help="run each step as a replayed hipGraph of all layers (the timing pass stays eager)")
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
                     help="BASELINE config: 2 = the metric (default); 3, 4, 5 print their own line")
+    ap.add_argument("--linear", action="store_true",
+                    help="time the layer either side of the path (input RMSNorm, qkv and o GEMVs); its own line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size page copy used to scale the HBM byte counters")
     args = ap.parse_args()
@@ -586,15 +662,15 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.steps)
-    if args.config != 2:
+    if args.config != 2 or args.linear:
         import torch
 
         from ember_amd import lib
 
         lib()
         assert torch.cuda.is_available(), "bench.py needs a GPU"
-        log(f"[bench] BASELINE config {args.config}")
-        fn = {3: run_config3, 4: run_config4, 5: run_config5}[args.config]
+        log("[bench] linear layers" if args.linear else f"[bench] BASELINE config {args.config}")
+        fn = run_linear if args.linear else {3: run_config3, 4: run_config4, 5: run_config5}[args.config]
         line = fn(args)
         line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                      "vs_baseline": None, "dtype": "f16", "data": "synthetic, seeded"})
