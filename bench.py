@@ -48,7 +48,7 @@ def log(msg: str) -> None:
 class Workload:
     """Config 2 on the GPU path."""
 
-    def __init__(self, total_steps: int, split_len: int = 512, graph: bool = False):
+    def __init__(self, total_steps: int, split_len: int = 512, graph: bool = False, block: bool = False):
         import torch
 
         from ember_amd import BlockManager
@@ -99,6 +99,42 @@ class Workload:
         self.graph_io = [(self.qkv[layer], self.out, self.qn[layer], self.kn[layer], None) for layer in range(N_LAYERS)]
         self.sum_ctx_timed = 0
         self.alloc_s = 0.0
+        self.block = block
+        if block:
+            self._init_block(g)
+
+    def _init_block(self, g) -> None:
+        """The whole attention block per layer (input RMSNorm, qkv GEMV, append + attention, o GEMV into the f32
+        residual), with random weights of its own per layer (704 MB in all), called through the C ABI."""
+        import ctypes
+
+        from ember_amd import _lib
+
+        torch, HID, NQKV = self.torch, H * D, (H + 2 * KVH) * D
+        with torch.cuda.stream(self.stream):
+            self.w_qkv = [torch.randn((NQKV, HID), generator=g, device="cuda", dtype=torch.float16) * 0.02
+                          for _ in range(N_LAYERS)]
+            self.w_o = [torch.randn((HID, HID), generator=g, device="cuda", dtype=torch.float16) * 0.02
+                        for _ in range(N_LAYERS)]
+            self.in_norm = [torch.ones(HID, device="cuda") for _ in range(N_LAYERS)]
+            self.h = torch.randn((BATCH, HID), generator=g, device="cuda")
+            self.xn = torch.empty((BATCH, HID), device="cuda", dtype=torch.float16)
+            self.qkv_buf = torch.empty((BATCH, NQKV), device="cuda", dtype=torch.float16)
+        self.stream.synchronize()
+        self.block_args = []
+        for layer in range(N_LAYERS):
+            n = _lib.NormArgs()
+            n.x, n.w, n.out, n.R, n.hidden, n.eps = (self.h.data_ptr(), self.in_norm[layer].data_ptr(),
+                                                     self.xn.data_ptr(), BATCH, HID, 1e-6)
+            gq = _lib.GemvArgs()
+            gq.A, gq.lda, gq.W, gq.M, gq.N, gq.K = self.xn.data_ptr(), HID, self.w_qkv[layer].data_ptr(), BATCH, NQKV, HID
+            gq.C, gq.ldc, gq.epilogue = self.qkv_buf.data_ptr(), NQKV, _lib.EPILOGUE_STORE_F16
+            go = _lib.GemvArgs()
+            go.A, go.lda, go.W, go.M, go.N, go.K = self.out.data_ptr(), HID, self.w_o[layer].data_ptr(), BATCH, HID, HID
+            go.C, go.ldc, go.epilogue = self.h.data_ptr(), HID, _lib.EPILOGUE_ADD_F32
+            self.block_args.append((ctypes.byref(n), ctypes.byref(gq), ctypes.byref(go), n, gq, go,
+                                    self.qn[layer].data_ptr(), self.kn[layer].data_ptr()))
+        self.block_weight_bytes = N_LAYERS * (NQKV * HID * 2 + HID * HID * 2)
 
     def _ensure(self, s: int, upto: int) -> None:
         need = (upto + PAGE - 1) // PAGE
@@ -125,6 +161,14 @@ class Workload:
             return int(pos.sum() + BATCH)
         self.kv.plan(b)
         layer_fn, h, out = _lib.lib().ember_kv_layer, self.kv._h, self.out.data_ptr()
+        if self.block:
+            lib, st, qkv = _lib.lib(), self.stream.cuda_stream, self.qkv_buf.data_ptr()
+            for layer, (na, ga, oa, _n, _g, _o, qn, kn) in enumerate(self.block_args):
+                if (lib.ember_hip_rmsnorm_rows(na, st) != _lib.OK or lib.ember_hip_gemv(ga, st) != _lib.OK
+                        or layer_fn(h, layer, qkv, qn, kn, None, out) != _lib.OK or lib.ember_hip_gemv(oa, st) != _lib.OK):
+                    _lib.check(-1, "attention block")
+            self.ctx += 1
+            return int(pos.sum() + BATCH)
         for layer, (qkv, qn, kn) in enumerate(self.layer_args):
             if layer_fn(h, layer, qkv, qn, kn, None, out) != _lib.OK:
                 _lib.check(-1, "kv_layer")
@@ -448,6 +492,39 @@ def run_linear(args) -> dict:
     }
 
 
+def run_block(args) -> dict:
+    """Config 2's decode step with the whole attention block per layer (input RMSNorm, qkv GEMV, the fused
+    append + paged attention, o GEMV into the f32 residual), 28 layers: the attention half of a Qwen3-1.7B
+    layer on MI355X. Bytes: the decode path's (K/V of every context token, the new tokens' traffic) plus every
+    layer's qkv and o weights once."""
+    torch = __import__("torch")
+    w = Workload(args.warmup + 2 * args.steps, args.split_len, block=True)
+    for _ in range(args.warmup):
+        w.step()
+    w.stream.synchronize()
+    sum_ctx = 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        sum_ctx += w.step()
+    w.stream.synchronize()
+    torch.cuda.synchronize()
+    step_s = (time.perf_counter() - t0) / args.steps
+    kv_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + TOKEN_BYTES * BATCH)
+    step_bytes = kv_bytes + w.block_weight_bytes
+    gbs = step_bytes / step_s / 1e9
+    log(f"[bench] attention block: {step_s * 1e3:.3f} ms/step, {BATCH / step_s:.0f} tokens/s, "
+        f"{gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of peak)")
+    return {
+        "metric": "attention-block decode tokens/s and % HBM peak (Qwen3-1.7B shape, batch 32: input RMSNorm + "
+                  "qkv GEMV + paged append/attention + o GEMV, 28 layers)",
+        "value": round(BATCH / step_s, 1), "unit": "tokens/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "config": {"workload": "BASELINE configs[1] (batch 32, context U[256,4096], 8192-page pool) with the "
+                               "attention block's RMSNorm and projections, own random weights per layer",
+                   "split_len": args.split_len},
+    }
+
+
 def run_config3(args) -> dict:
     """a continuous-batching mixed step at Qwen3-1.7B shape. 64 sequences share one
     1024-token system prefix held in 64 sealed, refcounted pages (prefix cache: match_prefix). 4 of them
@@ -651,6 +728,8 @@ def main() -> int:
                     help="run each step as a replayed hipGraph of all layers (the timing pass stays eager)")
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4, 5],
                     help="BASELINE config: 2 = the metric (default); 3, 4, 5 print their own line")
+    ap.add_argument("--block", action="store_true",
+                    help="config 2 with the whole attention block per layer (RMSNorm, qkv/o GEMVs); its own line")
     ap.add_argument("--linear", action="store_true",
                     help="time the layer either side of the path (input RMSNorm, qkv and o GEMVs); its own line")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -662,15 +741,17 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.steps)
-    if args.config != 2 or args.linear:
+    if args.config != 2 or args.linear or args.block:
         import torch
 
         from ember_amd import lib
 
         lib()
         assert torch.cuda.is_available(), "bench.py needs a GPU"
-        log("[bench] linear layers" if args.linear else f"[bench] BASELINE config {args.config}")
-        fn = run_linear if args.linear else {3: run_config3, 4: run_config4, 5: run_config5}[args.config]
+        log("[bench] linear layers" if args.linear else "[bench] attention block" if args.block
+            else f"[bench] BASELINE config {args.config}")
+        fn = (run_linear if args.linear else run_block if args.block
+              else {3: run_config3, 4: run_config4, 5: run_config5}[args.config])
         line = fn(args)
         line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
                      "vs_baseline": None, "dtype": "f16", "data": "synthetic, seeded"})

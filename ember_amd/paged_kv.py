@@ -102,6 +102,28 @@ class PagedKv:
         check(_lib.lib().ember_kv_layer(self._h, layer, qkv.data_ptr(), ptr(q_norm), ptr(k_norm), ptr(bias),
                                         out.data_ptr()), "kv_layer")
 
+    def attention_block(self, layer: int, h: torch.Tensor, in_norm: torch.Tensor, w_qkv: torch.Tensor,
+                        w_o: torch.Tensor, *, xn: torch.Tensor, qkv: torch.Tensor, att: torch.Tensor, q_norm=None,
+                        k_norm=None, bias=None) -> None:
+        """One layer's attention block in the reference's order (cuda_backend.cu:350-362), for a planned step of
+        at most 64 tokens and f16 pools: xn = rmsnorm(h) * in_norm (f16), qkv = xn . w_qkv^T (f16), the append +
+        attention of `layer` into att, then h += att . w_o^T (the f32 residual).
+        h: f32 [T, hidden]; in_norm: f32 [hidden]; w_qkv: f16 [(n_heads + 2 n_kv) head_dim, hidden];
+        w_o: f16 [hidden, n_heads head_dim]; xn, qkv, att: f16 scratch of [T, hidden], [T, w_qkv rows] and
+        [T, n_heads, head_dim]."""
+        from . import _lib as L
+        from . import kernels as K
+
+        if self.dtype != torch.float16:
+            raise EmberError("attention_block: f16 pools only (the GEMV takes f16 activations)")
+        T = h.shape[0]
+        if T > 64:
+            raise EmberError("attention_block: at most 64 tokens (decode-sized GEMV)")
+        K.rmsnorm_rows(h, in_norm, xn, self.cfg.rms_eps, stream=self.stream)
+        K.gemv(xn, w_qkv, qkv, L.EPILOGUE_STORE_F16, stream=self.stream)
+        self.layer(layer, qkv, att, q_norm, k_norm, bias)
+        K.gemv(att.view(T, -1), w_o, h, L.EPILOGUE_ADD_F32, stream=self.stream)
+
     def copy_blocks(self, src, dst) -> None:
         s, d = _arr(src), _arr(dst)
         p = ctypes.POINTER(ctypes.c_int32)

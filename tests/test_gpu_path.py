@@ -313,3 +313,62 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
     two = StepBatch(tokens=[0, 0], positions=np.array([5, 6], np.int32), query_start=np.array([0, 2], np.int32),
                     context_len=np.array([7], np.int32), block_tables=np.array(blocks[0][:1], np.int32), max_blocks=1)
     assert not ga.decode_graph(two, io)
+
+
+def test_attention_block_matches_oracle(device):
+    """Two layers of the full attention block (input RMSNorm, qkv GEMV, fused append + attention, o GEMV into
+    the f32 residual) on a decode step of 24 sequences, against the oracle's composition of the same pieces
+    with the GPU path's f16 roundings (xn, qkv and att stored as f16, as cuda_backend.cu:350-362 does).
+    Bound: the residual update within 5e-3 of the oracle's (relative to its largest element)."""
+    HID = H * D
+    L, NB = 2, 1024
+    w = World(device, torch.float16, NB, n_layers=L, max_batch_tokens=16384, seed=5)
+    rng = np.random.default_rng(21)
+    S = 24
+    ctx = rng.integers(20, 600, S)
+    perm = rng.permutation(NB)
+    mb = int((ctx.max() + PAGE) // PAGE) + 1
+    tables = np.full((S, mb), -1, np.int32)
+    used = 0
+    for s_ in range(S):
+        n = int(ctx[s_]) // PAGE + 1
+        tables[s_, :n] = perm[used:used + n]
+        used += n
+    # a cached context first (one prefill step of random K/V through the plain path), then the block step
+    qs0 = np.concatenate([[0], np.cumsum(ctx - 1)]).astype(np.int32)
+    pos0 = np.concatenate([np.arange(c - 1) for c in ctx]).astype(np.int32)
+    pre = _acts(rng, pos0.size, L, True)
+    w.step(pos0, qs0, tables, pre, check=False)
+    positions = (ctx - 1).astype(np.int32)
+    qs = np.arange(S + 1, dtype=np.int32)
+    T = S
+    in_norm = [(1 + 0.1 * rng.standard_normal(HID)).astype(np.float32) for _ in range(L)]
+    w_qkv = [(rng.standard_normal((W, HID)) * 0.03).astype(np.float16) for _ in range(L)]
+    w_o = [(rng.standard_normal((HID, HID)) * 0.03).astype(np.float16) for _ in range(L)]
+    h0 = rng.standard_normal((T, HID)).astype(np.float32)
+    h = torch.from_numpy(h0).to(device)
+    xn = torch.empty((T, HID), dtype=torch.float16, device=device)
+    qkv = torch.empty((T, W), dtype=torch.float16, device=device)
+    att = torch.empty((T, H, D), dtype=torch.float16, device=device)
+    w.kv.plan(StepBatch(tokens=[0] * T, positions=positions.tolist(), query_start=qs.tolist(),
+                        context_len=(positions + 1).tolist(), block_tables=tables.reshape(-1).tolist(), max_blocks=mb))
+    for layer in range(L):
+        w.kv.attention_block(layer, h, torch.from_numpy(in_norm[layer]).to(device),
+                             torch.from_numpy(w_qkv[layer]).to(device), torch.from_numpy(w_o[layer]).to(device),
+                             xn=xn, qkv=qkv, att=att, q_norm=w.qn_d[layer], k_norm=w.kn_d[layer])
+    torch.cuda.synchronize()
+    got = h.cpu().numpy()
+    # the oracle: the same composition in f32 / double, rounding where the GPU path stores f16
+    ho = h0.copy()
+    for layer in range(L):
+        xo = np.stack([oracle.rmsnorm(ho[t], in_norm[layer], EPS) for t in range(T)]).astype(np.float16)
+        qkv_o = oracle.linear(xo, w_qkv[layer], 0).astype(np.float16).astype(np.float32)
+        q_ref = oracle.append_layer(qkv_o, positions, qs, tables, w.ko[layer], w.vo[layer], n_heads=H, n_kv=KVH,
+                                    inv_freq_=w.inv, eps=EPS, q_norm=w.qn[layer], k_norm=w.kn[layer],
+                                    num_blocks=NB + 1, kv_f16=False)
+        att_o = oracle.attention_layer(q_ref, positions, qs, tables, w.ko[layer], w.vo[layer], n_heads=H, n_kv=KVH,
+                                       num_blocks=NB + 1, kv_f16=False, threads=8)
+        ho = oracle.linear(att_o.reshape(T, HID).astype(np.float16), w_o[layer], 2, ho)
+    d_got, d_want = got - h0, ho - h0
+    assert np.isfinite(got).all()
+    assert float(np.abs(d_got - d_want).max()) / float(np.abs(d_want).max()) < 5e-3
