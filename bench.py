@@ -661,16 +661,31 @@ def run_config4(args) -> dict:
     dev = torch.device("cuda")
     q_out = torch.empty((resume_rows, H, D), device=dev, dtype=torch.float16)
     inv = torch.tensor([1.0 / (1e6 ** (2 * i / D)) for i in range(D // 2)], dtype=torch.float32, device=dev)
-    tables_dev = torch.empty(path.tables.shape, dtype=torch.int32, device=dev)
+    # The re-append's integers go up from pinned staging with asynchronous copies, double-buffered: a
+    # synchronous copy would make the host wait for the previous step's kernels and leave the GPU idle
+    # while the host prepares the next step (an engine uploads asynchronously too).
+    n_tab = path.tables.size
+    stage = [torch.empty(2 * resume_rows + n_tab, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+    dev_ints = [torch.empty(2 * resume_rows + n_tab, dtype=torch.int32, device=dev) for _ in range(2)]
+    uploaded = [torch.cuda.Event() for _ in range(2)]
+    n_uploads = [0]
 
     def reappend(seqs):
         """The resumed sequences' K/V written again, every context token, through the append kernel."""
+        i = n_uploads[0] % 2
+        n_uploads[0] += 1
+        uploaded[i].synchronize()  # the copy out of this staging buffer two uploads ago has run
         pos = np.concatenate([np.arange(0, ctx[s]) for s in seqs]).astype(np.int32)
         tsq = np.concatenate([np.full(ctx[s], s) for s in seqs]).astype(np.int32)
+        n = pos.size
+        host = stage[i].numpy()
+        host[:n], host[resume_rows:resume_rows + n] = pos, tsq
+        host[2 * resume_rows:] = path.tables.reshape(-1)
         with torch.cuda.stream(path.stream):
-            pos_d = torch.from_numpy(pos).to(dev, non_blocking=False)
-            tsq_d = torch.from_numpy(tsq).to(dev, non_blocking=False)
-            tables_dev.copy_(torch.from_numpy(path.tables))
+            dev_ints[i].copy_(stage[i], non_blocking=True)
+            uploaded[i].record(path.stream)
+        pos_d, tsq_d = dev_ints[i][:n], dev_ints[i][resume_rows:resume_rows + n]
+        tables_dev = dev_ints[i][2 * resume_rows:]
         a = _lib.QkvArgs()
         a.q_out, a.inv_freq = q_out.data_ptr(), inv.data_ptr()
         a.positions, a.token_seq, a.block_tables = pos_d.data_ptr(), tsq_d.data_ptr(), tables_dev.data_ptr()
@@ -681,14 +696,14 @@ def run_config4(args) -> dict:
             a.k_cache, a.v_cache = path.kv.pool_view(layer, "k").data_ptr(), path.kv.pool_view(layer, "v").data_ptr()
             a.q_norm, a.k_norm = path.qn[layer].data_ptr(), path.kn[layer].data_ptr()
             _lib.check(_lib.lib().ember_hip_kv_append(a, path.stream.cuda_stream), "kv_append")
-        return pos_d, tsq_d  # kept alive until the stream has run them
 
     def step():
         nonlocal paused
         running = [s for s in order if s not in paused]
         for s in paused:
             path.ensure(s, int(ctx[s]))
-        keep = reappend(paused) if paused else None
+        if paused:
+            reappend(paused)
         for s in running:
             path.ensure(s, int(ctx[s]) + 1)
         path.run(running, ctx[running], np.arange(len(running) + 1))
@@ -700,7 +715,6 @@ def run_config4(args) -> dict:
             path.release(s)
         order[:] = [s for s in order if s not in newest] + newest
         paused = newest
-        del keep
         return N_LAYERS * (kv_bytes + TOKEN_BYTES * len(running))
 
     step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)

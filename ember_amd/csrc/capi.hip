@@ -84,6 +84,9 @@ int ember_hip_kv_append(const EmberQkvArgs *a, void *stream) {
         return set_error(EMBER_ERR_INVALID, "kv_append: a required pointer is null");
     if ((a->q_norm == nullptr) != (a->k_norm == nullptr))
         return set_error(EMBER_ERR_INVALID, "kv_append: q_norm and k_norm go together");
+    if ((reinterpret_cast<uintptr_t>(a->qkv) | reinterpret_cast<uintptr_t>(a->q_out) |
+         reinterpret_cast<uintptr_t>(a->k_cache) | reinterpret_cast<uintptr_t>(a->v_cache)) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "kv_append: qkv, q_out and the pools must be 16-byte aligned");
     return hip_status(launch_kv_append(*a, static_cast<hipStream_t>(stream)), "kv_append");
 }
 

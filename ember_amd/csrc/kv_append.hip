@@ -6,12 +6,16 @@
 // append loop, :262-272 rope) so that the f32 path reproduces it to the last
 // bit almost everywhere.
 //
-// One wave64 per head vector of one token. Lane l holds elements l and l + 64:
-// exactly a rotary pair (x_i, x_{i + D/2}), so the rotation needs no lane
-// exchange, and each half-vector is one coalesced 128-byte (f16) or 256-byte
-// (f32) access. The sum of squares is taken in double (products of f32 values
-// are exact in double), matching the CPU's double accumulator; the angle's
-// sine and cosine are evaluated in double and rounded once to f32.
+// One wave64 per token and group of 8 heads: lane l serves head 8 * group +
+// l / 8 and, of its 128 elements, the 8 from 8 * (l % 8) on and their rotary
+// partners 64 elements further, so every access is 16 bytes wide and a wave
+// moves 2 KiB (f16) per instruction pair. The angle's sine and cosine are
+// evaluated in double once per frequency (lane f takes frequency f) and rounded
+// once to f32, then shuffled to the lanes that use them; the sum of squares is
+// taken in double (products of f32 values are exact in double), matching the
+// CPU's double accumulator, in the same pairing order as the one-pair-per-lane
+// form the fused decode step uses (elements 32 apart first, then 16, 8, 4, 2,
+// 1), so both write bit-identical pages.
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -19,31 +23,112 @@ namespace ember::hip {
 namespace {
 
 constexpr int kWavesPerBlock = 4;
+constexpr int kLanesPerHead = 8;
+constexpr int kHeadsPerWave = kWave / kLanesPerHead;
+constexpr int kElems = kHeadDim / 2 / kLanesPerHead;  // elements per lane in each half
+
+template <typename T>
+__device__ __forceinline__ void load8(const T *src, float (&x)[kElems]) {
+    if constexpr (sizeof(T) == 2) {
+        const f16x8 v = *reinterpret_cast<const f16x8 *>(src);
+#pragma unroll
+        for (int e = 0; e < kElems; e++) x[e] = static_cast<float>(v[e]);
+    } else {
+        const f32x4 lo = *reinterpret_cast<const f32x4 *>(src), hi = *reinterpret_cast<const f32x4 *>(src + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) x[e] = lo[e], x[e + 4] = hi[e];
+    }
+}
+
+template <typename T, bool PAGE>
+__device__ __forceinline__ void store8(T *dst, const float (&x)[kElems]) {
+    if constexpr (sizeof(T) == 2) {
+        f16x8 v;
+#pragma unroll
+        for (int e = 0; e < kElems; e++) v[e] = PAGE ? to_page<T>(x[e]) : from_f32<T>(x[e]);
+        *reinterpret_cast<f16x8 *>(dst) = v;
+    } else {
+        *reinterpret_cast<f32x4 *>(dst) = f32x4{x[0], x[1], x[2], x[3]};
+        *reinterpret_cast<f32x4 *>(dst + 4) = f32x4{x[4], x[5], x[6], x[7]};
+    }
+}
 
 template <typename T>
 __global__ void __launch_bounds__(kWavesPerBlock * kWave) kv_append_kernel(EmberQkvArgs a) {
     constexpr int D = kHeadDim, HALF = D / 2;
     const int t = blockIdx.x;
-    const int head = blockIdx.y * kWavesPerBlock + static_cast<int>(threadIdx.x) / kWave;
     const int lane = static_cast<int>(threadIdx.x) % kWave;
+    const int group = static_cast<int>(blockIdx.y) * kWavesPerBlock + static_cast<int>(threadIdx.x) / kWave;
     const int total = a.n_heads + 2 * a.n_kv;
-    if (head >= total) return;  // whole wave
+    if (group * kHeadsPerWave >= total) return;  // whole wave
+    const int head = group * kHeadsPerWave + lane / kLanesPerHead;
+    const int e0 = (lane % kLanesPerHead) * kElems;
+    const bool live = head < total;
 
+    float x0[kElems] = {}, x1[kElems] = {};
     const T *src = static_cast<const T *>(a.qkv) + (static_cast<int64_t>(t) * total + head) * D;
-    float x0 = to_f32(src[lane]), x1 = to_f32(src[lane + HALF]);
-    if (a.bias) {
-        x0 = x0 + a.bias[head * D + lane];
-        x1 = x1 + a.bias[head * D + lane + HALF];
+    if (live) {
+        load8(src + e0, x0);
+        load8(src + HALF + e0, x1);
+        if (a.bias) {
+            const float *b = a.bias + head * D;
+#pragma unroll
+            for (int e = 0; e < kElems; e++) x0[e] = x0[e] + b[e0 + e], x1[e] = x1[e] + b[HALF + e0 + e];
+        }
     }
-
     const int pos = a.positions[t];
     const bool is_q = head < a.n_heads, is_k = !is_q && head < a.n_heads + a.n_kv;
-    if (is_q || is_k) qk_norm_rope(x0, x1, is_q ? a.q_norm : a.k_norm, a.eps, pos, a.inv_freq, lane);
+
+    // Sine and cosine of frequency `lane`, then the lane's own eight.
+    const float angle = static_cast<float>(pos) * a.inv_freq[lane];
+    double sd, cd;
+    sincos(static_cast<double>(angle), &sd, &cd);
+    const float s_f = static_cast<float>(sd), c_f = static_cast<float>(cd);
+    float sn[kElems], cs[kElems];
+#pragma unroll
+    for (int e = 0; e < kElems; e++) sn[e] = __shfl(s_f, e0 + e, kWave), cs[e] = __shfl(c_f, e0 + e, kWave);
+
+    // Sum of squares over the head, every lane of the 8 taking part (the head
+    // groups never mix): element bits 5, 4, 3 are lane bits 2, 1, 0; bits 2, 1, 0
+    // are the register index.
+    double ss[kElems];
+#pragma unroll
+    for (int e = 0; e < kElems; e++)
+        ss[e] = static_cast<double>(x0[e]) * x0[e] + static_cast<double>(x1[e]) * x1[e];
+#pragma unroll
+    for (int o = kLanesPerHead / 2; o > 0; o >>= 1) {
+#pragma unroll
+        for (int e = 0; e < kElems; e++) ss[e] += __shfl_xor(ss[e], o, kLanesPerHead);
+    }
+#pragma unroll
+    for (int o = kElems / 2; o > 0; o >>= 1) {
+#pragma unroll
+        for (int e = 0; e < o; e++) ss[e] += ss[e + o];
+    }
+
+    if (is_q || is_k) {
+        const float *w = is_q ? a.q_norm : a.k_norm;
+        if (w) {
+            const float scale = static_cast<float>(1.0 / sqrt(ss[0] / kHeadDim + static_cast<double>(a.eps)));
+#pragma unroll
+            for (int e = 0; e < kElems; e++) {
+                x0[e] = w[e0 + e] * (x0[e] * scale);
+                x1[e] = w[HALF + e0 + e] * (x1[e] * scale);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < kElems; e++) {
+            const float lo = x0[e], hi = x1[e];
+            x0[e] = lo * cs[e] - hi * sn[e];
+            x1[e] = hi * cs[e] + lo * sn[e];
+        }
+    }
+    if (!live) return;
 
     if (is_q) {
         T *dst = static_cast<T *>(a.q_out) + (static_cast<int64_t>(t) * a.n_heads + head) * D;
-        dst[lane] = from_f32<T>(x0);
-        dst[lane + HALF] = from_f32<T>(x1);
+        store8<T, false>(dst + e0, x0);
+        store8<T, false>(dst + HALF + e0, x1);
         return;
     }
     const int kvh = is_k ? head - a.n_heads : head - a.n_heads - a.n_kv;
@@ -53,16 +138,16 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave) kv_append_kernel(Ember
     if (block < 0 || block >= a.num_blocks) return;  // never write outside the pool
     T *pool = static_cast<T *>(is_k ? a.k_cache : a.v_cache);
     T *dst = pool + ((static_cast<int64_t>(block) * a.n_kv + kvh) * kPage + pos % kPage) * D;
-    dst[lane] = to_page<T>(x0);
-    dst[lane + HALF] = to_page<T>(x1);
+    store8<T, true>(dst + e0, x0);
+    store8<T, true>(dst + HALF + e0, x1);
 }
 
 }  // namespace
 
 hipError_t launch_kv_append(const EmberQkvArgs &a, hipStream_t stream) {
     if (a.T <= 0) return hipSuccess;
-    const int heads = a.n_heads + 2 * a.n_kv;
-    const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((heads + kWavesPerBlock - 1) / kWavesPerBlock));
+    const int groups = (a.n_heads + 2 * a.n_kv + kHeadsPerWave - 1) / kHeadsPerWave;
+    const dim3 grid(static_cast<unsigned>(a.T), static_cast<unsigned>((groups + kWavesPerBlock - 1) / kWavesPerBlock));
     const dim3 block(kWavesPerBlock * kWave);
     if (a.dtype == EMBER_DTYPE_F16)
         hipLaunchKernelGGL(kv_append_kernel<f16>, grid, block, 0, stream, a);

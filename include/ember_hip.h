@@ -73,7 +73,8 @@ typedef struct EmberQkvArgs {
 
 /* QK-RMSNorm, rotate-half RoPE and the K/V cache write, fused.
  * Replaces cuda::qk_norm_rope_store (kernels.cuh:85-86; k_elementwise.cu:159-171).
- * head_dim must be 128; n_heads and n_kv at most 64. */
+ * head_dim must be 128; n_heads and n_kv at most 64; qkv, q_out and the
+ * pools 16-byte aligned (the kernel moves 8 elements per access). */
 int ember_hip_kv_append(const EmberQkvArgs *args, void *stream);
 
 /* Replaces cuda::AttentionArgs (kernels.cuh:88-101). */
