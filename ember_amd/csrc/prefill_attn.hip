@@ -20,13 +20,15 @@
 //                 32-dim chunks; lane l ends with query l % 16 and keys
 //                 4 (l / 16) + 0..3 of each 16-key half;
 //   softmax       per query in base 2, the block max reduced over the four
-//                 lanes that hold a query; each lane sums its own keys' p;
+//                 lanes that hold a query; the causal mask only where a key
+//                 of the block passes some row's position; O rescaled only
+//                 when a row's max passes its reference by more than 2^8;
 //   O += P V      P is the A operand as the S^T lanes hold it: lane l's eight
 //                 k-slots are keys {4g..4g+3, 16+4g..16+4g+3} (g = l / 16),
 //                 and V^T in LDS serves exactly those keys per dim, so the
 //                 products pair up (k order inside one MFMA is free).
-// P is rounded to f16 for the MFMA and the row sum adds the same rounded
-// values, so numerator and denominator agree.
+// P is rounded to f16 for the MFMA and the row sums are one more MFMA of the
+// same P against ones, so numerator and denominator agree.
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -42,6 +44,10 @@ constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), h
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+// How far a block's max may pass the running reference max (base 2) before
+// the reference moves: P stays below 2^8.
+constexpr float kLazyLog2 = 8.0f;
 
 // 2^x by the hardware instruction (v_exp_f32); 0 at -inf.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -72,13 +78,19 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     const int my_i = 16 * (wave % 4) + ql;
     const bool my_ok = my_i < nt;
     const int my_pos = my_ok ? a.positions[t0 + my_i] : -1;
-    int mx = my_pos;
-    for (int o = 32; o > 0; o >>= 1) mx = max(mx, __shfl_xor(mx, o, kWave));
+    int mx = my_pos, mn_pos = my_pos;
+    for (int o = 32; o > 0; o >>= 1) {
+        mx = max(mx, __shfl_xor(mx, o, kWave));
+        mn_pos = min(mn_pos, __shfl_xor(mn_pos, o, kWave));
+    }
+    // The wave's lowest position: a block every key of which is at or below it
+    // needs no causal mask in this wave (a tile's unused rows hold -1: masked).
+    const int wave_min_pos = __builtin_amdgcn_readfirstlane(mn_pos);
     if (lane == 0) wave_max[wave] = mx;
     __syncthreads();
     int max_pos = wave_max[0];
     for (int w = 1; w < kWavesP; w++) max_pos = max(max_pos, wave_max[w]);
-    max_pos = min(max_pos, a.max_blocks * kPage - 1);
+    max_pos = __builtin_amdgcn_readfirstlane(min(max_pos, a.max_blocks * kPage - 1));
     const int n_blocks = (max_pos + kKeyBlock) / kKeyBlock;
 
     // Q^T operands: for 32-dim chunk c, dims 32c + 8g .. + 8 of this lane's query.
@@ -92,51 +104,64 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         qb[c] = v;
     }
 
-    float m = -INFINITY, l = 0.0f;
+    float m = -INFINITY;  // the reference max of this lane's query (base 2, scaled)
     f32x4v o_acc[8];
 #pragma unroll
     for (int dt = 0; dt < 8; dt++) o_acc[dt] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+    // Row sums by the MFMA: P times a ones operand, so lane l holds the sums of
+    // exactly the query rows 4g + r its O values belong to, in the same f32
+    // accumulation as O and of the same f16-rounded P.
+    f32x4v l_acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    f16x8 ones;
+#pragma unroll
+    for (int i = 0; i < 8; i++) ones[i] = static_cast<f16>(1.0f);
 
-    // A key block's K and V, fetched into registers and later stored to LDS;
-    // keys past the tile's last position or in a block outside the pool are
-    // zeros. K: 512 chunks of 8 dims of one key (one or two per thread), stored
-    // as rows. V: 512 pieces of 4 keys x 2 dims (dims 2 dp, 2 dp + 1 of keys
+    // A key block's K and V, fetched into registers and later stored to LDS.
+    // K: 512 chunks of 8 dims of one key (one or two per thread), stored as
+    // rows. V: 512 pieces of 4 keys x 2 dims (dims 2 dp, 2 dp + 1 of keys
     // 4 kq .. 4 kq + 3), each one 4-byte load per key - a wave's load reads one
     // 256-byte key row - regrouped into two 8-byte rows of V^T (dims x keys),
-    // so V is transposed without sub-dword LDS stores.
+    // so V is transposed without sub-dword LDS stores. A chunk's page (the
+    // block's first or second) is the same for a whole wave, so the block ids
+    // are scalar loads and each thread's offsets inside a page are fixed.
+    // Pages past the tile's last position or outside the pool give zeros, and
+    // so do V slots past the last position (an unwritten slot may hold
+    // anything, and P = 0 must not meet a NaN).
     constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kPThreads;
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int64_t page_elems = static_cast<int64_t>(a.n_kv) * kPage * kHeadDim;
+    uint32_t koff[kChunks], voff[kChunks];
+    int vkey[kChunks];
+#pragma unroll
+    for (int j = 0; j < kChunks; j++) {
+        const int chunk = tid + j * kPThreads;
+        koff[j] = static_cast<uint32_t>((kvh * kPage + (chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8);
+        const int kq = chunk / 64, dp = chunk % 64;
+        voff[j] = static_cast<uint32_t>((kvh * kPage + (4 * kq) % kPage) * kHeadDim + 2 * dp);
+        vkey[j] = 4 * kq;
+    }
     auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
+        const bool whole = kb * kKeyBlock + kKeyBlock - 1 <= max_pos;  // no slot past the last position
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-            const int chunk = tid + j * kPThreads;
-            {
-                const int key = chunk / 16, d8 = (chunk % 16) * 8;
-                kv4[j] = make_uint4(0, 0, 0, 0);
-                const int pos = kb * kKeyBlock + key;
-                if (kb < n_blocks && pos <= max_pos) {
-                    const int blk = table[pos / kPage];
-                    if (blk >= 0 && blk < a.num_blocks) {
-                        const int64_t off =
-                            ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos % kPage) * kHeadDim + d8;
-                        kv4[j] = *reinterpret_cast<const uint4 *>(kc + off);
-                    }
-                }
-            }
-            {
-                const int kq = chunk / 64, dp = chunk % 64;
-                const int pos0 = kb * kKeyBlock + 4 * kq;  // the quad's 4 keys share a page
-                uint32_t w[4] = {0, 0, 0, 0};
-                if (kb < n_blocks && pos0 <= max_pos) {
-                    const int blk = table[pos0 / kPage];
-                    if (blk >= 0 && blk < a.num_blocks) {
-                        const int64_t off =
-                            ((static_cast<int64_t>(blk) * a.n_kv + kvh) * kPage + pos0 % kPage) * kHeadDim + 2 * dp;
+            const int pg = 2 * kb + (wave_u * kWave + j * kPThreads) / (kPage * 16);  // wave-uniform
+            kv4[j] = make_uint4(0, 0, 0, 0);
+            vq[j] = make_uint4(0, 0, 0, 0);
+            if (kb < n_blocks && pg * kPage <= max_pos) {
+                const int blk = table[pg];
+                if (blk >= 0 && blk < a.num_blocks) {
+                    const f16 *kp = kc + blk * page_elems, *vp = vc + blk * page_elems;
+                    kv4[j] = *reinterpret_cast<const uint4 *>(kp + koff[j]);
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; e++) w[e] = *reinterpret_cast<const uint32_t *>(vp + voff[j] + e * kHeadDim);
+                    if (!whole) {
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            if (pos0 + e <= max_pos) w[e] = *reinterpret_cast<const uint32_t *>(vc + off + e * kHeadDim);
+                            if (kb * kKeyBlock + vkey[j] + e > max_pos) w[e] = 0;
                     }
+                    vq[j] = make_uint4(w[0], w[1], w[2], w[3]);
                 }
-                vq[j] = make_uint4(w[0], w[1], w[2], w[3]);
             }
         }
     };
@@ -165,84 +190,84 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         const int buf = kb & 1;
         fetch(kb + 1, nk, nv);  // in flight while this block computes
 
-        // Keys of this lane in the block: 16 st + 4g + r (st = half, r = 0..3).
-        const int key_base = kb * kKeyBlock + 4 * g;
-        const bool full = kb * kKeyBlock + kKeyBlock - 1 <= my_pos;  // every key of the block visible
-        f32x4v s[2];
-#pragma unroll
-        for (int st = 0; st < 2; st++) {
-            f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const f16x8 ka = *reinterpret_cast<const f16x8 *>(&k_lds[buf][(16 * st + ql) * kKRow + 32 * c + 8 * g]);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qb[c], acc, 0, 0, 0);
-            }
-            s[st] = acc;
-        }
-        float sv[8];
-        float bm = -INFINITY;
+        // Every LDS operand of the block is read up front: the V^T reads then
+        // overlap the scores and the softmax instead of waiting one by one.
+        f16x8 ka[2][4], vb[8];
 #pragma unroll
         for (int st = 0; st < 2; st++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float x = s[st][r] * scale_log2;
-                if (!full && key_base + 16 * st + r > my_pos) x = -INFINITY;
-                sv[4 * st + r] = x;
-                bm = fmaxf(bm, x);
-            }
-        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-        const float mn = fmaxf(m, bm);
-        const float ref = mn == -INFINITY ? 0.0f : mn;
-        const float corr = m == mn ? 1.0f : exp2_fast(m - ref);
-        f16x8 pa;
-        float psum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const f16 ph = static_cast<f16>(exp2_fast(sv[i] - ref));
-            pa[i] = ph;
-            psum += static_cast<float>(ph);
-        }
-        l = l * corr + psum;
-        m = mn;
-        // O rows are queries 4g + r: their correction factors live in lanes 4g + r.
-        float cq[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
+            for (int c = 0; c < 4; c++)
+                ka[st][c] = *reinterpret_cast<const f16x8 *>(&k_lds[buf][(16 * st + ql) * kKRow + 32 * c + 8 * g]);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const f16 *vrow = &v_lds[buf][(16 * dt + ql) * kVRow];
             const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
             const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
-            const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            f32x4v acc = o_acc[dt];
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[r] = acc[r] * cq[r];
-            o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, acc, 0, 0, 0);
+            vb[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
+
+        // S^T: lane l holds query ql and keys 16 st + 4g + r (st = half, r = 0..3).
+        float sv[8];
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+            f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int c = 0; c < 4; c++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[st][c], qb[c], acc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) sv[4 * st + r] = acc[r];
+        }
+        if (kb * kKeyBlock + kKeyBlock - 1 > wave_min_pos) {  // some key of the block is past some row's position
+            const int key_base = kb * kKeyBlock + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (key_base + 16 * (i / 4) + i % 4 > my_pos) sv[i] = -INFINITY;
+        }
+        float bm = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) bm = fmaxf(bm, sv[i]);
+        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+        // The reference max moves only when the block's max passes it by more
+        // than kLazyLog2, so P stays below 2^kLazyLog2 (f16 holds it) and O is
+        // rescaled in few blocks; O / l is the same for any reference.
+        const float bx = bm * scale_log2;
+        const bool grow = bx > m + kLazyLog2;
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+            const float corr = grow ? exp2_fast(m - bx) : 1.0f;  // 0 from an empty row
+            m = grow ? bx : m;
+            float cq[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                l_acc[r] = l_acc[r] * cq[r];
+#pragma unroll
+                for (int dt = 0; dt < 8; dt++) o_acc[dt][r] = o_acc[dt][r] * cq[r];
+            }
+        }
+        const float neg_ref = m == -INFINITY ? 0.0f : -m;  // a row with no visible key yet has only -inf scores
+        f16x8 pa;
+#pragma unroll
+        for (int i = 0; i < 8; i++) pa[i] = static_cast<f16>(exp2_fast(fmaf(sv[i], scale_log2, neg_ref)));
+        l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[dt], o_acc[dt], 0, 0, 0);
         // The next block goes into the other buffer, which nobody reads any more:
         // the barrier that ended the previous block separated its readers.
         if (kb + 1 < n_blocks) stage(buf ^ 1, nk, nv);
         __syncthreads();
     }
 
-    // Row sums over the four lanes of each query, then out = O / l for the
-    // queries 4g + r this lane's O rows hold.
-    float lt = l;
-    lt = lt + __shfl_xor(lt, 16, kWave);
-    lt = lt + __shfl_xor(lt, 32, kWave);
-    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-    float iq[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) iq[r] = __shfl(inv, 4 * g + r, kWave);
+    // out = O / l for the queries 4g + r this lane's O rows hold.
     f16 *out = static_cast<f16 *>(a.out);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const int i = 16 * (wave % 4) + 4 * g + r;
         if (i >= nt) continue;
+        const float inv = l_acc[r] > 0.0f ? 1.0f / l_acc[r] : 0.0f;
         f16 *row = out + (static_cast<int64_t>(t0 + i) * a.n_heads + head) * kHeadDim;
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) row[16 * dt + ql] = static_cast<f16>(o_acc[dt][r] * iq[r]);
+        for (int dt = 0; dt < 8; dt++) row[16 * dt + ql] = static_cast<f16>(o_acc[dt][r] * inv);
     }
 }
 
