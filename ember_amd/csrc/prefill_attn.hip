@@ -13,9 +13,10 @@
 // reference's block serves one head): 4 waves per head, wave w owning tokens
 // 16 (w % 4) .. + 15 of the tile for head w / 4. Keys go in blocks of 32 (two
 // pages): the work-group stages a block's K rows and V transposed (dims x
-// keys) in LDS, double-buffered (every thread fetches its part of block k + 1
-// into registers while block k computes, then stores it to the other buffer),
-// and every wave runs
+// keys) in LDS, double-buffered: every thread fetches its part of block k + 2
+// from HBM while block k computes, and each wave reads block k + 1's MFMA
+// operands from LDS into registers while it runs block k's MFMAs. Every wave
+// runs
 //   S^T = K Q^T   16 keys x 16 queries per v_mfma_f32_16x16x32_f16, four
 //                 32-dim chunks; lane l ends with query l % 16 and keys
 //                 4 (l / 16) + 0..3 of each 16-key half;
@@ -182,22 +183,16 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         }
     };
 
-    uint4 nk[kChunks], nv[kChunks];
-    fetch(0, nk, nv);
-    stage(0, nk, nv);
-    __syncthreads();
-    for (int kb = 0; kb < n_blocks; kb++) {
-        const int buf = kb & 1;
-        fetch(kb + 1, nk, nv);  // in flight while this block computes
-
-        // Every LDS operand of the block is read up front: the V^T reads then
-        // overlap the scores and the softmax instead of waiting one by one.
-        f16x8 ka[2][4], vb[8];
+    // A block's MFMA operands from LDS buffer `buf`: K rows for S^T, and V^T
+    // for O += P V.
+    auto read_k = [&](int buf, f16x8 (&ka)[2][4]) {
 #pragma unroll
         for (int st = 0; st < 2; st++)
 #pragma unroll
             for (int c = 0; c < 4; c++)
                 ka[st][c] = *reinterpret_cast<const f16x8 *>(&k_lds[buf][(16 * st + ql) * kKRow + 32 * c + 8 * g]);
+    };
+    auto read_v = [&](int buf, f16x8 (&vb)[8]) {
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const f16 *vrow = &v_lds[buf][(16 * dt + ql) * kVRow];
@@ -205,6 +200,28 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
             const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
             vb[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
+    };
+
+    // Two LDS buffers, operands one block ahead in registers. While block kb
+    // computes from registers, block kb + 1 is already in LDS (stored before
+    // the last barrier): its K operands are read as soon as block kb's score
+    // MFMAs have taken theirs, its V operands after the P V MFMAs, so LDS
+    // reads overlap the MFMAs and the softmax instead of queueing behind
+    // every wave after each barrier. Block kb + 2 loads from HBM meanwhile and
+    // goes into block kb's buffer, whose reads all ended before the previous
+    // barrier (they were block kb's operand reads, made during block kb - 1).
+    uint4 nk[kChunks], nv[kChunks];
+    fetch(0, nk, nv);
+    stage(0, nk, nv);
+    fetch(1, nk, nv);
+    if (n_blocks > 1) stage(1, nk, nv);
+    __syncthreads();
+    f16x8 ka[2][4], vb[8];
+    read_k(0, ka);
+    read_v(0, vb);
+    for (int kb = 0; kb < n_blocks; kb++) {
+        const int buf = kb & 1, next = buf ^ 1;
+        fetch(kb + 2, nk, nv);  // in flight while this block computes
 
         // S^T: lane l holds query ql and keys 16 st + 4g + r (st = half, r = 0..3).
         float sv[8];
@@ -216,23 +233,26 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
             for (int r = 0; r < 4; r++) sv[4 * st + r] = acc[r];
         }
+        if (kb + 1 < n_blocks) read_k(next, ka);
         if (kb * kKeyBlock + kKeyBlock - 1 > wave_min_pos) {  // some key of the block is past some row's position
             const int key_base = kb * kKeyBlock + 4 * g;
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 if (key_base + 16 * (i / 4) + i % 4 > my_pos) sv[i] = -INFINITY;
         }
-        float bm = sv[0];
-#pragma unroll
-        for (int i = 1; i < 8; i++) bm = fmaxf(bm, sv[i]);
-        bm = fmaxf(bm, __shfl_xor(bm, 16, kWave));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-        // The reference max moves only when the block's max passes it by more
+        // The reference max moves only when a block's max passes it by more
         // than kLazyLog2, so P stays below 2^kLazyLog2 (f16 holds it) and O is
-        // rescaled in few blocks; O / l is the same for any reference.
-        const float bx = bm * scale_log2;
-        const bool grow = bx > m + kLazyLog2;
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        // rescaled in few blocks; O / l is the same for any reference. Each
+        // lane first checks its own eight keys: only when one of them passes
+        // does the wave reduce to the query max over its four lanes.
+        float lmax = sv[0];
+#pragma unroll
+        for (int i = 1; i < 8; i++) lmax = fmaxf(lmax, sv[i]);
+        if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m + kLazyLog2) != 0) {
+            float bm = fmaxf(lmax, __shfl_xor(lmax, 16, kWave));
+            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+            const float bx = bm * scale_log2;
+            const bool grow = bx > m + kLazyLog2;
             const float corr = grow ? exp2_fast(m - bx) : 1.0f;  // 0 from an empty row
             m = grow ? bx : m;
             float cq[4];
@@ -252,9 +272,8 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[dt], o_acc[dt], 0, 0, 0);
-        // The next block goes into the other buffer, which nobody reads any more:
-        // the barrier that ended the previous block separated its readers.
-        if (kb + 1 < n_blocks) stage(buf ^ 1, nk, nv);
+        if (kb + 1 < n_blocks) read_v(next, vb);
+        if (kb + 2 < n_blocks) stage(buf, nk, nv);
         __syncthreads();
     }
 
