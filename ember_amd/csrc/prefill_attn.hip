@@ -10,13 +10,16 @@
 //
 // Shape on MI355X: one work-group per (tile, pair of query heads of one kv
 // head), so each K/V block is read once for both heads of a GQA pair (the
-// reference's block serves one head): 4 waves per head, wave w owning tokens
-// 16 (w % 4) .. + 15 of the tile for head w / 4. Keys go in blocks of 32 (two
-// pages): the work-group stages a block's K rows and V transposed (dims x
-// keys) in LDS, double-buffered: every thread fetches its part of block k + 2
-// from HBM while block k computes, and each wave reads block k + 1's MFMA
-// operands from LDS into registers while it runs block k's MFMAs. Every wave
-// runs
+// reference's block serves one head). The work-group is two key groups of 4
+// waves per head: group 0 takes key blocks 0, 2, 4, ..., group 1 blocks 1, 3,
+// 5, ..., and in each group wave w owns tokens 16 (w % 4) .. + 15 of the tile
+// for head w / 4 - four waves per SIMD, so one wave's LDS and MFMA latency
+// hides behind the others'. Keys go in blocks of 32 (two pages): each group
+// stages its block's K rows and V transposed (dims x keys) in its own
+// double-buffered LDS, fetching its next block from HBM while the current one
+// computes; both groups pass one barrier per step. At the end group 1 hands
+// its partial (reference max, row sums, O) through LDS to the group 0 wave
+// with the same rows, which merges them. Every wave runs
 //   S^T = K Q^T   16 keys x 16 queries per v_mfma_f32_16x16x32_f16, four
 //                 32-dim chunks; lane l ends with query l % 16 and keys
 //                 4 (l / 16) + 0..3 of each 16-key half;
@@ -39,7 +42,8 @@ namespace {
 constexpr int kTileTokens = EMBER_PREFILL_TILE;  // 64
 constexpr int kKeyBlock = 32;                     // keys per LDS block: two pages
 template <int HG>
-constexpr int kThreadsFor = 256 * HG;  // 4 waves per query head
+constexpr int kThreadsFor = 512 * HG;  // two key groups of 4 waves per query head
+constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's partial: O (8), l, m
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
 constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), halves: 18 dwords, rows 2 apart 4 banks apart
 
@@ -56,16 +60,22 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 template <int HG>  // query heads per work-group (1 or 2), all of one kv head
 __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillArgs a, float scale_log2) {
     constexpr int kPThreads = kThreadsFor<HG>;
-    constexpr int kWavesP = kPThreads / kWave;         // 4 x HG: wave w takes tokens 16 (w % 4).. and head w / 4
-    __shared__ __align__(16) f16 k_lds[2][kKeyBlock * kKRow];
-    __shared__ __align__(16) f16 v_lds[2][kHeadDim * kVRow];
+    constexpr int kGroupThreads = kPThreads / 2;       // one key group
+    constexpr int kGroupWaves = kGroupThreads / kWave; // 4 x HG: wave w takes tokens 16 (w % 4).. and head w / 4
+    constexpr int kWavesP = 2 * kGroupWaves;
+    constexpr int kKBytes = kKeyBlock * kKRow * 2, kVBytes = kHeadDim * kVRow * 2;
+    constexpr int kStageBytes = 2 * 2 * (kKBytes + kVBytes);           // [group][buffer] K and V
+    constexpr int kMergeBytes = kGroupWaves * kMergeSlots * kWave * 16;  // group 1's partials, one float4 per slot
+    __shared__ __align__(16) unsigned char lds[kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes];
     __shared__ int wave_max[kWavesP];
 
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid % kWave, wave = tid / kWave;
+    const int grp = __builtin_amdgcn_readfirstlane(wave / kGroupWaves);  // key blocks grp, grp + 2, ...
+    const int wl = wave % kGroupWaves, tg = tid % kGroupThreads;
     const int ql = lane % 16, g = lane / 16;
     const int tile = static_cast<int>(blockIdx.x);
-    const int head = static_cast<int>(blockIdx.y) * HG + wave / 4;
+    const int head = static_cast<int>(blockIdx.y) * HG + wl / 4;
     const int G = a.n_heads / a.n_kv;
     const int kvh = static_cast<int>(blockIdx.y) * HG / G;
     const int t0 = a.tile_start[tile];
@@ -74,9 +84,11 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     const f16 *q = static_cast<const f16 *>(a.q);
     const f16 *kc = static_cast<const f16 *>(a.k_cache);
     const f16 *vc = static_cast<const f16 *>(a.v_cache);
+    auto k_lds = [&](int buf) { return reinterpret_cast<f16 *>(lds + (grp * 2 + buf) * kKBytes); };
+    auto v_lds = [&](int buf) { return reinterpret_cast<f16 *>(lds + 4 * kKBytes + (grp * 2 + buf) * kVBytes); };
 
-    // This lane's query (token 16 (wave % 4) + ql of the tile) and the tile's key range.
-    const int my_i = 16 * (wave % 4) + ql;
+    // This lane's query (token 16 (wl % 4) + ql of the tile) and the tile's key range.
+    const int my_i = 16 * (wl % 4) + ql;
     const bool my_ok = my_i < nt;
     const int my_pos = my_ok ? a.positions[t0 + my_i] : -1;
     int mx = my_pos, mn_pos = my_pos;
@@ -117,25 +129,25 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
     for (int i = 0; i < 8; i++) ones[i] = static_cast<f16>(1.0f);
 
-    // A key block's K and V, fetched into registers and later stored to LDS.
-    // K: 512 chunks of 8 dims of one key (one or two per thread), stored as
-    // rows. V: 512 pieces of 4 keys x 2 dims (dims 2 dp, 2 dp + 1 of keys
-    // 4 kq .. 4 kq + 3), each one 4-byte load per key - a wave's load reads one
-    // 256-byte key row - regrouped into two 8-byte rows of V^T (dims x keys),
-    // so V is transposed without sub-dword LDS stores. A chunk's page (the
-    // block's first or second) is the same for a whole wave, so the block ids
-    // are scalar loads and each thread's offsets inside a page are fixed.
-    // Pages past the tile's last position or outside the pool give zeros, and
-    // so do V slots past the last position (an unwritten slot may hold
-    // anything, and P = 0 must not meet a NaN).
-    constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kPThreads;
-    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    // A key block's K and V, fetched by its group into registers and later
+    // stored to the group's LDS buffer. K: 512 chunks of 8 dims of one key
+    // (one or two per thread), stored as rows. V: 512 pieces of 4 keys x 2 dims
+    // (dims 2 dp, 2 dp + 1 of keys 4 kq .. 4 kq + 3), each one 4-byte load per
+    // key - a wave's load reads one 256-byte key row - regrouped into two
+    // 8-byte rows of V^T (dims x keys), so V is transposed without sub-dword
+    // LDS stores. A chunk's page (the block's first or second) is the same for
+    // a whole wave, so the block ids are scalar loads and each thread's
+    // offsets inside a page are fixed. Pages past the tile's last position or
+    // outside the pool give zeros, and so do V slots past the last position
+    // (an unwritten slot may hold anything, and P = 0 must not meet a NaN).
+    constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kGroupThreads;
+    const int wl_u = __builtin_amdgcn_readfirstlane(wl);
     const int64_t page_elems = static_cast<int64_t>(a.n_kv) * kPage * kHeadDim;
     uint32_t koff[kChunks], voff[kChunks];
     int vkey[kChunks];
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
-        const int chunk = tid + j * kPThreads;
+        const int chunk = tg + j * kGroupThreads;
         koff[j] = static_cast<uint32_t>((kvh * kPage + (chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8);
         const int kq = chunk / 64, dp = chunk % 64;
         voff[j] = static_cast<uint32_t>((kvh * kPage + (4 * kq) % kPage) * kHeadDim + 2 * dp);
@@ -145,7 +157,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         const bool whole = kb * kKeyBlock + kKeyBlock - 1 <= max_pos;  // no slot past the last position
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-            const int pg = 2 * kb + (wave_u * kWave + j * kPThreads) / (kPage * 16);  // wave-uniform
+            const int pg = 2 * kb + (wl_u * kWave + j * kGroupThreads) / (kPage * 16);  // wave-uniform
             kv4[j] = make_uint4(0, 0, 0, 0);
             vq[j] = make_uint4(0, 0, 0, 0);
             if (kb < n_blocks && pg * kPage <= max_pos) {
@@ -167,129 +179,135 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         }
     };
     auto stage = [&](int buf, const uint4 (&kv4)[kChunks], const uint4 (&vq)[kChunks]) {
+        f16 *kl = k_lds(buf), *vl = v_lds(buf);
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
-            const int chunk = tid + j * kPThreads;
+            const int chunk = tg + j * kGroupThreads;
             const int key = chunk / 16, d8 = (chunk % 16) * 8;
-            *reinterpret_cast<uint4 *>(&k_lds[buf][key * kKRow + d8]) = kv4[j];
+            *reinterpret_cast<uint4 *>(&kl[key * kKRow + d8]) = kv4[j];
             // vq = (key e: dim 2dp | dim 2dp+1 << 16), e = 0..3; v_perm picks halves.
             const int kq = chunk / 64, dp = chunk % 64;
             const uint2 lo = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x05040100u),
                                         __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x05040100u));
             const uint2 hi = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x07060302u),
                                         __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x07060302u));
-            *reinterpret_cast<uint2 *>(&v_lds[buf][(2 * dp) * kVRow + 4 * kq]) = lo;
-            *reinterpret_cast<uint2 *>(&v_lds[buf][(2 * dp + 1) * kVRow + 4 * kq]) = hi;
+            *reinterpret_cast<uint2 *>(&vl[(2 * dp) * kVRow + 4 * kq]) = lo;
+            *reinterpret_cast<uint2 *>(&vl[(2 * dp + 1) * kVRow + 4 * kq]) = hi;
         }
     };
 
-    // A block's MFMA operands from LDS buffer `buf`: K rows for S^T, and V^T
-    // for O += P V.
-    auto read_k = [&](int buf, f16x8 (&ka)[2][4]) {
-#pragma unroll
-        for (int st = 0; st < 2; st++)
-#pragma unroll
-            for (int c = 0; c < 4; c++)
-                ka[st][c] = *reinterpret_cast<const f16x8 *>(&k_lds[buf][(16 * st + ql) * kKRow + 32 * c + 8 * g]);
-    };
-    auto read_v = [&](int buf, f16x8 (&vb)[8]) {
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) {
-            const f16 *vrow = &v_lds[buf][(16 * dt + ql) * kVRow];
-            const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
-            const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
-            vb[dt] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-    };
-
-    // Two LDS buffers, operands one block ahead in registers. While block kb
-    // computes from registers, block kb + 1 is already in LDS (stored before
-    // the last barrier): its K operands are read as soon as block kb's score
-    // MFMAs have taken theirs, its V operands after the P V MFMAs, so LDS
-    // reads overlap the MFMAs and the softmax instead of queueing behind
-    // every wave after each barrier. Block kb + 2 loads from HBM meanwhile and
-    // goes into block kb's buffer, whose reads all ended before the previous
-    // barrier (they were block kb's operand reads, made during block kb - 1).
+    // The two groups step together, one barrier per step: at step s group
+    // grp computes block 2 s + grp from its buffer s % 2 while it fetches block
+    // 2 (s + 1) + grp, which goes into its other buffer (whose readers all
+    // finished before the previous barrier) at the end of the step.
+    const int n_steps = (n_blocks + 1) / 2;
     uint4 nk[kChunks], nv[kChunks];
-    fetch(0, nk, nv);
+    fetch(grp, nk, nv);
     stage(0, nk, nv);
-    fetch(1, nk, nv);
-    if (n_blocks > 1) stage(1, nk, nv);
     __syncthreads();
-    f16x8 ka[2][4], vb[8];
-    read_k(0, ka);
-    read_v(0, vb);
-    for (int kb = 0; kb < n_blocks; kb++) {
-        const int buf = kb & 1, next = buf ^ 1;
+    for (int st = 0; st < n_steps; st++) {
+        const int buf = st & 1, kb = 2 * st + grp;
         fetch(kb + 2, nk, nv);  // in flight while this block computes
-
-        // S^T: lane l holds query ql and keys 16 st + 4g + r (st = half, r = 0..3).
-        float sv[8];
+        if (kb < n_blocks) {
+            const f16 *kl = k_lds(buf), *vl = v_lds(buf);
+            // S^T: lane l holds query ql and keys 16 h + 4g + r (h = half, r = 0..3).
+            float sv[8];
 #pragma unroll
-        for (int st = 0; st < 2; st++) {
-            f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int h = 0; h < 2; h++) {
+                f16x8 ka[4];
 #pragma unroll
-            for (int c = 0; c < 4; c++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[st][c], qb[c], acc, 0, 0, 0);
+                for (int c = 0; c < 4; c++)
+                    ka[c] = *reinterpret_cast<const f16x8 *>(&kl[(16 * h + ql) * kKRow + 32 * c + 8 * g]);
+                f32x4v acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 4; r++) sv[4 * st + r] = acc[r];
-        }
-        if (kb + 1 < n_blocks) read_k(next, ka);
-        if (kb * kKeyBlock + kKeyBlock - 1 > wave_min_pos) {  // some key of the block is past some row's position
-            const int key_base = kb * kKeyBlock + 4 * g;
+                for (int c = 0; c < 4; c++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka[c], qb[c], acc, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                if (key_base + 16 * (i / 4) + i % 4 > my_pos) sv[i] = -INFINITY;
-        }
-        // The reference max moves only when a block's max passes it by more
-        // than kLazyLog2, so P stays below 2^kLazyLog2 (f16 holds it) and O is
-        // rescaled in few blocks; O / l is the same for any reference. Each
-        // lane first checks its own eight keys: only when one of them passes
-        // does the wave reduce to the query max over its four lanes.
-        float lmax = sv[0];
+                for (int r = 0; r < 4; r++) sv[4 * h + r] = acc[r];
+            }
+            if (kb * kKeyBlock + kKeyBlock - 1 > wave_min_pos) {  // some key of the block is past some row's position
+                const int key_base = kb * kKeyBlock + 4 * g;
 #pragma unroll
-        for (int i = 1; i < 8; i++) lmax = fmaxf(lmax, sv[i]);
-        if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m + kLazyLog2) != 0) {
-            float bm = fmaxf(lmax, __shfl_xor(lmax, 16, kWave));
-            bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-            const float bx = bm * scale_log2;
-            const bool grow = bx > m + kLazyLog2;
-            const float corr = grow ? exp2_fast(m - bx) : 1.0f;  // 0 from an empty row
-            m = grow ? bx : m;
-            float cq[4];
+                for (int i = 0; i < 8; i++)
+                    if (key_base + 16 * (i / 4) + i % 4 > my_pos) sv[i] = -INFINITY;
+            }
+            // The reference max moves only when a block's max passes it by more
+            // than kLazyLog2, so P stays below 2^kLazyLog2 (f16 holds it) and O is
+            // rescaled in few blocks; O / l is the same for any reference. Each
+            // lane first checks its own eight keys: only when one of them passes
+            // does the wave reduce to the query max over its four lanes.
+            float lmax = sv[0];
 #pragma unroll
-            for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
+            for (int i = 1; i < 8; i++) lmax = fmaxf(lmax, sv[i]);
+            if (__builtin_amdgcn_ballot_w64(lmax * scale_log2 > m + kLazyLog2) != 0) {
+                float bm = fmaxf(lmax, __shfl_xor(lmax, 16, kWave));
+                bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+                const float bx = bm * scale_log2;
+                const bool grow = bx > m + kLazyLog2;
+                const float corr = grow ? exp2_fast(m - bx) : 1.0f;  // 0 from an empty row
+                m = grow ? bx : m;
+                float cq[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                l_acc[r] = l_acc[r] * cq[r];
+                for (int r = 0; r < 4; r++) cq[r] = __shfl(corr, 4 * g + r, kWave);
 #pragma unroll
-                for (int dt = 0; dt < 8; dt++) o_acc[dt][r] = o_acc[dt][r] * cq[r];
+                for (int r = 0; r < 4; r++) {
+                    l_acc[r] = l_acc[r] * cq[r];
+#pragma unroll
+                    for (int dt = 0; dt < 8; dt++) o_acc[dt][r] = o_acc[dt][r] * cq[r];
+                }
+            }
+            const float neg_ref = m == -INFINITY ? 0.0f : -m;  // a row with no visible key yet has only -inf scores
+            f16x8 pa;
+#pragma unroll
+            for (int i = 0; i < 8; i++) pa[i] = static_cast<f16>(exp2_fast(fmaf(sv[i], scale_log2, neg_ref)));
+            l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                const f16 *vrow = &vl[(16 * dt + ql) * kVRow];
+                const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
+                const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
+                const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o_acc[dt], 0, 0, 0);
             }
         }
-        const float neg_ref = m == -INFINITY ? 0.0f : -m;  // a row with no visible key yet has only -inf scores
-        f16x8 pa;
-#pragma unroll
-        for (int i = 0; i < 8; i++) pa[i] = static_cast<f16>(exp2_fast(fmaf(sv[i], scale_log2, neg_ref)));
-        l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
-#pragma unroll
-        for (int dt = 0; dt < 8; dt++) o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[dt], o_acc[dt], 0, 0, 0);
-        if (kb + 1 < n_blocks) read_v(next, vb);
-        if (kb + 2 < n_blocks) stage(buf, nk, nv);
+        if (kb + 2 < n_blocks) stage(buf ^ 1, nk, nv);
         __syncthreads();
     }
 
-    // out = O / l for the queries 4g + r this lane's O rows hold.
+    // Group 1 hands its partial (reference max, row sums, O) to the group 0
+    // wave with the same rows, through LDS (the staging buffers are free after
+    // the last barrier); that wave merges the two and writes out = O / l.
+    f32x4v *slot = reinterpret_cast<f32x4v *>(lds) + (wl * kMergeSlots) * kWave + lane;
+    if (grp == 1) {
+#pragma unroll
+        for (int dt = 0; dt < 8; dt++) slot[dt * kWave] = o_acc[dt];
+        slot[8 * kWave] = l_acc;
+        slot[9 * kWave] = f32x4v{m, 0.0f, 0.0f, 0.0f};
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float m1 = slot[9 * kWave][0];
+    const float mm = fmaxf(m, m1);
+    const float f0 = mm == -INFINITY ? 0.0f : exp2_fast(m - mm);   // per query ql
+    const float f1 = mm == -INFINITY ? 0.0f : exp2_fast(m1 - mm);
+    float c0[4], c1[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) c0[r] = __shfl(f0, 4 * g + r, kWave), c1[r] = __shfl(f1, 4 * g + r, kWave);
+    const f32x4v l1 = slot[8 * kWave];
     f16 *out = static_cast<f16 *>(a.out);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        const int i = 16 * (wave % 4) + 4 * g + r;
+        const int i = 16 * (wl % 4) + 4 * g + r;
+        const float l = l_acc[r] * c0[r] + l1[r] * c1[r];
+        const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         if (i >= nt) continue;
-        const float inv = l_acc[r] > 0.0f ? 1.0f / l_acc[r] : 0.0f;
         f16 *row = out + (static_cast<int64_t>(t0 + i) * a.n_heads + head) * kHeadDim;
 #pragma unroll
-        for (int dt = 0; dt < 8; dt++) row[16 * dt + ql] = static_cast<f16>(o_acc[dt][r] * inv);
+        for (int dt = 0; dt < 8; dt++) {
+            const float o = o_acc[dt][r] * c0[r] + slot[dt * kWave][r] * c1[r];
+            row[16 * dt + ql] = static_cast<f16>(o * inv);
+        }
     }
 }
-
 }  // namespace
 
 hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream) {
