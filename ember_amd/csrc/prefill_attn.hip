@@ -191,8 +191,11 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
                                         __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x05040100u));
             const uint2 hi = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x07060302u),
                                         __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x07060302u));
-            *reinterpret_cast<uint2 *>(&vl[(2 * dp) * kVRow + 4 * kq]) = lo;
-            *reinterpret_cast<uint2 *>(&vl[(2 * dp + 1) * kVRow + 4 * kq]) = hi;
+            // The 4-key unit is XOR-swizzled by bit 4 of the dim, so lanes dp and
+            // dp + 8 (rows 36 dwords apart) land on different banks.
+            const int unit = kq ^ ((dp >> 3) & 1);
+            *reinterpret_cast<uint2 *>(&vl[(2 * dp) * kVRow + 4 * unit]) = lo;
+            *reinterpret_cast<uint2 *>(&vl[(2 * dp + 1) * kVRow + 4 * unit]) = hi;
         }
     };
 
@@ -263,8 +266,9 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
             for (int dt = 0; dt < 8; dt++) {
                 const f16 *vrow = &vl[(16 * dt + ql) * kVRow];
-                const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * g);
-                const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * g);
+                const int gs = g ^ (dt & 1);  // the staging swizzle: bit 4 of the dim is dt's low bit
+                const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * gs);
+                const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * gs);
                 const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o_acc[dt], 0, 0, 0);
             }
