@@ -310,6 +310,7 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {
     EMBER_CHECK(T_ > 0, "layer() before plan()");
     EMBER_CHECK(qkv && out, "layer(): null qkv or out");
+    EMBER_CHECK(reinterpret_cast<uintptr_t>(qkv) % 16 == 0, "layer(): qkv must be 16-byte aligned");
     void *kc = k_pool(l), *vc = v_pool(l);
 
     EmberQkvArgs qa{};

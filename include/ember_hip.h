@@ -324,7 +324,8 @@ void ember_kv_destroy(EmberPagedKv *kv);
  * step behind), and the stream then needs no cross-stream wait. */
 int32_t ember_kv_plan(EmberPagedKv *kv, const EmberStepBatch *batch);
 /* One layer of the planned step: append K/V of every new token, then attention
- * for every token into out [num_tokens, n_heads, head_dim] (cuda_backend.cu:357-361). */
+ * for every token into out [num_tokens, n_heads, head_dim] (cuda_backend.cu:357-361).
+ * qkv must be 16-byte aligned. */
 int32_t ember_kv_layer(EmberPagedKv *kv, int32_t layer, const void *qkv, const float *q_norm, const float *k_norm,
                        const float *bias, void *out);
 /* One layer's buffers for a decode step replayed as a graph. */

@@ -372,3 +372,20 @@ def test_attention_block_matches_oracle(device):
     d_got, d_want = got - h0, ho - h0
     assert np.isfinite(got).all()
     assert float(np.abs(d_got - d_want).max()) / float(np.abs(d_want).max()) < 5e-3
+
+
+def test_layer_rejects_misaligned_qkv(device):
+    """ember_kv_layer refuses a qkv that is not 16-byte aligned (the append kernel moves 8 elements per
+    access) with an error, before any launch; the same step then runs from an aligned buffer."""
+    from ember_amd import _lib
+
+    w = World(device, torch.float16, num_blocks=8)
+    w.kv.plan(StepBatch(tokens=[0], positions=[0], query_start=[0, 1], context_len=[1], block_tables=[0], max_blocks=1))
+    buf = torch.zeros(W + 8, dtype=torch.float16, device=device)
+    out = torch.zeros((1, H, D), dtype=torch.float16, device=device)
+    rc = _lib.lib().ember_kv_layer(w.kv._h, 0, buf.data_ptr() + 2, None, None, None, out.data_ptr())
+    assert rc == _lib.ERR_INVALID
+    assert "16-byte aligned" in _lib.last_error()
+    w.kv.layer(0, buf[:W].view(1, W), out)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
