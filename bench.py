@@ -35,6 +35,7 @@ POOL_PAGES = 8192
 PAGE = 16
 SEED = 20261005
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA (no sparsity)
 KV_BYTES_PER_TOKEN = 2 * KVH * D * 2  # f16 K + V of one token, one layer: 4096 B
 # Per new token per layer: qkv in 8 KiB + q out 4 KiB + KV append 4 KiB + q in 4 KiB + attention out 4 KiB.
 TOKEN_BYTES = 8192 + 4096 + 4096 + 4096 + 4096
@@ -369,10 +370,12 @@ def _timed(path, step, steps, warmup):
     alloc_us = path.alloc_s / steps * 1e6
     path.kv.set_timing(True)
     path.kv.timing()
+    path.kv.prefill_timing()
     for _ in range(steps):
         step()
     path.stream.synchronize()
     launches, kernel_ms = path.kv.timing()
+    path.prefill_timed = path.kv.prefill_timing()  # (launches, total ms) of the prefill tiles in the same pass
     path.kv.set_timing(False)
     return wall / steps, bytes_ / steps, alloc_us, launches, kernel_ms
 
@@ -575,6 +578,7 @@ def run_config3(args) -> dict:
     for s in range(NPRE):
         admit(s, CHUNK * NCHUNK)
     cow = {"copies": 0}
+    prefill_flops = []  # per step, per layer
 
     def step():
         # copy-on-write before any write into a shared page
@@ -591,11 +595,14 @@ def run_config3(args) -> dict:
                     cow["copies"] += 1
         pos, qs = [], [0]
         kv_tokens = 0
+        flops = 0  # prefill tiles, per layer: QK and PV, 2 flops per multiply-add, over keys 0..pos of every head
         for s in range(NPRE):
             c0 = PREFIX + CHUNK * chunk_of[s]
             pos.append(np.arange(c0, c0 + CHUNK))
             qs.append(qs[-1] + CHUNK)
             kv_tokens += c0 + CHUNK
+            flops += 4 * D * H * (CHUNK * c0 + CHUNK * (CHUNK + 1) // 2)
+        prefill_flops.append(flops)
         for s in range(NPRE, NSEQ):
             path.ensure(s, int(ctx[s]) + 1)
             pos.append(np.array([ctx[s]]))
@@ -616,11 +623,18 @@ def run_config3(args) -> dict:
     assert bm.refcount(prefix_blocks[0]) == NSEQ and bm.check() == "", bm.check()
     gbs = step_bytes / step_s / 1e9
     T = NPRE * CHUNK + NSEQ - NPRE
+    p_launches, p_ms = path.prefill_timed
+    p_us = p_ms / max(p_launches, 1) * 1e3
+    p_tflops = float(np.mean(prefill_flops[-args.steps:])) / (p_us * 1e-6) / 1e12 if p_launches else None
     return {
         "metric": "continuous-batching mixed step tokens/s and % HBM peak (Qwen3-1.7B shape, 4 x 512 prefill + 60 decode)",
         "value": round(T / step_s, 1), "unit": "tokens/s", "ms_per_step": round(step_s * 1e3, 4),
         "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "prefill_kernel_avg_us": round(p_us, 2),
+        "prefill_mfma": None if p_tflops is None else {
+            "achieved": round(p_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(p_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
         "host_blockmanager_us_per_step": round(alloc_us, 2), "cow_copies": cow["copies"],
         "prefix_refcount": bm.refcount(prefix_blocks[0]),
         "config": {"workload": "BASELINE configs[2]: 64 sequences sharing a 1024-token prefix (64 sealed pages), "

@@ -153,6 +153,7 @@ PROTOTYPES = {
     "ember_kv_plan_info": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), POINTER(c_int32), POINTER(c_int32)]),
     "ember_kv_set_timing": (c_int32, [c_void_p, c_int32]),
     "ember_kv_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
+    "ember_kv_prefill_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
 }
 
 _lib = None

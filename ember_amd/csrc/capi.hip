@@ -1,6 +1,7 @@
 // C ABI of the kernel launchers (include/ember_hip.h, part 1): argument
 // validation, instance selection, error reporting. Nothing here throws; every
 // failure is a return code plus a per-thread message.
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -101,6 +102,24 @@ int ember_hip_decode_step(const EmberQkvArgs *qkv, const EmberAttnArgs *attn, vo
 
 }  // extern "C"
 
+int ember::hip::prefill_attn(const EmberPrefillArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "prefill_attn: null arguments");
+    if (int e = check_heads("prefill_attn", a->head_dim, a->n_heads, a->n_kv)) return e;
+    const int G = a->n_heads / a->n_kv;
+    if (G > 8) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1..8 (got %d)", G);
+    if (a->dtype != EMBER_DTYPE_F16) return set_error(EMBER_ERR_INVALID, "prefill_attn: the MFMA path takes f16 only");
+    if (a->num_tiles < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: bad sizes");
+    if (!(a->scale > 0.0f) || !std::isfinite(a->scale))  // the block max is taken before scaling
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: scale must be positive and finite");
+    if (a->num_tiles == 0) return EMBER_OK;
+    if (!a->q || !a->k_cache || !a->v_cache || !a->tile_start || !a->tile_end || !a->tile_seq || !a->positions ||
+        !a->block_tables || !a->out)
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: a required pointer is null");
+    return hip_status(launch_prefill(*a, stream, start, stop), "prefill_attn");
+}
+
 int ember::hip::decode_rows(int G, int max_run) {
     for (int r : kDecodeRowInstances)
         if (r >= G * max_run) return r;
@@ -161,19 +180,7 @@ int ember::hip::paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEven
 extern "C" {
 
 int ember_hip_prefill_attn(const EmberPrefillArgs *a, void *stream) {
-    g_last_error.clear();
-    if (!a) return set_error(EMBER_ERR_INVALID, "prefill_attn: null arguments");
-    if (int e = check_heads("prefill_attn", a->head_dim, a->n_heads, a->n_kv)) return e;
-    const int G = a->n_heads / a->n_kv;
-    if (G > 8) return set_error(EMBER_ERR_INVALID, "prefill_attn: query heads per kv head must be 1..8 (got %d)", G);
-    if (a->dtype != EMBER_DTYPE_F16) return set_error(EMBER_ERR_INVALID, "prefill_attn: the MFMA path takes f16 only");
-    if (a->num_tiles < 0 || a->max_blocks <= 0 || a->num_blocks <= 0)
-        return set_error(EMBER_ERR_INVALID, "prefill_attn: bad sizes");
-    if (a->num_tiles == 0) return EMBER_OK;
-    if (!a->q || !a->k_cache || !a->v_cache || !a->tile_start || !a->tile_end || !a->tile_seq || !a->positions ||
-        !a->block_tables || !a->out)
-        return set_error(EMBER_ERR_INVALID, "prefill_attn: a required pointer is null");
-    return hip_status(launch_prefill(*a, static_cast<hipStream_t>(stream)), "prefill_attn");
+    return prefill_attn(a, static_cast<hipStream_t>(stream), nullptr, nullptr);
 }
 
 int ember_hip_copy_pages(const EmberCopyArgs *a, void *stream) {

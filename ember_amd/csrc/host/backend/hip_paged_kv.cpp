@@ -108,7 +108,8 @@ HipPagedKv::~HipPagedKv() {
         (void)hipStreamSynchronize(upload_stream_);
         (void)hipStreamDestroy(upload_stream_);
     }
-    for (hipEvent_t e : timing_events_) (void)hipEventDestroy(e);
+    for (const Timing *t : {&decode_timing_, &prefill_timing_})
+        for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
     for (int i = 0; i < 2; i++) {
         if (staged_[i]) (void)hipEventDestroy(staged_[i]);
         if (consumed_[i]) (void)hipEventDestroy(consumed_[i]);
@@ -367,17 +368,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         at.work_desc = d_work_desc_;
         at.merge_counters = merge_counters_;
         hipEvent_t start = nullptr, stop = nullptr;
-        if (timing_) {  // the kernel's own dispatch is timed (hipExtLaunchKernel), not the gap before it
-            if (timing_used_ + 2 > timing_events_.size())
-                for (int i = 0; i < 2; i++) {
-                    hipEvent_t e;
-                    EMBER_HIP_CHECK(hipEventCreate(&e));
-                    timing_events_.push_back(e);
-                }
-            start = timing_events_[timing_used_];
-            stop = timing_events_[timing_used_ + 1];
-            timing_used_ += 2;
-        }
+        if (timing_) decode_timing_.next(&start, &stop);  // the kernel's own dispatch (hipExtLaunchKernel), not the gap before it
         check_abi(hip::paged_decode(&at, stream_, start, stop, fused_ ? &qa : nullptr), "paged_decode");
     }
     if (tiles_ > 0) {
@@ -399,23 +390,41 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         pa.out = out;
         pa.num_blocks = opt_.num_blocks + 1;
         pa.dtype = opt_.dtype;
-        check_abi(ember_hip_prefill_attn(&pa, stream_), "prefill_attn");
+        hipEvent_t start = nullptr, stop = nullptr;
+        if (timing_) prefill_timing_.next(&start, &stop);
+        check_abi(hip::prefill_attn(&pa, stream_, start, stop), "prefill_attn");
     }
 }
 
-int HipPagedKv::collect_timing(double *total_ms) {
+void HipPagedKv::Timing::next(hipEvent_t *start, hipEvent_t *stop) {
+    if (used + 2 > events.size())
+        for (int i = 0; i < 2; i++) {
+            hipEvent_t e;
+            EMBER_HIP_CHECK(hipEventCreate(&e));
+            events.push_back(e);
+        }
+    *start = events[used];
+    *stop = events[used + 1];
+    used += 2;
+}
+
+int HipPagedKv::Timing::collect(double *total_ms) {
     double ms = 0;
-    for (size_t i = 0; i + 1 < timing_used_; i += 2) {
-        EMBER_HIP_CHECK(hipEventSynchronize(timing_events_[i + 1]));
+    for (size_t i = 0; i + 1 < used; i += 2) {
+        EMBER_HIP_CHECK(hipEventSynchronize(events[i + 1]));
         float one = 0;
-        EMBER_HIP_CHECK(hipEventElapsedTime(&one, timing_events_[i], timing_events_[i + 1]));
+        EMBER_HIP_CHECK(hipEventElapsedTime(&one, events[i], events[i + 1]));
         ms += one;
     }
-    const int launches = static_cast<int>(timing_used_ / 2);
-    timing_used_ = 0;
+    const int launches = static_cast<int>(used / 2);
+    used = 0;
     if (total_ms) *total_ms = ms;
     return launches;
 }
+
+int HipPagedKv::collect_timing(double *total_ms) { return decode_timing_.collect(total_ms); }
+
+int HipPagedKv::collect_prefill_timing(double *total_ms) { return prefill_timing_.collect(total_ms); }
 
 int HipPagedKv::token_bucket(int T) {
     static const int buckets[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 40, 48, 56, 64};

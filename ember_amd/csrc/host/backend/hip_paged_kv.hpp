@@ -84,10 +84,12 @@ public:
     int num_splits() const { return splits_; }
     hipStream_t stream() const { return stream_; }
 
-    // Benchmark timing of the paged-decode kernel (events around each launch).
+    // Benchmark timing of the paged-decode and prefill kernels (events around each launch).
     void set_timing(bool on) { timing_ = on; }
-    // Waits for the recorded launches; returns their count and total ms, then starts over.
+    // Waits for the recorded paged-decode launches; returns their count and total ms, then starts over.
     int collect_timing(double *total_ms);
+    // The same for the prefill-tile launches.
+    int collect_prefill_timing(double *total_ms);
 
 private:
     // graph_splits > 0: a graph step's plan, with num_splits fixed to it and the
@@ -136,8 +138,13 @@ private:
     int num_work_ = 0;
 
     bool timing_ = false;
-    std::vector<hipEvent_t> timing_events_;  // start/stop pairs, reused after collect_timing
-    size_t timing_used_ = 0;
+    struct Timing {  // start/stop pairs, reused after collection
+        std::vector<hipEvent_t> events;
+        size_t used = 0;
+        void next(hipEvent_t *start, hipEvent_t *stop);
+        int collect(double *total_ms);
+    };
+    Timing decode_timing_, prefill_timing_;
 };
 
 }  // namespace ember

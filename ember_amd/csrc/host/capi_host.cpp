@@ -261,4 +261,12 @@ int32_t ember_kv_timing(EmberPagedKv *h, int32_t *launches, double *total_ms) {
     });
 }
 
+int32_t ember_kv_prefill_timing(EmberPagedKv *h, int32_t *launches, double *total_ms) {
+    return guarded("kv_prefill_timing", [&] {
+        const int n = h->kv.collect_prefill_timing(total_ms);
+        if (launches) *launches = n;
+        return EMBER_OK;
+    });
+}
+
 }  // extern "C"

@@ -28,7 +28,13 @@ hipError_t launch_decode_step(const EmberQkvArgs &qa, const EmberAttnArgs &a, in
 int paged_decode(const EmberAttnArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop,
                  const EmberQkvArgs *qkv = nullptr);
 
-hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream);
+// Given events, the prefill kernel's own dispatch is timed into them.
+hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEvent_t start = nullptr,
+                          hipEvent_t stop = nullptr);
+
+// Validation + launch behind ember_hip_prefill_attn, for in-library callers
+// that time the kernel. Returns an EMBER_* / hipError_t code.
+int prefill_attn(const EmberPrefillArgs *a, hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
 

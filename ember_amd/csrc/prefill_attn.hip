@@ -33,6 +33,8 @@
 //                 products pair up (k order inside one MFMA is free).
 // P is rounded to f16 for the MFMA and the row sums are one more MFMA of the
 // same P against ones, so numerator and denominator agree.
+#include <hip/hip_ext.h>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -314,15 +316,15 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 }
 }  // namespace
 
-hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream) {
+hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const int G = a.n_heads / a.n_kv;
     const int hg = G % 2 == 0 ? 2 : 1;
     const dim3 grid(static_cast<unsigned>(a.num_tiles), static_cast<unsigned>(a.n_heads / hg));
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)
-        hipLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, a, scale_log2);
+        hipExtLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, start, stop, 0, a, scale_log2);
     else
-        hipLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, a, scale_log2);
+        hipExtLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, start, stop, 0, a, scale_log2);
     return hipGetLastError();
 }
 

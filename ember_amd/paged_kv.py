@@ -153,6 +153,12 @@ class PagedKv:
         check(_lib.lib().ember_kv_timing(self._h, ctypes.byref(n), ctypes.byref(ms)), "kv_timing")
         return n.value, ms.value
 
+    def prefill_timing(self) -> tuple[int, float]:
+        """(launches, total ms) of the prefill-tile kernel since the last call, from HIP events."""
+        n, ms = ctypes.c_int32(), ctypes.c_double()
+        check(_lib.lib().ember_kv_prefill_timing(self._h, ctypes.byref(n), ctypes.byref(ms)), "kv_prefill_timing")
+        return n.value, ms.value
+
     def plan_info(self) -> tuple[int, int, int, bool]:
         """(decode runs, prefill tiles, splits, fused) of the current plan."""
         r, t, s, f = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int32()

@@ -362,10 +362,13 @@ int32_t ember_kv_plan_info(const EmberPagedKv *kv, int32_t *decode_runs, int32_t
                            int32_t *fused);
 /* Kernel timing for benchmarks: while on, every layer() records HIP events on
  * the path's stream right before and right after the paged-decode kernel
- * (before the split merge). ember_kv_timing waits for them and returns the
- * number of timed launches and their total duration in ms, then starts over. */
+ * (before the split merge) and the prefill-tile kernel. ember_kv_timing waits
+ * for the paged-decode ones and returns the number of timed launches and their
+ * total duration in ms, then starts over. */
 int32_t ember_kv_set_timing(EmberPagedKv *kv, int32_t on);
 int32_t ember_kv_timing(EmberPagedKv *kv, int32_t *launches, double *total_ms);
+/* The same for the prefill-tile kernel's launches (timed while timing is on). */
+int32_t ember_kv_prefill_timing(EmberPagedKv *kv, int32_t *launches, double *total_ms);
 
 #ifdef __cplusplus
 }

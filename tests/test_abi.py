@@ -53,6 +53,9 @@ def test_launchers_reject_bad_arguments_without_a_gpu():
     pf = _lib.PrefillArgs()
     pf.head_dim, pf.n_heads, pf.n_kv, pf.dtype = 128, 16, 8, _lib.DTYPE_F32
     assert lib.ember_hip_prefill_attn(pf, None) == _lib.ERR_INVALID
+    pf.dtype, pf.max_blocks, pf.num_blocks, pf.num_tiles, pf.scale = _lib.DTYPE_F16, 4, 4, 1, 0.0
+    assert lib.ember_hip_prefill_attn(pf, None) == _lib.ERR_INVALID  # the block max is taken before scaling
+    assert "scale" in _lib.last_error()
     assert lib.ember_hip_copy_pages(None, None) == _lib.ERR_INVALID
     g = _lib.GemvArgs()
     g.M, g.N, g.K, g.lda, g.ldc, g.epilogue = 65, 16, 64, 64, 16, 0  # M above 64
