@@ -37,8 +37,10 @@ SEED = 20261005
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, 8 TB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense f16 MFMA (no sparsity)
 KV_BYTES_PER_TOKEN = 2 * KVH * D * 2  # f16 K + V of one token, one layer: 4096 B
-# Per new token per layer: qkv in 8 KiB + q out 4 KiB + KV append 4 KiB + q in 4 KiB + attention out 4 KiB.
+# Per new token per layer: qkv in 8 KiB + q out 4 KiB + KV append 4 KiB + q in 4 KiB + attention out 4 KiB
+# when the append is its own launch; the fused append + attention keeps q on chip (16 KiB).
 TOKEN_BYTES = 8192 + 4096 + 4096 + 4096 + 4096
+FUSED_TOKEN_BYTES = 8192 + 4096 + 4096
 METRIC = "paged decode-attn+append tokens/s and % HBM peak (Qwen3-1.7B shape, batch 32)"
 
 
@@ -405,7 +407,7 @@ def run_config5(args) -> dict:
         path.run(range(B5), pos, qs)
         kv_bytes = KV_BYTES_PER_TOKEN * int((ctx + Q).sum())
         ctx[:] += 1 + acc_rng.integers(0, Q, B5)
-        return N_LAYERS * (kv_bytes + TOKEN_BYTES * B5 * Q)
+        return N_LAYERS * (kv_bytes + FUSED_TOKEN_BYTES * B5 * Q)
 
     step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
     gbs = step_bytes / step_s / 1e9
@@ -729,7 +731,7 @@ def run_config4(args) -> dict:
             path.release(s)
         order[:] = [s for s in order if s not in newest] + newest
         paused = newest
-        return N_LAYERS * (kv_bytes + TOKEN_BYTES * len(running))
+        return N_LAYERS * (kv_bytes + FUSED_TOKEN_BYTES * len(running))
 
     step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
     gbs = step_bytes / step_s / 1e9
@@ -827,12 +829,13 @@ def main() -> int:
 
     ms_per_step = wall * 1e3 / args.steps
     tokens_s = BATCH * args.steps / wall
-    step_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + TOKEN_BYTES * BATCH)
-    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     # Decode kernel roofline: algorithmic bytes per launch = K+V of every context token, plus per new token
     # either the query (4 KiB, unfused) or, fused, qkv in (8 KiB) + its K/V written (4 KiB) + the output (4 KiB).
     fused = w.kv.fused()
-    per_token = 16384 if fused else 4096
+    per_token = FUSED_TOKEN_BYTES if fused else 4096
+    token_bytes = FUSED_TOKEN_BYTES if fused else TOKEN_BYTES
+    step_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + token_bytes * BATCH)
+    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
     kernel_bytes = (KV_BYTES_PER_TOKEN * sum_ctx_inst + per_token * BATCH * args.steps) * N_LAYERS
     kernel_gbs = kernel_bytes / (kernel_ms * 1e-3) / 1e9 if kernel_ms > 0 else 0.0
     avg_us = kernel_ms / max(launches, 1) * 1e3
