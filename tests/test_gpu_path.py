@@ -389,3 +389,37 @@ def test_layer_rejects_misaligned_qkv(device):
     w.kv.layer(0, buf[:W].view(1, W), out)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
+
+
+def test_config2_full_size_decode_step(rng, device):
+    """BASELINE config 2 at full size, one layer: 32 sequences with cached contexts U[256, 4096], one new token
+    each, pages scattered by a random permutation of an 8192-page pool. This is the step bench.py times (fused
+    append + attention, work list, in-kernel split merge): attention within 2e-3 of the oracle, and the new K/V
+    slots equal to the oracle's to f16 rounding."""
+    NB, S = 8192, 32
+    w = World(device, torch.float16, num_blocks=NB, max_position=4096 + 2 * PAGE)
+    ctx = rng.integers(256, 4097, S)
+    mb = 4096 // PAGE + 2
+    tables = np.zeros((S, mb), np.int32)
+    pages, used = rng.permutation(NB).astype(np.int32), 0
+    for s in range(S):
+        n = int(ctx[s]) // PAGE + 1  # the new token at position ctx[s] included
+        tables[s, :n] = pages[used:used + n]
+        used += n
+    # cached K/V: every slot of the pool random, the same values in the oracle's f32 pools
+    for which, ref in (("k", w.ko[0]), ("v", w.vo[0])):
+        pool = w.kv.pool_view(0, which)
+        pool.copy_(torch.randn(pool.shape, dtype=torch.float32, device=device).mul_(0.5).to(torch.float16))
+        ref[:] = pool.float().cpu().numpy()
+    torch.cuda.synchronize()
+    positions = ctx.astype(np.int32)
+    qkv = _acts(rng, S, 1, True)
+    (got, want), = w.step(positions, np.arange(S + 1, dtype=np.int32), tables, qkv)
+    assert w.kv.fused(), "a pure decode step of one token per sequence runs fused"
+    assert np.isfinite(got).all()
+    assert rel_err(got, want) < 2e-3
+    kg, vg = w.pools(0)
+    for s in range(S):
+        b, slot = tables[s, ctx[s] // PAGE], ctx[s] % PAGE
+        np.testing.assert_allclose(kg[b, :, slot], w.ko[0][b, :, slot], rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(vg[b, :, slot], w.vo[0][b, :, slot], rtol=1e-3, atol=1e-3)
