@@ -423,3 +423,46 @@ def test_config2_full_size_decode_step(rng, device):
         b, slot = tables[s, ctx[s] // PAGE], ctx[s] % PAGE
         np.testing.assert_allclose(kg[b, :, slot], w.ko[0][b, :, slot], rtol=1e-3, atol=1e-3)
         np.testing.assert_allclose(vg[b, :, slot], w.vo[0][b, :, slot], rtol=1e-3, atol=1e-3)
+
+
+def test_config4_pool_size_and_long_contexts(rng, device):
+    """BASELINE config 4's pool at one layer: 131,072 pages, so one layer's K (or V) pool is 4.3 GB and element
+    offsets pass 2^31, and contexts up to 16,384 tokens (32 splits of 512). Four sequences whose pages sit at the
+    top of the pool take a fused decode step through the path; the oracle gets a compacted copy of their pages."""
+    NB = 131072
+    kv = PagedKv(n_layers=1, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA, max_position=16384 + 2 * PAGE,
+                 num_blocks=NB, max_batch_tokens=64, max_seqs=8, dtype=torch.float16)
+    ctx = np.array([16384, 9000, 12345, 700])
+    S, mb = len(ctx), 16384 // PAGE + 2
+    top = rng.permutation(np.arange(NB - 4096, NB)).astype(np.int32)
+    tables, compact, used = np.zeros((S, mb), np.int32), np.zeros((S, mb), np.int32), 0
+    for s in range(S):
+        n = int(ctx[s]) // PAGE + 1  # the new token's page included
+        tables[s, :n], compact[s, :n] = top[used:used + n], np.arange(used, used + n)
+        used += n
+    ko, vo = np.zeros((used + 1, KVH, PAGE, D), np.float32), np.zeros((used + 1, KVH, PAGE, D), np.float32)
+    idx = torch.from_numpy(np.concatenate([tables[s, :int(ctx[s]) // PAGE + 1] for s in range(S)]).astype(np.int64))
+    for which, ref in (("k", ko), ("v", vo)):
+        vals = (0.5 * torch.randn((used, KVH, PAGE, D), dtype=torch.float32)).to(torch.float16)
+        kv.pool_view(0, which)[idx.to(device)] = vals.to(device)
+        ref[:used] = vals.float().numpy()
+    positions, qs = ctx.astype(np.int32), np.arange(S + 1, dtype=np.int32)
+    qkv = rng.standard_normal((S, W)).astype(np.float16)
+    qn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kv.plan(StepBatch(tokens=[0] * S, positions=positions.tolist(), query_start=qs.tolist(),
+                      context_len=(ctx + 1).tolist(), block_tables=tables.reshape(-1).tolist(), max_blocks=mb))
+    out = torch.full((S, H, D), float("nan"), dtype=torch.float16, device=device)
+    kv.layer(0, torch.from_numpy(qkv).to(device), out, q_norm=torch.from_numpy(qn).to(device),
+             k_norm=torch.from_numpy(kn).to(device))
+    torch.cuda.synchronize()
+    assert kv.fused()
+    q_ref = oracle.append_layer(qkv.astype(np.float32), positions, qs, compact, ko, vo, n_heads=H, n_kv=KVH,
+                                inv_freq_=oracle.inv_freq(THETA, D), eps=EPS, q_norm=qn, k_norm=kn, num_blocks=used + 1,
+                                kv_f16=False)
+    want = oracle.attention_layer(q_ref, positions, qs, compact, ko, vo, n_heads=H, n_kv=KVH, num_blocks=used + 1,
+                                  kv_f16=False, threads=8)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, want) < 2e-3
+    del kv
