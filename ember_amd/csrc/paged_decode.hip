@@ -256,6 +256,13 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 
 // Merges this lane's (m, l, acc) with the lane `mask` away; both lanes end
 // with the same values.
+// The running max of a row before any visible key: finite and far below any
+// score (|q.k| * scale of f16 vectors is below 1e12), so a row's first visible
+// key gives corr = 2^(kNoMax - max) = 0 exactly, as -inf would, while an empty
+// row keeps l = 0 and O = 0; the merges below treat it like -inf (weight 0
+// against any real max, and zeros when every part is empty).
+constexpr float kNoMax = -1.0e30f;
+
 __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8], int mask) {
     const float mo = __shfl_xor(m, mask, kWave), lo = __shfl_xor(l, mask, kWave);
     const float M = fmaxf(m, mo);
@@ -480,7 +487,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     float m[ROWS], l[ROWS], acc[ROWS][8];
 #pragma unroll
     for (int row = 0; row < ROWS; row++) {
-        m[row] = -INFINITY;
+        m[row] = kNoMax;
         l[row] = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) acc[row][e] = 0.0f;
@@ -614,11 +621,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
                     if (!vis[row][i]) s[i] = -INFINITY;
                 }
             }
+            // m starts at kNoMax, not -inf, so mn is always finite: no select guards
+            // the subtraction, and corr is 2^0 = 1 exactly when the max stays.
             const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-            const float ref = mn == -INFINITY ? 0.0f : mn;
-            const float corr = m[row] == mn ? 1.0f : exp2_hw(m[row] - ref);
+            const float corr = exp2_hw(m[row] - mn);
 #pragma unroll
-            for (int i = 0; i < 4; i++) pj[row][i] = exp2_hw(s[i] - ref);  // 2^-inf = 0 for hidden keys
+            for (int i = 0; i < 4; i++) pj[row][i] = exp2_hw(s[i] - mn);  // 2^-inf = 0 for hidden keys
             l[row] = l[row] * corr + ((pj[row][0] + pj[row][1]) + (pj[row][2] + pj[row][3]));
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
