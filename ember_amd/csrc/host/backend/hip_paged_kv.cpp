@@ -93,9 +93,15 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&consumed_[i], hipEventDisableTiming));
     }
     EMBER_HIP_CHECK(hipStreamCreateWithFlags(&upload_stream_, hipStreamNonBlocking));  // default priority
+    for (int i = 0; i < 2; i++) {  // copy-on-write pair lists: kCowPairs (src, dst) pairs per buffer
+        cow_dev_[i] = device_alloc<int32_t>(2 * static_cast<size_t>(kCowPairs));
+        EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&cow_host_[i]), 2 * kCowPairs * sizeof(int32_t), 0));
+        EMBER_HIP_CHECK(hipEventCreateWithFlags(&cow_done_[i], hipEventDisableTiming));
+    }
     for (int i = 0; i < 2; i++) {  // every event starts out recorded, so the first plans wait on nothing pending
         EMBER_HIP_CHECK(hipEventRecord(staged_[i], stream_));
         EMBER_HIP_CHECK(hipEventRecord(consumed_[i], stream_));
+        EMBER_HIP_CHECK(hipEventRecord(cow_done_[i], stream_));
     }
     EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
 }
@@ -115,6 +121,9 @@ HipPagedKv::~HipPagedKv() {
         if (consumed_[i]) (void)hipEventDestroy(consumed_[i]);
         if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
         if (dev_ints_[i]) (void)hipFree(dev_ints_[i]);
+        if (cow_done_[i]) (void)hipEventDestroy(cow_done_[i]);
+        if (cow_host_[i]) (void)hipHostFree(cow_host_[i]);
+        if (cow_dev_[i]) (void)hipFree(cow_dev_[i]);
     }
     for (void *p : {k_, v_, q_, static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
                     static_cast<void *>(part_ml_), static_cast<void *>(merge_counters_)})
@@ -153,6 +162,9 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     int max_ctx = 0;
     max_run_ = 1;
     fused_ = true;
+    // A decode work-group holds at most 16 query rows (G heads x run tokens), so
+    // the run length shrinks as the group grows: 8 at G <= 2, 5 at G = 3, 4 at G = 4, 2 at G = 8.
+    const int run_cap = std::max(1, std::min(EMBER_MAX_RUN, kMaxDecodeRows / cfg_.group()));
     for (int s = 0; s < S; s++) {
         const int q0 = b.query_start[static_cast<size_t>(s)], q1 = b.query_start[static_cast<size_t>(s) + 1];
         EMBER_CHECK(q0 <= q1, "malformed query_start");
@@ -165,7 +177,7 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
             ctx = std::max(ctx, pos + 1);
             if (t > q0 && pos != b.positions[static_cast<size_t>(t) - 1] + 1) fused_ = false;
         }
-        if (q1 - q0 > EMBER_MAX_RUN) fused_ = false;  // one run per sequence, or runs would read each other's new slots
+        if (q1 - q0 > run_cap) fused_ = false;  // one run per sequence, or runs would read each other's new slots
         // Every page a token of this sequence reads must be a real block (or the spare).
         const int32_t *row = &b.block_tables[static_cast<size_t>(s) * b.max_blocks];
         for (int p = 0; p * kBlockSize < ctx; p++)
@@ -178,8 +190,8 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
                 tile_seq_.push_back(s);
             }
         } else {
-            for (int t = q0; t < q1; t += EMBER_MAX_RUN) {
-                const int n = std::min(EMBER_MAX_RUN, q1 - t);
+            for (int t = q0; t < q1; t += run_cap) {
+                const int n = std::min(run_cap, q1 - t);
                 int run_ctx = 0;
                 for (int i = 0; i < n; i++) run_ctx = std::max(run_ctx, b.positions[static_cast<size_t>(t + i)] + 1);
                 run_first_.push_back(static_cast<int32_t>(decode_.size()));
@@ -452,6 +464,18 @@ bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
     EMBER_CHECK(static_cast<int64_t>(b.block_tables.size()) == static_cast<int64_t>(S) * b.max_blocks &&
                     static_cast<int>(b.positions.size()) == T,
                 "decode_graph: malformed batch");
+    // The real rows are checked as plan() checks them, before padding widens
+    // their tables with the spare block: a position past the caller's own
+    // table would otherwise land in the spare block instead of failing.
+    for (int t = 0; t < T; t++) {
+        const int pos = b.positions[static_cast<size_t>(t)];
+        EMBER_CHECK(pos >= 0 && pos < b.max_blocks * kBlockSize, "token {} at position {} is beyond its block table", t,
+                    pos);
+        const int32_t *row = &b.block_tables[static_cast<size_t>(t) * b.max_blocks];
+        for (int p = 0; p <= pos / kBlockSize; p++)
+            EMBER_CHECK(row[p] >= 0 && row[p] <= opt_.num_blocks, "sequence {} page {} names block {} (pool of {})", t, p,
+                        row[p], opt_.num_blocks);
+    }
 
     // The padded step: real rows keep their table and continue with the spare
     // block; padding rows are sequences of one token at position 0 whose whole
@@ -524,28 +548,35 @@ void HipPagedKv::copy_blocks(std::span<const int32_t> src, std::span<const int32
     for (size_t i = 0; i < src.size(); i++)
         EMBER_CHECK(src[i] >= 0 && src[i] <= opt_.num_blocks && dst[i] >= 0 && dst[i] <= opt_.num_blocks,
                     "copy_blocks: pair {} ({} -> {}) is outside the pool", i, src[i], dst[i]);
-    const size_t n = src.size();
-    std::vector<int32_t> packed(2 * n);
-    std::copy(src.begin(), src.end(), packed.begin());
-    std::copy(dst.begin(), dst.end(), packed.begin() + static_cast<ptrdiff_t>(n));
-    int32_t *dev = device_alloc<int32_t>(2 * n);
-    EMBER_HIP_CHECK(hipMemcpyAsync(dev, packed.data(), 2 * n * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
-    EmberCopyArgs ca{};
-    ca.k_cache = k_;
-    ca.v_cache = v_;
-    ca.src_blocks = dev;
-    ca.dst_blocks = dev + n;
-    ca.n = static_cast<int32_t>(n);
-    ca.n_layers = cfg_.n_layers;
-    ca.layer_stride = layer_elems_;
-    ca.n_kv = cfg_.n_kv_heads;
-    ca.head_dim = cfg_.head_dim;
-    ca.num_blocks = opt_.num_blocks + 1;
-    ca.dtype = opt_.dtype;
-    const int code = ember_hip_copy_pages(&ca, stream_);
-    EMBER_HIP_CHECK(hipStreamSynchronize(stream_));  // the pair list is freed below
-    (void)hipFree(dev);
-    check_abi(code, "copy_pages");
+    // The pair list goes up through one of two pinned staging buffers into the
+    // matching preallocated device list, on stream_, ahead of the copy kernel.
+    // A buffer is reused once the copy kernel that read it has run (its event;
+    // normally long done), so nothing is allocated and the host does not wait
+    // for the stream.
+    for (size_t at = 0; at < src.size(); at += kCowPairs) {
+        const size_t n = std::min(src.size() - at, static_cast<size_t>(kCowPairs));
+        cow_stage_ ^= 1;
+        EMBER_HIP_CHECK(hipEventSynchronize(cow_done_[cow_stage_]));
+        int32_t *hp = cow_host_[cow_stage_], *dp = cow_dev_[cow_stage_];
+        std::copy_n(src.begin() + static_cast<ptrdiff_t>(at), n, hp);
+        std::copy_n(dst.begin() + static_cast<ptrdiff_t>(at), n, hp + n);
+        EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, 2 * n * sizeof(int32_t), hipMemcpyHostToDevice, stream_));
+        EmberCopyArgs ca{};
+        ca.k_cache = k_;
+        ca.v_cache = v_;
+        ca.src_blocks = dp;
+        ca.dst_blocks = dp + n;
+        ca.n = static_cast<int32_t>(n);
+        ca.n_layers = cfg_.n_layers;
+        ca.layer_stride = layer_elems_;
+        ca.n_kv = cfg_.n_kv_heads;
+        ca.head_dim = cfg_.head_dim;
+        ca.num_blocks = opt_.num_blocks + 1;
+        ca.dtype = opt_.dtype;
+        const int code = ember_hip_copy_pages(&ca, stream_);
+        EMBER_HIP_CHECK(hipEventRecord(cow_done_[cow_stage_], stream_));
+        check_abi(code, "copy_pages");
+    }
 }
 
 }  // namespace ember

@@ -10,8 +10,8 @@
 //
 // Routing: a sequence with >= 16 new tokens goes to 64-token MFMA prefill
 // tiles (f16 pools: the MFMA path); every other run, and every run of an f32
-// pool, is cut into runs of at most 8 tokens for the paged decode kernel,
-// which reads each page once per run. Decode splits are fixed 512-key chunks ([0, 512), [512, 1024), ...)
+// pool, is cut into runs of at most min(8, 16 / G) tokens for the paged decode
+// kernel, which reads each page once per run for its G x run query rows. Decode splits are fixed 512-key chunks ([0, 512), [512, 1024), ...)
 // at every batch size, so a token's result never depends on its batch.
 #pragma once
 
@@ -39,6 +39,7 @@ struct PagedKvOptions {
 class HipPagedKv {
 public:
     static constexpr int kFlashMinTokens = 16;  // a run this long uses prefill tiles (cuda_backend.cu:257)
+    static constexpr int kMaxDecodeRows = 16;   // query rows (G heads x run tokens) of the widest decode instance
 
     HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStream_t stream);
     ~HipPagedKv();
@@ -125,6 +126,13 @@ private:
     hipEvent_t consumed_[2] = {nullptr, nullptr}; // the kernels that read each buffer have run
     hipStream_t upload_stream_ = nullptr;
     int stage_ = 0;
+    // copy_blocks' pair lists, double-buffered: pinned staging, the device list
+    // the copy kernel reads, and an event recorded after that kernel.
+    static constexpr int kCowPairs = 4096;
+    int32_t *cow_host_[2] = {nullptr, nullptr};
+    int32_t *cow_dev_[2] = {nullptr, nullptr};
+    hipEvent_t cow_done_[2] = {nullptr, nullptr};
+    int cow_stage_ = 0;
     size_t ints_capacity_ = 0;
 
     // The current plan (device addresses into dev_ints_[stage_]).

@@ -121,8 +121,11 @@ def qk_norm_rope_store(qkv, q_out, k_pool, v_pool, ints: StepInts, *, n_heads, n
     check(_lib.lib().ember_hip_kv_append(a, _stream_handle(stream)), "kv_append")
 
 
-def decode_runs(ints: StepInts, token_list, max_run: int = MAX_RUN):
-    """Cuts a list of tokens into runs of consecutive tokens of one sequence (at most max_run each)."""
+def decode_runs(ints: StepInts, token_list, max_run: int = MAX_RUN, group: int = 1):
+    """Cuts a list of tokens into runs of consecutive tokens of one sequence, at most max_run each and at
+    most 16 // group (a decode work-group holds at most 16 query rows: group heads x run tokens), the cap
+    the C++ planner applies."""
+    max_run = max(1, min(max_run, 16 // group))
     first, count = [], []
     i, tl = 0, list(token_list)
     while i < len(tl):

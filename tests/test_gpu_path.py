@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from ember_amd import BlockManager
+from ember_amd import BlockManager, EmberError
 from ember_amd.paged_kv import PagedKv, StepBatch
 from helpers import D, PAGE, rel_err
 
@@ -23,18 +23,20 @@ EPS, THETA = 1e-6, 1e6
 class World:
     """The GPU path and the oracle side by side, driven with identical steps."""
 
-    def __init__(self, device, dtype, num_blocks, n_layers=1, max_position=8192, max_batch_tokens=2048, seed=0):
+    def __init__(self, device, dtype, num_blocks, n_layers=1, max_position=8192, max_batch_tokens=2048, seed=0,
+                 n_heads=H, n_kv=KVH, max_seqs=64):
         self.dev, self.dtype, self.NB, self.L = device, dtype, num_blocks, n_layers
-        self.kv = PagedKv(n_layers=n_layers, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,
+        self.H, self.KVH, self.W = n_heads, n_kv, (n_heads + 2 * n_kv) * D
+        self.kv = PagedKv(n_layers=n_layers, n_heads=n_heads, n_kv_heads=n_kv, rms_eps=EPS, rope_theta=THETA,
                           max_position=max_position, num_blocks=num_blocks, max_batch_tokens=max_batch_tokens,
-                          max_seqs=64, dtype=dtype)
+                          max_seqs=max_seqs, dtype=dtype)
         r = np.random.default_rng(seed)
         self.qn = [(1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(n_layers)]
         self.kn = [(1 + 0.1 * r.standard_normal(D)).astype(np.float32) for _ in range(n_layers)]
         self.qn_d = [torch.from_numpy(a).to(device) for a in self.qn]
         self.kn_d = [torch.from_numpy(a).to(device) for a in self.kn]
         # the oracle keeps f32 pools with the same number of blocks (+ the spare, never read)
-        self.ko = [np.zeros((num_blocks + 1, KVH, PAGE, D), np.float32) for _ in range(n_layers)]
+        self.ko = [np.zeros((num_blocks + 1, n_kv, PAGE, D), np.float32) for _ in range(n_layers)]
         self.vo = [np.zeros_like(self.ko[0]) for _ in range(n_layers)]
         self.inv = oracle.inv_freq(THETA, D)
 
@@ -53,15 +55,17 @@ class World:
         for layer in range(self.L):
             qkv = qkv_layers[layer]
             qkv_d = torch.from_numpy(qkv).to(self.dev, self.dtype)
-            out = torch.full((T, H, D), float("nan"), dtype=self.dtype, device=self.dev)
+            out = torch.full((T, self.H, D), float("nan"), dtype=self.dtype, device=self.dev)
             self.kv.layer(layer, qkv_d, out, q_norm=self.qn_d[layer], k_norm=self.kn_d[layer])
-            q_ref = oracle.append_layer(qkv, positions, query_start, tables, self.ko[layer], self.vo[layer], n_heads=H,
-                                        n_kv=KVH, inv_freq_=self.inv, eps=EPS, q_norm=self.qn[layer],
-                                        k_norm=self.kn[layer], num_blocks=self.NB + 1, kv_f16=False)
+            q_ref = oracle.append_layer(qkv, positions, query_start, tables, self.ko[layer], self.vo[layer],
+                                        n_heads=self.H, n_kv=self.KVH, inv_freq_=self.inv, eps=EPS,
+                                        q_norm=self.qn[layer], k_norm=self.kn[layer], num_blocks=self.NB + 1,
+                                        kv_f16=False)
             want = None
             if check:
                 want = oracle.attention_layer(q_ref, positions, query_start, tables, self.ko[layer], self.vo[layer],
-                                              n_heads=H, n_kv=KVH, num_blocks=self.NB + 1, kv_f16=False, threads=8)
+                                              n_heads=self.H, n_kv=self.KVH, num_blocks=self.NB + 1, kv_f16=False,
+                                              threads=8)
             torch.cuda.synchronize()
             res.append((out.float().cpu().numpy(), want))
         return res
@@ -74,8 +78,8 @@ class World:
         return 2e-3 if self.dtype == torch.float16 else 1e-5
 
 
-def _acts(rng, T, L, f16):
-    a = [rng.standard_normal((T, W)).astype(np.float32) for _ in range(L)]
+def _acts(rng, T, L, f16, width=W):
+    a = [rng.standard_normal((T, width)).astype(np.float32) for _ in range(L)]
     return [x.astype(np.float16).astype(np.float32) for x in a] if f16 else a
 
 
@@ -127,6 +131,41 @@ def test_mixed_step(rng, device, dtype):
     res = w.step(pos, qs, tables, _acts(rng, len(pos), 2, f16))
     for got, want in res:
         assert rel_err(got, want) < w.tol
+
+
+@pytest.mark.parametrize("heads", [(32, 8), (24, 8), (64, 8)], ids=["G4", "G3", "G8"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_group_sizes_verify_chunk_and_decode(rng, device, dtype, heads):
+    """Wider GQA groups (Qwen3-4B/8B have 32 query heads over 8 kv heads, G = 4; also G = 3 and G = 8): a
+    decode work-group holds at most 16 query rows, so the planner cuts runs at min(8, 16 / G) tokens. One step
+    with a 5-token verify run, a 12-token chunk (decode runs at every G), a 40-token prompt chunk (prefill tiles
+    for f16, decode runs for f32) and a single decode, checked against the oracle."""
+    f16 = dtype == torch.float16
+    n_heads, n_kv = heads
+    w = World(device, dtype, num_blocks=400, n_heads=n_heads, n_kv=n_kv, max_position=2048)
+    perm = rng.permutation(400).astype(np.int32)
+    ctx0 = [700, 300, 0, 1100]   # cached before the step
+    new = [5, 12, 40, 1]         # new tokens this step
+    tables = np.zeros((4, 80), np.int32)
+    at = 0
+    for s in range(4):
+        n_pages = (ctx0[s] + new[s] + PAGE - 1) // PAGE
+        tables[s, :n_pages] = perm[at:at + n_pages]
+        at += n_pages
+    for s in range(4):
+        if ctx0[s]:
+            w.step(np.arange(ctx0[s]), [0, ctx0[s]], tables[s:s + 1], _acts(rng, ctx0[s], 1, f16, w.W), check=False)
+    pos, qs = [], [0]
+    for s in range(4):
+        pos += list(range(ctx0[s], ctx0[s] + new[s]))
+        qs.append(len(pos))
+    (got, want), = w.step(pos, qs, tables, _acts(rng, len(pos), 1, f16, w.W))
+    assert np.isfinite(got).all()
+    assert rel_err(got, want) < w.tol
+    runs, tiles, _, fused = w.kv.plan_info()
+    cap = min(8, 16 // (n_heads // n_kv))
+    want_runs = sum(-(-n // cap) for n in new if not (f16 and n >= 16))
+    assert runs == want_runs and tiles == (1 if f16 else 0) and not fused
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -313,6 +352,42 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
     two = StepBatch(tokens=[0, 0], positions=np.array([5, 6], np.int32), query_start=np.array([0, 2], np.int32),
                     context_len=np.array([7], np.int32), block_tables=np.array(blocks[0][:1], np.int32), max_blocks=1)
     assert not ga.decode_graph(two, io)
+    # a real row whose position lies past its own table is refused, as plan() refuses it (padding would
+    # otherwise widen the table with the spare block and write the token there)
+    bad = StepBatch(tokens=[0], positions=np.array([16], np.int32), query_start=np.array([0, 1], np.int32),
+                    context_len=np.array([17], np.int32), block_tables=np.array(blocks[0][:1], np.int32), max_blocks=1)
+    with pytest.raises(EmberError, match="beyond its block table"):
+        ga.decode_graph(bad, io)
+    with pytest.raises(EmberError, match="beyond its block table"):
+        eb.plan(bad)
+
+
+def test_copy_blocks_many_pairs_back_to_back(rng, device):
+    """copy_blocks stages its pair lists through preallocated, double-buffered lists (no allocation, no host
+    wait): 5000 pairs (more than one list holds) and then 3 more pairs right behind them, every layer, K and V,
+    bit-exact."""
+    NB, L = 10240, 2
+    kv = PagedKv(n_layers=L, n_heads=H, n_kv_heads=KVH, max_position=256, num_blocks=NB, max_batch_tokens=64,
+                 max_seqs=8, dtype=torch.float16)
+    for layer in range(L):
+        for which in ("k", "v"):
+            pool = kv.pool_view(layer, which)
+            pool.copy_(torch.randn(pool.shape, device=device).to(torch.float16))
+    torch.cuda.synchronize()
+    before = [[kv.pool_view(layer, which).clone() for which in ("k", "v")] for layer in range(L)]
+    perm = rng.permutation(NB)
+    src1, dst1 = perm[:5000], perm[5000:10000]
+    src2, dst2 = perm[10000:10003], perm[10003:10006]
+    kv.copy_blocks(src1, dst1)
+    kv.copy_blocks(src2, dst2)
+    torch.cuda.synchronize()
+    for layer in range(L):
+        for i, which in enumerate(("k", "v")):
+            got, want = kv.pool_view(layer, which), before[layer][i].clone()
+            want[torch.from_numpy(dst1).to(device)] = before[layer][i][torch.from_numpy(src1).to(device)]
+            want[torch.from_numpy(dst2).to(device)] = before[layer][i][torch.from_numpy(src2).to(device)]
+            assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"layer {layer} {which}"
+    kv.close()
 
 
 def test_attention_block_matches_oracle(device):
