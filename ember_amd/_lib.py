@@ -18,6 +18,8 @@ BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
 MAX_SPLIT_LEN = 1024
+STATIC_MAX_PARTIALS = 49152
+STATIC_MAX_COUNTERS = 16384
 OK = 0
 ERR_INVALID = -1
 DTYPE_F16 = 0
@@ -112,6 +114,7 @@ STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, Layer
 PROTOTYPES = {
     "ember_hip_kv_append": (c_int32, [POINTER(QkvArgs), c_void_p]),
     "ember_hip_paged_decode": (c_int32, [POINTER(AttnArgs), c_void_p]),
+    "ember_hip_paged_decode_static": (c_int32, [POINTER(AttnArgs), c_void_p]),
     "ember_hip_decode_step": (c_int32, [POINTER(QkvArgs), POINTER(AttnArgs), c_void_p]),
     "ember_hip_prefill_attn": (c_int32, [POINTER(PrefillArgs), c_void_p]),
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),

@@ -27,6 +27,7 @@ SOURCES = [
     CSRC / "prefill_attn.hip",
     CSRC / "copy_pages.hip",
     CSRC / "linear.hip",
+    CSRC / "static_scratch.hip",
     CSRC / "host" / "kvcache" / "block_manager.cpp",
     CSRC / "host" / "backend" / "hip_paged_kv.cpp",
     CSRC / "host" / "capi_host.cpp",

@@ -137,6 +137,27 @@ typedef struct EmberAttnArgs {
  * head_dim must be 128; G in 1..8. */
 int ember_hip_paged_decode(const EmberAttnArgs *args, void *stream);
 
+/* Limits of ember_hip_paged_decode_static's scratch (per GPU, held until the
+ * process ends): (token, head, split) partials of 130 floats each, and
+ * (run, kv head) merge counters. */
+#define EMBER_STATIC_MAX_PARTIALS 49152
+#define EMBER_STATIC_MAX_COUNTERS 16384
+#define EMBER_STATIC_SCRATCH_BYTES (4 * EMBER_STATIC_MAX_COUNTERS + 4 * 130 * EMBER_STATIC_MAX_PARTIALS)
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). ember_hip_paged_decode with its scratch (split partials
+ * and merge counters) taken from a static device array of the library instead
+ * of args->part_acc / part_ml / merge_counters, which must be NULL; the splits
+ * are merged in the kernel, with the merge kernel's arithmetic and order, so
+ * the results are bit-identical to ember_hip_paged_decode's. Allocates
+ * nothing. Rejects (EMBER_ERR_INVALID) a call needing more than
+ * EMBER_STATIC_MAX_PARTIALS partials (T * n_heads * num_splits) or
+ * EMBER_STATIC_MAX_COUNTERS counters (runs * n_kv). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams or
+ * host threads) race. */
+int ember_hip_paged_decode_static(const EmberAttnArgs *args, void *stream);
+
 /* Append + attention in one launch, for a step in which every sequence's new
  * tokens form one decode run (decode: 1 token; speculative verify: k + 1 <= 8)
  * with consecutive positions. Each work-group computes its rows' q
