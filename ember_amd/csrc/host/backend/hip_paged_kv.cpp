@@ -82,10 +82,12 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_HIP_CHECK(hipMemcpyAsync(inv_freq_, inv.data(), inv.size() * sizeof(float), hipMemcpyHostToDevice, stream_));
 
     // Step integers: positions, token_seq, decode list, runs (2), tiles (3), tables, work items and their
-    // descriptors (kDescInts each, 128-byte aligned like every array here).
-    ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + 1) +
-                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * T * max_splits_) +
-                     pad32(static_cast<size_t>(kDescInts) * T * max_splits_) + 64;
+    // descriptors (kDescInts each, 128-byte aligned like every array here). Work items exist for decode
+    // runs only, at most one per (decode token, split).
+    const size_t items = static_cast<size_t>(decode_cap_) * max_splits_;
+    ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + static_cast<size_t>(opt_.max_seqs)) +
+                     static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * items) +
+                     pad32(static_cast<size_t>(kDescInts) * items) + 64;
     for (int i = 0; i < 2; i++) {
         dev_ints_[i] = device_alloc<int32_t>(ints_capacity_);
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));

@@ -399,15 +399,17 @@ int32_t ember_oracle_append_layer(const float *qkv, int32_t T, int32_t H, int32_
         if (seq[static_cast<size_t>(t)] < 0 || pos < 0 || pos / kPage >= max_blocks) return -1;
         for (int h = 0; h < H; h++) {
             float *q = q_out + (static_cast<int64_t>(t) * H + h) * D;
-            for (int d = 0; d < D; d++) q[d] = src[h * D + d] + (bias ? bias[h * D + d] : 0.0f);
+            // The bias is added only when there is one (cpu_backend.cpp:146-154): x + 0.0f would turn a
+            // -0.0 input into +0.0, and the reference stores such a V as it came (the memcpy at :169).
+            for (int d = 0; d < D; d++) q[d] = bias ? src[h * D + d] + bias[h * D + d] : src[h * D + d];
             if (norm) rmsnorm(q, q_norm, D, eps, q);
             rope(q, D, pos, inv_freq);
         }
         for (int h = 0; h < KVH; h++) {
             const int ko = (H + h) * D, vo = (H + KVH + h) * D;
             for (int d = 0; d < D; d++) {
-                k[static_cast<size_t>(d)] = src[ko + d] + (bias ? bias[ko + d] : 0.0f);
-                v[static_cast<size_t>(d)] = src[vo + d] + (bias ? bias[vo + d] : 0.0f);
+                k[static_cast<size_t>(d)] = bias ? src[ko + d] + bias[ko + d] : src[ko + d];
+                v[static_cast<size_t>(d)] = bias ? src[vo + d] + bias[vo + d] : src[vo + d];
             }
             if (norm) rmsnorm(k.data(), k_norm, D, eps, k.data());
             rope(k.data(), D, pos, inv_freq);

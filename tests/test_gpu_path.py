@@ -11,6 +11,7 @@ import torch
 import oracle
 from ember_amd import BlockManager, EmberError
 from ember_amd.paged_kv import PagedKv, StepBatch
+from gpu_oracle import oracle_layer, snapshot
 from helpers import D, PAGE, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -40,13 +41,14 @@ class World:
         self.vo = [np.zeros_like(self.ko[0]) for _ in range(n_layers)]
         self.inv = oracle.inv_freq(THETA, D)
 
-    def step(self, positions, query_start, tables, qkv_layers, check=True):
+    def step(self, positions, query_start, tables, qkv_layers, check=True, oracle_tables=None):
         """One step: plan, then per layer append + attention. qkv_layers: [L][T, W] f32 values (f16-exact
-        when the pools are f16). Returns (gpu outputs, oracle outputs or None when not check) per layer,
-        f32 arrays [T, H, D]."""
+        when the pools are f16). oracle_tables: the oracle's own block tables (default: the GPU's). Returns
+        (gpu outputs, oracle outputs or None when not check) per layer, f32 arrays [T, H, D]."""
         positions = np.asarray(positions, np.int32)
         query_start = np.asarray(query_start, np.int32)
         tables = np.asarray(tables, np.int32)
+        otab = tables if oracle_tables is None else np.asarray(oracle_tables, np.int32)
         S, T = tables.shape[0], positions.size
         ctx = [int(positions[query_start[s + 1] - 1]) + 1 for s in range(S)]
         self.kv.plan(StepBatch(tokens=[0] * T, positions=positions.tolist(), query_start=query_start.tolist(),
@@ -57,13 +59,13 @@ class World:
             qkv_d = torch.from_numpy(qkv).to(self.dev, self.dtype)
             out = torch.full((T, self.H, D), float("nan"), dtype=self.dtype, device=self.dev)
             self.kv.layer(layer, qkv_d, out, q_norm=self.qn_d[layer], k_norm=self.kn_d[layer])
-            q_ref = oracle.append_layer(qkv, positions, query_start, tables, self.ko[layer], self.vo[layer],
+            q_ref = oracle.append_layer(qkv, positions, query_start, otab, self.ko[layer], self.vo[layer],
                                         n_heads=self.H, n_kv=self.KVH, inv_freq_=self.inv, eps=EPS,
                                         q_norm=self.qn[layer], k_norm=self.kn[layer], num_blocks=self.NB + 1,
                                         kv_f16=False)
             want = None
             if check:
-                want = oracle.attention_layer(q_ref, positions, query_start, tables, self.ko[layer], self.vo[layer],
+                want = oracle.attention_layer(q_ref, positions, query_start, otab, self.ko[layer], self.vo[layer],
                                               n_heads=self.H, n_kv=self.KVH, num_blocks=self.NB + 1, kv_f16=False,
                                               threads=8)
             torch.cuda.synchronize()
@@ -104,6 +106,35 @@ def test_config1_prefill_then_decode(rng, device, dtype):
     assert set(np.nonzero(written_g.any(axis=1))[0]) == set(table[0].tolist())
     tolk = 2e-3 if f16 else 1e-5
     assert rel_err(kg[table[0]], w.ko[0][table[0]]) < tolk and rel_err(vg[table[0]], w.vo[0][table[0]]) < tolk
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_uneven_chunks_at_block_offset_3(device, dtype):
+    """The reference's uneven-chunk check (tests/test_model.cpp:124-157) at the attention layer: a 700-token
+    prompt (seeded N(0,1) activations) run in chunks of 300, 37 (ending in the middle of a page) and 363 (64-token
+    tiles and partial tiles), then 8 decode steps. As there, the GPU sequence sits on consecutive blocks from 3
+    (SingleSequence(gpu, 3), tests/model_helpers.hpp:13) and the oracle's from 0: different physical blocks on
+    purpose. Every token of every step within 2e-3 (f16) / 1e-5 (f32); the pages match slot for slot."""
+    f16 = dtype == torch.float16
+    rng = np.random.default_rng(12345)
+    w = World(device, dtype, num_blocks=64, max_position=1024)
+    n_pages = (700 + 8 + PAGE - 1) // PAGE
+    gtab = (3 + np.arange(n_pages, dtype=np.int32))[None, :]
+    otab = np.arange(n_pages, dtype=np.int32)[None, :]
+    length = 0
+    for chunk in (300, 37, 363):
+        (got, want), = w.step(np.arange(length, length + chunk), [0, chunk], gtab, _acts(rng, chunk, 1, f16),
+                              oracle_tables=otab)
+        assert rel_err(got, want) < w.tol, f"chunk ending at {length + chunk}"
+        length += chunk
+    for _ in range(8):
+        (got, want), = w.step([length], [0, 1], gtab, _acts(rng, 1, 1, f16), oracle_tables=otab)
+        assert rel_err(got, want) < w.tol, f"decode at {length}"
+        length += 1
+    kg, vg = w.pools(0)
+    tolk = 2e-3 if f16 else 1e-5
+    assert rel_err(kg[gtab[0]], w.ko[0][otab[0]]) < tolk and rel_err(vg[gtab[0]], w.vo[0][otab[0]]) < tolk
+    assert not np.abs(kg[:3]).any() and not np.abs(kg[3 + n_pages:]).any(), "a block outside the table was written"
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
@@ -300,7 +331,9 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
     """Decode steps run as replayed hipGraphs (padded to a token bucket and a block-table width bucket,
     padding tokens on the spare block) leave the same outputs and pools, to the bit, as plan + layer: the
     same graph replayed step after step with eager work in between, and new graphs when the batch moves
-    to another bucket. Only the spare block differs (the padding writes there and nowhere else)."""
+    to another bucket. Only the spare block differs (the padding writes there and nowhere else). Every
+    replay's outputs are also checked against the oracle (2e-3 f16, 1e-5 f32) on a snapshot of the pages
+    the step reads."""
     L, NB, maxpos = 2, 700, 2048
     mk = lambda: PagedKv(n_layers=L, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,  # noqa: E731
                          max_position=maxpos, num_blocks=NB, max_batch_tokens=64, max_seqs=64, dtype=dtype)
@@ -335,6 +368,8 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
         acts = _acts(rng, n_act, L, dtype == torch.float16)
         for l in range(L):
             qkv[l][:n_act] = torch.from_numpy(acts[l]).to(device, dtype)
+        # the oracle's view of the pages this step reads, before the step (both worlds hold the same pages)
+        snaps = [snapshot(eb, l, tables, (pos + PAGE) // PAGE) for l in range(L)]
         assert ga.decode_graph(batch, io)
         eb.plan(batch)
         for l in range(L):
@@ -342,6 +377,11 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
         torch.cuda.synchronize()
         bits = lambda t: t.cpu().numpy().view(np.uint16 if dtype == torch.float16 else np.uint32)  # noqa: E731
         for l in range(L):
+            want = oracle_layer(snaps[l], acts[l], pos, np.arange(n_act + 1), n_heads=H, n_kv=KVH,
+                                q_norm=qn[l].cpu().numpy(), k_norm=kn[l].cpu().numpy(), inv_freq=oracle.inv_freq(THETA, D),
+                                eps=EPS, threads=8)
+            tol = 2e-3 if dtype == torch.float16 else 1e-5
+            assert rel_err(out_g[l][:n_act].float().cpu().numpy(), want) < tol, f"step {step} layer {l}: graph vs oracle"
             assert np.array_equal(bits(out_g[l][:n_act]), bits(out_e[l][:n_act])), f"step {step} layer {l} output"
             for which in ("k", "v"):
                 a, b = bits(ga.pool_view(l, which)), bits(eb.pool_view(l, which))

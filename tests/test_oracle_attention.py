@@ -56,6 +56,50 @@ def test_append_writes_exactly_the_token_slots(rng, kv_f16):
         assert np.array_equal(row, expect)
 
 
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_append_k_at_position_zero_is_each_heads_unit_rms_vector(rng, kv_f16):
+    """A direct pin of the stored K (and of q): at position 0 the rotation is the identity, so with unit norm
+    weights the oracle stores k = x / sqrt(mean(x^2) + eps) of its own kv head (cpu_backend.cpp:34-39, :163-170).
+    Every head's source gets its own scale, so a wrong head offset fails; computed here in float64."""
+    NB, eps = 4, 1e-6
+    tables = np.array([[2]], np.int32)
+    qkv = rng.standard_normal((1, (H + 2 * KVH) * D)) * np.repeat(np.arange(1, H + 2 * KVH + 1), D)[None, :]
+    qkv = qkv.astype(np.float32)
+    dt = np.uint16 if kv_f16 else np.float32
+    k = np.zeros((NB, KVH, PAGE, D), dt)
+    v = np.zeros_like(k)
+    q = oracle.append_layer(qkv, [0], [0, 1], tables, k, v, n_heads=H, n_kv=KVH, inv_freq_=oracle.inv_freq(1e6, D),
+                            eps=eps, q_norm=np.ones(D, np.float32), k_norm=np.ones(D, np.float32), num_blocks=NB,
+                            kv_f16=kv_f16)
+    heads = qkv[0].astype(np.float64).reshape(H + 2 * KVH, D)
+    unit = heads / np.sqrt((heads ** 2).mean(axis=1, keepdims=True) + eps)
+    got_k = k[2, :, 0].view(np.float16).astype(np.float64) if kv_f16 else k[2, :, 0].astype(np.float64)
+    np.testing.assert_allclose(got_k, unit[H:H + KVH], rtol=1e-3 if kv_f16 else 1e-6, atol=1e-3 if kv_f16 else 1e-7)
+    np.testing.assert_allclose(q[0], unit[:H], rtol=1e-6, atol=1e-7)
+    assert not k[[0, 1, 3]].any() and not k[2, :, 1:].any()  # nothing else written
+
+
+@pytest.mark.parametrize("kv_f16", [False, True])
+def test_append_keeps_the_sign_of_zero_without_a_bias(kv_f16):
+    """Without a bias the reference copies V into the cache as it is (the memcpy at cpu_backend.cpp:169; the bias
+    is added only for qkv_bias models, :146-154), so a -0.0 input stays -0.0; with a bias, -0.0 + 0.0 is +0.0."""
+    NB = 2
+    tables = np.array([[1]], np.int32)
+    qkv = np.zeros((1, (H + 2 * KVH) * D), np.float32)
+    qkv[0, (H + KVH) * D:] = -0.0
+    qkv[0, (H + KVH) * D + 5] = 1.5
+    dt = np.uint16 if kv_f16 else np.float32
+    for bias, neg_zero in ((None, True), (np.zeros((H + 2 * KVH) * D, np.float32), False)):
+        k = np.zeros((NB, KVH, PAGE, D), dt)
+        v = np.zeros_like(k)
+        oracle.append_layer(qkv, [3], [0, 1], tables, k, v, n_heads=H, n_kv=KVH, inv_freq_=oracle.inv_freq(1e6, D),
+                            bias=bias, num_blocks=NB, kv_f16=kv_f16)
+        row = v[1, 0, 3].view(np.uint16 if kv_f16 else np.uint32)
+        sign = 0x8000 if kv_f16 else 0x80000000
+        assert row[5] == (0x3E00 if kv_f16 else np.float32(1.5).view(np.uint32))
+        assert (row[[0, 1, 127]] == (sign if neg_zero else 0)).all()
+
+
 def _filled(rng, step, NB, kv_f16=False, scale=1.0):
     dt = np.float32
     k = np.zeros((NB, KVH, PAGE, D), dt)
