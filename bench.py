@@ -182,17 +182,20 @@ class Workload:
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_config2.json"
 
 
-def measured_traffic(algorithmic_bytes: float):
-    """HBM bytes per decode launch as the rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured them (already scaled
-    by the copy-kernel calibration), read from the summary committed with those passes; None without one."""
+def measured_traffic():
+    """HBM bytes per decode launch as the rocprofv3 FETCH_SIZE / WRITE_SIZE passes measured them (scaled by the
+    copy-kernel calibration), read from the summary committed with those passes, with the algorithmic bytes of
+    the launches those passes covered: (traffic, traffic / algorithmic). (None, None) without a summary. The
+    counters cannot run beside this timing, so the figure is that committed measurement, not this run's."""
     try:
         t = json.loads(TRAFFIC_FILE.read_text())
         total = float(t["fetch_bytes_per_launch"]) + float(t["write_bytes_per_launch"])
-    except (OSError, ValueError, KeyError):
-        return None
-    log(f"[bench] HBM traffic per launch (rocprofv3 PMC, {TRAFFIC_FILE.name}): {total / 1e6:.1f} MB, "
-        f"{total / algorithmic_bytes:.3f} x this run's algorithmic bytes")
-    return round(total)
+        ratio = total / float(t["algorithmic_bytes_per_launch"])
+    except (OSError, ValueError, KeyError, ZeroDivisionError):
+        return None, None
+    log(f"[bench] HBM traffic per launch (committed rocprofv3 PMC passes, {TRAFFIC_FILE.name}): {total / 1e6:.1f} MB, "
+        f"{ratio:.3f} x the algorithmic bytes of the launches it measured")
+    return round(total), round(ratio, 4)
 
 
 def copy_calibration(steps: int) -> int:
@@ -224,7 +227,11 @@ def cpu_baseline(seconds: float) -> dict:
     host's CPU share. Reported as tokens/s for 28 layers (per-layer time x 28)."""
     import oracle
 
-    threads = min(16, os.cpu_count() or 1)
+    # hardware_concurrency() on a one-GPU box shows the whole host, but this job's CPU share is 16 threads
+    # (OMP_NUM_THREADS says the same there): the baseline uses the share and names the host's count beside it.
+    host_cpus = os.cpu_count() or 1
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else host_cpus
+    threads = min(16, affinity)
     if os.environ.get("OMP_NUM_THREADS", "").isdigit():
         threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
     rng = np.random.default_rng(SEED)
@@ -274,13 +281,14 @@ def cpu_baseline(seconds: float) -> dict:
         "kind": "port",
         "sample": (f"1 of {N_LAYERS} layers of the same 32-sequence batch (sum of contexts {int(ctx_after.sum())}), "
                    f"f32 KV, median of {len(times)} steps ({per_layer * 1e3:.1f} ms/layer) x {N_LAYERS} layers; "
-                   f"{cpu_model or platform.processor()}"),
+                   f"{threads} threads = this job's CPU share (host: {host_cpus} CPUs, {affinity} in this process's "
+                   f"affinity); {cpu_model or platform.processor()}"),
     }
 
 
 # ---- BASELINE configs 3, 4 and 5 (reported beside the metric; `--config N`) ----
 
-class Path:
+class PathBench:
     """The GPU path plus the engine-side bookkeeping a config needs: a BlockManager over the pool, block
     tables kept as one array, pools filled with random f16 K/V, per-layer q/k/v activations."""
 
@@ -396,7 +404,7 @@ def run_config5(args) -> dict:
     max_ctx = int(ctx.max()) + Q * total + PAGE
     mb = (max_ctx + PAGE - 1) // PAGE
     pages = int(((ctx + Q * total) // PAGE + 2).sum())
-    path = Path(pool_pages=pages, max_seqs=B5, max_blocks=mb, max_tokens=B5 * Q, split_len=args.split_len, seed=SEED + 5)
+    path = PathBench(pool_pages=pages, max_seqs=B5, max_blocks=mb, max_tokens=B5 * Q, split_len=args.split_len, seed=SEED + 5)
     acc_rng = np.random.default_rng(SEED + 55)
     qs = np.arange(B5 + 1, dtype=np.int32) * Q
 
@@ -544,7 +552,7 @@ def run_config3(args) -> dict:
     max_ctx = PREFIX + max(CHUNK * NCHUNK, int(own.max()) + total) + PAGE
     mb = (max_ctx + PAGE - 1) // PAGE
     pages = PREFIX // PAGE + int((own + total).sum()) // PAGE + 2 * NSEQ + (NPRE + 2) * CHUNK * NCHUNK // PAGE + 64
-    path = Path(pool_pages=pages, max_seqs=NSEQ, max_blocks=mb, max_tokens=NPRE * CHUNK + NSEQ, split_len=args.split_len,
+    path = PathBench(pool_pages=pages, max_seqs=NSEQ, max_blocks=mb, max_tokens=NPRE * CHUNK + NSEQ, split_len=args.split_len,
                 prefix_caching=True, seed=SEED + 3)
     bm = path.bm
     prefix = rng.integers(0, 150000, PREFIX).astype(np.int32)
@@ -650,13 +658,13 @@ def run_config4(args) -> dict:
     """large-pool decode sized for 288 GB of HBM. A 2,097,152-token pool (131,072
     pages, 112 KiB of f16 K/V per token over 28 layers: 224 GiB) and 256 sequences with contexts
     log-uniform in [512, 16384]. Each step decodes one token for every running sequence, preempts the
-    newest 8 (their pages go back to the pool) and resumes the 8 preempted the step before: their pages
-    are allocated again and their K/V restored by re-appending every context token through the append
-    kernel (the re-prefill's cache writes; the rest of the model's recompute is outside this path). The
-    decode step and the re-append are timed together; GB/s counts the decode's K/V once per sequence."""
+    newest 8 (their pages go back to the pool) and resumes the 8 preempted the step before, as the
+    reference's engine does (engine.cpp:195-205, :302-335): their pages are allocated again and their whole
+    contexts re-prefilled in the same step through the plan, which routes each resumed context (>= 16 new
+    tokens) to the MFMA prefill tiles (cuda_backend.cu:174-179) while the running sequences decode. GB/s counts
+    the decode's K/V once per sequence plus the re-prefill's K/V once per resumed sequence and every new
+    token's bytes."""
     import torch
-
-    from ember_amd import _lib
 
     POOL, NSEQ, PRE = 131072, 256, 8
     free = torch.cuda.mem_get_info()[0]
@@ -668,62 +676,30 @@ def run_config4(args) -> dict:
     total = args.warmup + 2 * args.steps
     mb = (int(ctx.max()) + total + 2 * PAGE) // PAGE
     resume_rows = PRE * (int(ctx.max()) + total)
-    path = Path(pool_pages=POOL, max_seqs=NSEQ, max_blocks=mb, max_tokens=NSEQ, split_len=args.split_len,
-                seed=SEED + 4, qkv_tokens=max(NSEQ, resume_rows), shared_qkv=True)
+    path = PathBench(pool_pages=POOL, max_seqs=NSEQ, max_blocks=mb, max_tokens=NSEQ + resume_rows,
+                     split_len=args.split_len, seed=SEED + 4, shared_qkv=True)
     for s in range(NSEQ):
         path.ensure(s, int(ctx[s]))
     order = list(range(NSEQ))  # admission order: the newest are preempted
     paused = []
-    dev = torch.device("cuda")
-    q_out = torch.empty((resume_rows, H, D), device=dev, dtype=torch.float16)
-    inv = torch.tensor([1.0 / (1e6 ** (2 * i / D)) for i in range(D // 2)], dtype=torch.float32, device=dev)
-    # The re-append's integers go up from pinned staging with asynchronous copies, double-buffered: a
-    # synchronous copy would make the host wait for the previous step's kernels and leave the GPU idle
-    # while the host prepares the next step (an engine uploads asynchronously too).
-    n_tab = path.tables.size
-    stage = [torch.empty(2 * resume_rows + n_tab, dtype=torch.int32, pin_memory=True) for _ in range(2)]
-    dev_ints = [torch.empty(2 * resume_rows + n_tab, dtype=torch.int32, device=dev) for _ in range(2)]
-    uploaded = [torch.cuda.Event() for _ in range(2)]
-    n_uploads = [0]
-
-    def reappend(seqs):
-        """The resumed sequences' K/V written again, every context token, through the append kernel."""
-        i = n_uploads[0] % 2
-        n_uploads[0] += 1
-        uploaded[i].synchronize()  # the copy out of this staging buffer two uploads ago has run
-        pos = np.concatenate([np.arange(0, ctx[s]) for s in seqs]).astype(np.int32)
-        tsq = np.concatenate([np.full(ctx[s], s) for s in seqs]).astype(np.int32)
-        n = pos.size
-        host = stage[i].numpy()
-        host[:n], host[resume_rows:resume_rows + n] = pos, tsq
-        host[2 * resume_rows:] = path.tables.reshape(-1)
-        with torch.cuda.stream(path.stream):
-            dev_ints[i].copy_(stage[i], non_blocking=True)
-            uploaded[i].record(path.stream)
-        pos_d, tsq_d = dev_ints[i][:n], dev_ints[i][resume_rows:resume_rows + n]
-        tables_dev = dev_ints[i][2 * resume_rows:]
-        a = _lib.QkvArgs()
-        a.q_out, a.inv_freq = q_out.data_ptr(), inv.data_ptr()
-        a.positions, a.token_seq, a.block_tables = pos_d.data_ptr(), tsq_d.data_ptr(), tables_dev.data_ptr()
-        a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = path.tables.shape[1], int(pos.size), H, KVH, D
-        a.eps, a.num_blocks, a.dtype = 1e-6, POOL + 1, _lib.DTYPE_F16
-        for layer in range(N_LAYERS):
-            a.qkv = path.qkv[layer].data_ptr()
-            a.k_cache, a.v_cache = path.kv.pool_view(layer, "k").data_ptr(), path.kv.pool_view(layer, "v").data_ptr()
-            a.q_norm, a.k_norm = path.qn[layer].data_ptr(), path.kn[layer].data_ptr()
-            _lib.check(_lib.lib().ember_hip_kv_append(a, path.stream.cuda_stream), "kv_append")
+    prefill_flops, resumed_tokens = [], []
 
     def step():
         nonlocal paused
         running = [s for s in order if s not in paused]
-        for s in paused:
+        for s in paused:  # resume: fresh pages for the whole context, recomputed below
             path.ensure(s, int(ctx[s]))
-        if paused:
-            reappend(paused)
         for s in running:
             path.ensure(s, int(ctx[s]) + 1)
-        path.run(running, ctx[running], np.arange(len(running) + 1))
-        kv_bytes = KV_BYTES_PER_TOKEN * int((ctx[running] + 1).sum())
+        seqs = running + paused
+        pos = [np.array([ctx[s]]) for s in running] + [np.arange(0, ctx[s]) for s in paused]
+        qs = np.concatenate([[0], np.cumsum([p.size for p in pos])])
+        path.run(seqs, np.concatenate(pos), qs)
+        # per layer: QK and PV over keys 0..pos of every head, 2 flops per multiply-add
+        prefill_flops.append(sum(4 * D * H * int(ctx[s]) * (int(ctx[s]) + 1) // 2 for s in paused))
+        resumed_tokens.append(int(sum(int(ctx[s]) for s in paused)))
+        kv_bytes = KV_BYTES_PER_TOKEN * (int((ctx[running] + 1).sum()) + resumed_tokens[-1])
+        new_tokens = len(running) + resumed_tokens[-1]
         ctx[running] += 1
         # the resumed rejoin at the back; the newest 8 running are preempted and their pages freed
         newest = running[-PRE:]
@@ -731,19 +707,31 @@ def run_config4(args) -> dict:
             path.release(s)
         order[:] = [s for s in order if s not in newest] + newest
         paused = newest
-        return N_LAYERS * (kv_bytes + FUSED_TOKEN_BYTES * len(running))
+        return N_LAYERS * (kv_bytes + TOKEN_BYTES * new_tokens)
 
     step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
     gbs = step_bytes / step_s / 1e9
+    p_launches, p_ms = path.prefill_timed
+    p_us = p_ms / max(p_launches, 1) * 1e3
+    p_tflops = float(np.mean(prefill_flops[-args.steps:])) / (p_us * 1e-6) / 1e12 if p_launches else None
+    d_us = kernel_ms / max(launches, 1) * 1e3
     return {
         "metric": "large-pool decode tokens/s, % HBM peak and page-allocator overhead (2M-token pool, 256 sequences)",
         "value": round((NSEQ - PRE) / step_s, 1), "unit": "decode tokens/s", "ms_per_step": round(step_s * 1e3, 4),
         "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "decode_kernel_avg_us": round(d_us, 2),
+        "prefill_kernel_avg_us": round(p_us, 2),
+        "resumed_tokens_per_step": round(float(np.mean(resumed_tokens[-args.steps:])), 1),
+        "prefill_share_of_step": round(N_LAYERS * p_us * 1e-6 / step_s, 4),
+        "decode_share_of_step": round(N_LAYERS * d_us * 1e-6 / step_s, 4),
+        "prefill_mfma": None if p_tflops is None else {
+            "achieved": round(p_tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(p_tflops / MFMA_F16_PEAK_TFLOPS, 4)},
         "host_blockmanager_us_per_step": round(alloc_us, 2),
         "config": {"workload": "BASELINE configs[3]: 2,097,152-token f16 pool (224 GiB over 28 layers), 256 sequences "
-                               "with context logU[512,16384], each step preempting the newest 8 and re-appending the "
-                               "8 preempted the step before", "split_len": args.split_len},
+                               "with context logU[512,16384], each step preempting the newest 8 and re-prefilling the "
+                               "8 preempted the step before (whole contexts through the plan: MFMA prefill tiles) "
+                               "beside the running 248's decode", "split_len": args.split_len},
     }
 
 
@@ -844,7 +832,7 @@ def main() -> int:
     log(f"[bench] instrumented pass {wall_inst * 1e3 / args.steps:.3f} ms/step; paged_decode_kernel: {launches} "
         f"launches, avg {avg_us:.1f} us, {kernel_gbs:.0f} GB/s ({kernel_gbs / HBM_PEAK_GBS:.1%}); "
         f"host BlockManager {alloc_us:.1f} us/step")
-    traffic = measured_traffic(kernel_bytes / max(launches, 1))
+    traffic, traffic_ratio = measured_traffic()
 
     cpu = None
     if args.cpu_seconds > 0:
@@ -886,6 +874,9 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_ratio": traffic_ratio,
+            "traffic_source": f"profiles/{TRAFFIC_FILE.name} (rocprofv3 FETCH_SIZE / WRITE_SIZE passes, copy-kernel "
+                              "calibrated; committed, not measured in this run)" if traffic else None,
             "avg_launch_us": round(avg_us, 2),
             "timed_launches": launches,
             "bytes_per_launch": round(kernel_bytes / max(launches, 1)),

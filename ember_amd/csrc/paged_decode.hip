@@ -282,6 +282,21 @@ __device__ __forceinline__ void merge_lanes(float &m, float &l, float (&acc)[8],
 // across the XCDs' L2s by themselves, so the in-kernel merge needs no
 // cache-wide write-back or invalidate (an agent-scope fence is buffer_wbl2 of
 // the whole L2 per work-group, which serializes).
+//
+// Why the merge reads complete partials although every access is relaxed:
+// the compiler lowers an agent-scope release as "buffer_wbl2 sc1; s_waitcnt
+// vmcnt(0)" before the releasing store, and an acquire as "s_waitcnt
+// vmcnt(0); buffer_inv sc1" after the acquiring load (LLVM AMDGPU memory
+// model, GFX942 family, which gfx950 follows). The wbl2 / inv halves only
+// write back or drop cached lines of non-atomic accesses; the partials are
+// atomic sc1 accesses that bypass the non-coherent caches, so what ordering
+// needs is the waits. They are here by hand: each work-group waits for its
+// partial stores (s_waitcnt vmcnt(0), then a barrier) before its counter
+// increment, and the merging work-group issues its partial loads only after
+// the increment has returned (a barrier behind the returned value's branch).
+// So every partial counted before the last increment is visible to the
+// merge. The order is the hardware's, not the HIP source's: a port to another
+// target must use release / acquire orderings instead.
 __device__ __forceinline__ void put_partial(float *p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
