@@ -29,6 +29,10 @@ SOURCES = [
     CSRC / "linear.hip",
     CSRC / "static_scratch.hip",
     CSRC / "host" / "kvcache" / "block_manager.cpp",
+    CSRC / "host" / "common" / "json.cpp",
+    CSRC / "host" / "common" / "mmap_file.cpp",
+    CSRC / "host" / "model" / "config.cpp",
+    CSRC / "host" / "model" / "safetensors.cpp",
     CSRC / "host" / "backend" / "hip_paged_kv.cpp",
     CSRC / "host" / "capi_host.cpp",
 ]
