@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 3
+ABI_VERSION = 4
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
@@ -108,7 +108,39 @@ class NormArgs(ctypes.Structure):
     ]
 
 
-STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, LayerIo, GemvArgs, NormArgs]
+class EmbedArgs(ctypes.Structure):
+    _fields_ = [("tokens", c_void_p), ("T", c_int32), ("table", c_void_p), ("vocab", c_int32), ("hidden", c_int32),
+                ("out", c_void_p)]
+
+
+class SampleParams(ctypes.Structure):
+    _fields_ = [("temperature", c_float), ("top_p", c_float), ("min_p", c_float), ("top_k", c_int32),
+                ("seed", c_uint64), ("counter", c_uint64)]
+
+
+class SampleArgs(ctypes.Structure):
+    _fields_ = [("logits", c_void_p), ("R", c_int32), ("vocab", c_int32), ("params", c_void_p), ("out", c_void_p)]
+
+
+class ProbArgs(ctypes.Structure):
+    _fields_ = [("logits", c_void_p), ("vocab", c_int32), ("params", c_void_p), ("rows", c_void_p),
+                ("tokens", c_void_p), ("n", c_int32), ("out", c_void_p), ("R", c_int32)]
+
+
+class BackendOptions(ctypes.Structure):
+    _fields_ = [("max_batch_tokens", c_int32), ("max_seqs", c_int32), ("max_logit_rows", c_int32),
+                ("kv_cache_bytes", c_int64), ("kv_cache_tokens", c_int32), ("memory_fraction", c_double),
+                ("gpu", c_int32)]
+
+
+class ModelInfo(ctypes.Structure):
+    _fields_ = [("vocab_size", c_int32), ("hidden", c_int32), ("intermediate", c_int32), ("n_layers", c_int32),
+                ("n_heads", c_int32), ("n_kv_heads", c_int32), ("head_dim", c_int32), ("num_kv_blocks", c_int32),
+                ("max_logit_rows", c_int32)]
+
+
+STRUCTS = [QkvArgs, AttnArgs, PrefillArgs, CopyArgs, KvConfig, StepBatchC, LayerIo, GemvArgs, NormArgs, EmbedArgs,
+           SampleParams, SampleArgs, ProbArgs, BackendOptions, ModelInfo]
 
 # name -> (restype, argtypes); every extern "C" symbol of include/ember_hip.h.
 PROTOTYPES = {
@@ -120,6 +152,9 @@ PROTOTYPES = {
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
     "ember_hip_gemv": (c_int32, [POINTER(GemvArgs), c_void_p]),
     "ember_hip_rmsnorm_rows": (c_int32, [POINTER(NormArgs), c_void_p]),
+    "ember_hip_embed": (c_int32, [POINTER(EmbedArgs), c_void_p]),
+    "ember_hip_sample": (c_int32, [POINTER(SampleArgs), c_void_p]),
+    "ember_hip_token_probs": (c_int32, [POINTER(ProbArgs), c_void_p]),
     "ember_hip_last_error": (c_char_p, []),
     "ember_hip_abi_version": (c_int32, []),
     "ember_hip_sizeof": (c_int32, [c_int32]),
@@ -157,6 +192,16 @@ PROTOTYPES = {
     "ember_kv_set_timing": (c_int32, [c_void_p, c_int32]),
     "ember_kv_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
     "ember_kv_prefill_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
+    "ember_backend_create": (c_void_p, [c_char_p, POINTER(BackendOptions)]),
+    "ember_backend_destroy": (None, [c_void_p]),
+    "ember_backend_info": (c_int32, [c_void_p, POINTER(ModelInfo)]),
+    "ember_backend_forward": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(c_int32), c_int32]),
+    "ember_backend_sample": (c_int32, [c_void_p, POINTER(SampleParams), c_int32, POINTER(c_int32)]),
+    "ember_backend_token_probs": (c_int32, [c_void_p, POINTER(SampleParams), c_int32, POINTER(c_int32),
+                                            POINTER(c_int32), c_int32, POINTER(c_float)]),
+    "ember_backend_logits": (c_int32, [c_void_p, c_int32, POINTER(c_float), c_int32]),
+    "ember_backend_set_capture_hidden": (c_int32, [c_void_p, c_int32]),
+    "ember_backend_captured_hidden": (c_int32, [c_void_p, POINTER(c_float), c_int32]),
 }
 
 _lib = None

@@ -28,12 +28,15 @@ SOURCES = [
     CSRC / "copy_pages.hip",
     CSRC / "linear.hip",
     CSRC / "static_scratch.hip",
+    CSRC / "sampling.hip",
     CSRC / "host" / "kvcache" / "block_manager.cpp",
     CSRC / "host" / "common" / "json.cpp",
     CSRC / "host" / "common" / "mmap_file.cpp",
     CSRC / "host" / "model" / "config.cpp",
     CSRC / "host" / "model" / "safetensors.cpp",
     CSRC / "host" / "backend" / "hip_paged_kv.cpp",
+    CSRC / "host" / "backend" / "hip_backend.cpp",
+    CSRC / "host" / "backend" / "backend.cpp",
     CSRC / "host" / "capi_host.cpp",
 ]
 

@@ -65,6 +65,12 @@ int32_t ember_hip_sizeof(int32_t which) {
         case 6: return sizeof(EmberLayerIo);
         case 7: return sizeof(EmberGemvArgs);
         case 8: return sizeof(EmberNormArgs);
+        case 9: return sizeof(EmberEmbedArgs);
+        case 10: return sizeof(EmberSampleParams);
+        case 11: return sizeof(EmberSampleArgs);
+        case 12: return sizeof(EmberProbArgs);
+        case 13: return sizeof(EmberBackendOptions);
+        case 14: return sizeof(EmberModelInfo);
         default: return -1;
     }
 }
@@ -218,6 +224,41 @@ int ember_hip_gemv(const EmberGemvArgs *a, void *stream) {
     if (reinterpret_cast<uintptr_t>(a->A) % 16 != 0 || reinterpret_cast<uintptr_t>(a->W) % 16 != 0)
         return set_error(EMBER_ERR_INVALID, "gemv: A and W must be 16-byte aligned");
     return hip_status(launch_gemv(*a, static_cast<hipStream_t>(stream)), "gemv");
+}
+
+int ember_hip_embed(const EmberEmbedArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "embed: null arguments");
+    if (a->T < 0 || a->vocab < 1 || a->hidden < 8 || a->hidden % 8 != 0)
+        return set_error(EMBER_ERR_INVALID, "embed: bad sizes (T %d, vocab %d, hidden %d: a multiple of 8)", a->T,
+                         a->vocab, a->hidden);
+    if (a->T == 0) return EMBER_OK;
+    if (!a->tokens || !a->table || !a->out) return set_error(EMBER_ERR_INVALID, "embed: a required pointer is null");
+    if (reinterpret_cast<uintptr_t>(a->table) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "embed: the table must be 16-byte aligned");
+    return hip_status(launch_embed(*a, static_cast<hipStream_t>(stream)), "embed");
+}
+
+int ember_hip_sample(const EmberSampleArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "sample: null arguments");
+    if (a->R < 0 || a->vocab < 1 || a->vocab > (1 << 24))
+        return set_error(EMBER_ERR_INVALID, "sample: bad sizes (R %d, vocab %d: 1..2^24)", a->R, a->vocab);
+    if (a->R == 0) return EMBER_OK;
+    if (!a->logits || !a->params || !a->out) return set_error(EMBER_ERR_INVALID, "sample: a required pointer is null");
+    return hip_status(launch_sample(*a, static_cast<hipStream_t>(stream)), "sample");
+}
+
+int ember_hip_token_probs(const EmberProbArgs *a, void *stream) {
+    g_last_error.clear();
+    if (!a) return set_error(EMBER_ERR_INVALID, "token_probs: null arguments");
+    if (a->n < 0 || a->R < 0 || a->vocab < 1 || a->vocab > (1 << 24))
+        return set_error(EMBER_ERR_INVALID, "token_probs: bad sizes (n %d, R %d, vocab %d: 1..2^24)", a->n, a->R,
+                         a->vocab);
+    if (a->n == 0) return EMBER_OK;
+    if (!a->logits || !a->params || !a->rows || !a->tokens || !a->out)
+        return set_error(EMBER_ERR_INVALID, "token_probs: a required pointer is null");
+    return hip_status(launch_token_probs(*a, static_cast<hipStream_t>(stream)), "token_probs");
 }
 
 int ember_hip_rmsnorm_rows(const EmberNormArgs *a, void *stream) {

@@ -85,7 +85,7 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     // descriptors (kDescInts each, 128-byte aligned like every array here). Work items exist for decode
     // runs only, at most one per (decode token, split).
     const size_t items = static_cast<size_t>(decode_cap_) * max_splits_;
-    ints_capacity_ = 4 * pad32(T) + 2 * pad32(T) + 3 * pad32(T / 16 + static_cast<size_t>(opt_.max_seqs)) +
+    ints_capacity_ = 4 * pad32(T) + 4 * pad32(T) + 3 * pad32(T / 16 + static_cast<size_t>(opt_.max_seqs)) +
                      static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * items) +
                      pad32(static_cast<size_t>(kDescInts) * items) + 64;
     for (int i = 0; i < 2; i++) {
@@ -300,6 +300,11 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     put(tile_seq_.data(), tile_seq_.size());
     put(work_.data(), work_.size());
     put(work_desc_.data(), work_desc_.size());
+    // The step's token ids and logit rows ride along for a backend's embedding and final norm.
+    put(b.tokens.size() == static_cast<size_t>(T) ? b.tokens.data() : nullptr,
+        b.tokens.size() == static_cast<size_t>(T) ? static_cast<size_t>(T) : 0);
+    EMBER_CHECK(b.logit_rows.size() <= static_cast<size_t>(T), "{} logit rows for {} tokens", b.logit_rows.size(), T);
+    put(b.logit_rows.data(), b.logit_rows.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
     // The copy waits for the kernels that last read this buffer (two plans ago),
     // then runs beside stream_'s work. The host, not stream_, waits for it:
@@ -320,6 +325,8 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     d_tile_seq_ = dp + at[8];
     d_work_ = dp + at[9];
     d_work_desc_ = dp + at[10];
+    d_tokens_ = b.tokens.size() == static_cast<size_t>(T) ? dp + at[11] : nullptr;
+    d_logit_rows_ = dp + at[12];
 }
 
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {

@@ -84,6 +84,11 @@ public:
     int prefill_tiles() const { return tiles_; }
     int num_splits() const { return splits_; }
     hipStream_t stream() const { return stream_; }
+    // The planned step's token ids (null when the batch carried none) and
+    // logit rows on the device, uploaded with the rest of the plan.
+    const int32_t *d_tokens() const { return d_tokens_; }
+    const int32_t *d_logit_rows() const { return d_logit_rows_; }
+    const int32_t *d_positions() const { return d_positions_; }
 
     // Benchmark timing of the paged-decode and prefill kernels (events around each launch).
     void set_timing(bool on) { timing_ = on; }
@@ -144,6 +149,7 @@ private:
     std::vector<int32_t> token_seq_, decode_, run_first_, run_count_, run_ctx_, tile_start_, tile_end_, tile_seq_, work_,
         work_desc_;
     int num_work_ = 0;
+    const int32_t *d_tokens_ = nullptr, *d_logit_rows_ = nullptr;
 
     bool timing_ = false;
     struct Timing {  // start/stop pairs, reused after collection

@@ -4,9 +4,12 @@
 #include <algorithm>
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <new>
 #include <span>
+#include <vector>
 
+#include "backend/backend.hpp"
 #include "backend/hip_paged_kv.hpp"
 #include "capi_errors.hpp"
 #include "common/error.hpp"
@@ -21,6 +24,10 @@ struct EmberBlockManager {
 struct EmberPagedKv {
     ember::HipPagedKv kv;
     EmberPagedKv(const ember::ModelConfig &c, const ember::PagedKvOptions &o, hipStream_t s) : kv(c, o, s) {}
+};
+
+struct EmberBackend {
+    std::unique_ptr<ember::Backend> be;
 };
 
 using ember::hip::set_error;
@@ -266,6 +273,111 @@ int32_t ember_kv_prefill_timing(EmberPagedKv *h, int32_t *launches, double *tota
         const int n = h->kv.collect_prefill_timing(total_ms);
         if (launches) *launches = n;
         return EMBER_OK;
+    });
+}
+
+// ---- the backend ----
+
+EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOptions *o) {
+    try {
+        EMBER_CHECK(model_dir && o, "backend_create: null arguments");
+        ember::BackendOptions opt;
+        opt.device = "hip";
+        opt.max_batch_tokens = o->max_batch_tokens;
+        opt.max_seqs = o->max_seqs;
+        opt.max_logit_rows = o->max_logit_rows;
+        opt.kv_cache_bytes = o->kv_cache_bytes;
+        opt.kv_cache_tokens = o->kv_cache_tokens;
+        if (o->memory_fraction > 0.0) opt.memory_fraction = o->memory_fraction;
+        opt.gpu = o->gpu;
+        return new EmberBackend{ember::create_backend(model_dir, opt)};
+    } catch (const std::exception &e) {
+        set_error(EMBER_ERR_INVALID, "backend_create: %s", e.what());
+        return nullptr;
+    }
+}
+
+void ember_backend_destroy(EmberBackend *h) { delete h; }
+
+int32_t ember_backend_info(const EmberBackend *h, EmberModelInfo *out) {
+    return guarded("backend_info", [&] {
+        EMBER_CHECK(h && out, "null arguments");
+        const ember::ModelConfig &c = h->be->config();
+        *out = EmberModelInfo{c.vocab_size, c.hidden, c.intermediate, c.n_layers, c.n_heads, c.n_kv_heads,
+                              c.head_dim, h->be->num_kv_blocks(), h->be->options().max_logit_rows};
+        return EMBER_OK;
+    });
+}
+
+int32_t ember_backend_forward(EmberBackend *h, const EmberStepBatch *b, const int32_t *logit_rows, int32_t n_rows) {
+    return guarded("backend_forward", [&] {
+        EMBER_CHECK(h && n_rows >= 0 && (n_rows == 0 || logit_rows), "null arguments");
+        ember::StepBatch sb = step_batch(b);
+        sb.logit_rows.assign(logit_rows, logit_rows + n_rows);
+        h->be->forward(sb);
+        return EMBER_OK;
+    });
+}
+
+static std::vector<ember::SampleRequest> sample_requests(const EmberSampleParams *p, int32_t n) {
+    EMBER_CHECK(n >= 0 && (n == 0 || p), "null sampling parameters");
+    std::vector<ember::SampleRequest> reqs(static_cast<size_t>(n));
+    for (int32_t i = 0; i < n; i++) {
+        ember::SamplingParams &s = reqs[static_cast<size_t>(i)].params;
+        s.temperature = p[i].temperature;
+        s.top_p = p[i].top_p;
+        s.min_p = p[i].min_p;
+        s.top_k = p[i].top_k;
+        s.seed = p[i].seed;
+        reqs[static_cast<size_t>(i)].counter = p[i].counter;
+    }
+    return reqs;
+}
+
+int32_t ember_backend_sample(EmberBackend *h, const EmberSampleParams *params, int32_t n, int32_t *out) {
+    return guarded("backend_sample", [&] {
+        EMBER_CHECK(h && (n == 0 || out), "null arguments");
+        const auto reqs = sample_requests(params, n);
+        h->be->sample(reqs, std::span<int32_t>(out, static_cast<size_t>(n)));
+        return EMBER_OK;
+    });
+}
+
+int32_t ember_backend_token_probs(EmberBackend *h, const EmberSampleParams *params, int32_t n_params,
+                                  const int32_t *rows, const int32_t *tokens, int32_t n, float *out) {
+    return guarded("backend_token_probs", [&] {
+        EMBER_CHECK(h && n >= 0 && (n == 0 || (rows && tokens && out)), "null arguments");
+        const auto reqs = sample_requests(params, n_params);
+        const size_t m = static_cast<size_t>(n);
+        h->be->token_probs(reqs, std::span<const int32_t>(rows, m), std::span<const int32_t>(tokens, m),
+                           std::span<float>(out, m));
+        return EMBER_OK;
+    });
+}
+
+int32_t ember_backend_logits(EmberBackend *h, int32_t row, float *out, int32_t n) {
+    return guarded("backend_logits", [&] {
+        EMBER_CHECK(h && out && n > 0, "null arguments");
+        h->be->logits(row, std::span<float>(out, static_cast<size_t>(n)));
+        return EMBER_OK;
+    });
+}
+
+int32_t ember_backend_set_capture_hidden(EmberBackend *h, int32_t on) {
+    return guarded("backend_set_capture_hidden", [&] {
+        EMBER_CHECK(h, "null backend");
+        h->be->set_capture_hidden(on != 0);
+        return EMBER_OK;
+    });
+}
+
+int32_t ember_backend_captured_hidden(EmberBackend *h, float *out, int32_t n) {
+    return guarded("backend_captured_hidden", [&] {
+        EMBER_CHECK(h && out, "null arguments");
+        const std::vector<float> v = h->be->captured_hidden();
+        EMBER_CHECK(static_cast<size_t>(n) >= v.size(), "captured_hidden: {} floats needed", v.size());
+        std::copy(v.begin(), v.end(), out);
+        return static_cast<int32_t>(v.size());
     });
 }
 

@@ -42,6 +42,10 @@ hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream);
 
 hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream);
 
+hipError_t launch_embed(const EmberEmbedArgs &a, hipStream_t stream);
+hipError_t launch_sample(const EmberSampleArgs &a, hipStream_t stream);
+hipError_t launch_token_probs(const EmberProbArgs &a, hipStream_t stream);
+
 // Row capacities with a built decode kernel, ascending.
 constexpr int kDecodeRowInstances[] = {1, 2, 4, 8, 10, 16};
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 3
+#define EMBER_ABI_VERSION 4
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
@@ -255,13 +255,70 @@ typedef struct EmberNormArgs {
  * k_elementwise.cu:52-65). */
 int ember_hip_rmsnorm_rows(const EmberNormArgs *args, void *stream);
 
+/* The arguments of cuda::embed_tokens (kernels.cuh:68). */
+typedef struct EmberEmbedArgs {
+    const int32_t *tokens;        /* [T] device */
+    int32_t T;
+    const void *table;            /* f16 [vocab, hidden], rows 16-byte aligned */
+    int32_t vocab, hidden;        /* hidden a multiple of 8 */
+    float *out;                   /* f32 [T, hidden] */
+} EmberEmbedArgs;
+
+/* out[t] = table[tokens[t]] as f32 (the residual stream's start); a token id
+ * outside the table embeds as zeros. Replaces cuda::embed_tokens
+ * (kernels.cuh:68; k_elementwise.cu). */
+int ember_hip_embed(const EmberEmbedArgs *args, void *stream);
+
+/* cuda::DeviceSampleParams (kernels.cuh:124-128), one per row of logits. */
+typedef struct EmberSampleParams {
+    float temperature, top_p, min_p;   /* temperature <= 1e-5: greedy */
+    int32_t top_k;                     /* 0: no limit */
+    uint64_t seed, counter;            /* the Gumbel noise's inputs */
+} EmberSampleParams;
+
+/* The arguments of cuda::sample_tokens (kernels.cuh:130). */
+typedef struct EmberSampleArgs {
+    const float *logits;          /* [R, vocab] device */
+    int32_t R, vocab;
+    const EmberSampleParams *params; /* [R] device */
+    int32_t *out;                 /* [R] device */
+} EmberSampleArgs;
+
+/* One token per row: greedy rows take the first largest logit; the others
+ * keep v = logit / temperature within top-k, then top-p of the top-k set's
+ * mass, then min-p relative to the most likely token (the host sampler's
+ * sampling_distribution, src/backend/sampling_host.cpp:20-66), and take the
+ * argmax of v + Gumbel(seed, counter, token id) over the kept set
+ * (sampling_rng.hpp:20-33). Replaces cuda::sample_tokens (kernels.cuh:130;
+ * k_sampling.cu:149-170). */
+int ember_hip_sample(const EmberSampleArgs *args, void *stream);
+
+/* The arguments of cuda::token_probabilities (kernels.cuh:132-133). */
+typedef struct EmberProbArgs {
+    const float *logits;          /* [R, vocab] device */
+    int32_t vocab;
+    const EmberSampleParams *params; /* [R] per logit row, device */
+    const int32_t *rows, *tokens; /* [n] device */
+    int32_t n;
+    float *out;                   /* [n] device */
+    /* addition */
+    int32_t R;                    /* rows of logits; a query naming another row, or a token outside the
+                                   * vocabulary, gets probability 0 */
+} EmberProbArgs;
+
+/* out[i] = the probability of tokens[i] in row rows[i]'s sampling
+ * distribution (1 or 0 for greedy rows). Replaces cuda::token_probabilities
+ * (kernels.cuh:132-133; k_sampling.cu:172-186). */
+int ember_hip_token_probs(const EmberProbArgs *args, void *stream);
+
 /* Description of the last failure on this thread ("" if none). */
 const char *ember_hip_last_error(void);
 int ember_hip_abi_version(void);
 /* sizeof of each argument struct, for FFI bindings to check their layouts:
  * 0 EmberQkvArgs, 1 EmberAttnArgs, 2 EmberPrefillArgs, 3 EmberCopyArgs,
  * 4 EmberKvConfig, 5 EmberStepBatch, 6 EmberLayerIo, 7 EmberGemvArgs,
- * 8 EmberNormArgs; -1 otherwise. */
+ * 8 EmberNormArgs, 9 EmberEmbedArgs, 10 EmberSampleParams, 11 EmberSampleArgs,
+ * 12 EmberProbArgs, 13 EmberBackendOptions, 14 EmberModelInfo; -1 otherwise. */
 int32_t ember_hip_sizeof(int32_t which);
 
 /* ---- 2. KV block manager ------------------------------------------------- */
@@ -390,6 +447,53 @@ int32_t ember_kv_set_timing(EmberPagedKv *kv, int32_t on);
 int32_t ember_kv_timing(EmberPagedKv *kv, int32_t *launches, double *total_ms);
 /* The same for the prefill-tile kernel's launches (timed while timing is on). */
 int32_t ember_kv_prefill_timing(EmberPagedKv *kv, int32_t *launches, double *total_ms);
+
+/* ---- 4. the backend ---------------------------------------------------------
+ * ember::Backend (src/backend/backend.hpp:94-123) with device "hip", behind
+ * an opaque handle: create_backend(model_dir, options) (backend.hpp:125;
+ * backend.cpp:77-87) over a Hugging Face model directory (config.json,
+ * generation_config.json, model.safetensors or its index), then forward /
+ * sample / token_probs / logits per step. C++ callers use the classes in
+ * ember_amd/csrc/host directly; these calls are the same for other FFIs. */
+
+/* The BackendOptions fields a HIP backend reads (backend.hpp:35-48). */
+typedef struct EmberBackendOptions {
+    int32_t max_batch_tokens;     /* tokens per forward */
+    int32_t max_seqs;             /* sequences per forward */
+    int32_t max_logit_rows;       /* logit rows per forward (0 = max_seqs) */
+    int64_t kv_cache_bytes;       /* K + V cache size, or 0 */
+    int32_t kv_cache_tokens;      /* or the cache in tokens, or 0 (then memory_fraction of free memory) */
+    double memory_fraction;       /* 0 = the default (0.92) */
+    int32_t gpu;                  /* device index */
+} EmberBackendOptions;
+
+typedef struct EmberModelInfo {
+    int32_t vocab_size, hidden, intermediate, n_layers, n_heads, n_kv_heads, head_dim;
+    int32_t num_kv_blocks;        /* Backend::num_kv_blocks(): blocks the engine may hand out */
+    int32_t max_logit_rows;
+} EmberModelInfo;
+
+typedef struct EmberBackend EmberBackend;
+
+/* NULL on error (ember_hip_last_error() says why). */
+EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOptions *options);
+void ember_backend_destroy(EmberBackend *backend);
+int32_t ember_backend_info(const EmberBackend *backend, EmberModelInfo *out);
+/* Backend::forward (backend.hpp:104-106): appends every token's K/V and keeps
+ * the logits of the n_rows tokens logit_rows[] on the device. */
+int32_t ember_backend_forward(EmberBackend *backend, const EmberStepBatch *batch, const int32_t *logit_rows,
+                              int32_t n_rows);
+/* Backend::sample: one token per logit row, params[i] (with its counter) for row i. */
+int32_t ember_backend_sample(EmberBackend *backend, const EmberSampleParams *params, int32_t n, int32_t *out);
+/* Backend::token_probs: out[i] = P(tokens[i]) in row rows[i]'s distribution; n_params covers every row. */
+int32_t ember_backend_token_probs(EmberBackend *backend, const EmberSampleParams *params, int32_t n_params,
+                                  const int32_t *rows, const int32_t *tokens, int32_t n, float *out);
+/* Backend::logits: row `row`'s logits into out[0..n), n >= vocab_size. */
+int32_t ember_backend_logits(EmberBackend *backend, int32_t row, float *out, int32_t n);
+int32_t ember_backend_set_capture_hidden(EmberBackend *backend, int32_t on);
+/* Backend::captured_hidden: the last token's residual after the embedding and
+ * each layer, [(n_layers + 1) * hidden]; returns the count written. */
+int32_t ember_backend_captured_hidden(EmberBackend *backend, float *out, int32_t n);
 
 #ifdef __cplusplus
 }

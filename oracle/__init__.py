@@ -29,6 +29,11 @@ _PROTOS = {
     "ember_oracle_rmsnorm": (None, [_F32P, _F32P, c_int32, c_float, _F32P]),
     "ember_oracle_rope": (None, [_F32P, c_int32, c_int32, _F32P]),
     "ember_oracle_linear": (None, [_U16P, _U16P, c_int32, c_int32, c_int32, c_int32, _F32P, c_int32]),
+    "ember_oracle_linear_mt": (None, [_U16P, _U16P, c_int32, c_int32, c_int32, c_int32, _F32P, c_int32, c_int32]),
+    "ember_oracle_rng_mix": (c_uint64, [c_uint64]),
+    "ember_oracle_gumbel": (c_float, [c_uint64, c_uint64, ctypes.c_uint32]),
+    "ember_oracle_sampling_distribution": (c_int32, [_F32P, c_int32, c_float, c_float, c_int32, c_float, _I32P, _F32P]),
+    "ember_oracle_sample": (c_int32, [_F32P, c_int32, c_float, c_float, c_int32, c_float, c_uint64, c_uint64]),
     "ember_oracle_dot": (c_float, [_F32P, _F32P, c_int32]),
     "ember_oracle_cache_offset": (c_int64, [_I32P, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
     "ember_oracle_append_layer": (c_int32, [_F32P, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
@@ -121,16 +126,47 @@ def rmsnorm(x, w, eps: float) -> np.ndarray:
     return out
 
 
-def linear(a_f16, w_f16, epilogue: int, c=None) -> np.ndarray:
-    """C = A . W^T (f16 bits in, double sums, f32 out) with an epilogue; c is the f32 C that add_f32 adds to."""
+def linear(a_f16, w_f16, epilogue: int, c=None, threads: int = 1) -> np.ndarray:
+    """C = A . W^T (f16 bits in, double sums, f32 out) with an epilogue; c is the f32 C that add_f32 adds to.
+    threads > 1 spreads the outputs over threads with bit-identical results."""
     a = np.ascontiguousarray(np.asarray(a_f16, np.float16)).view(np.uint16)
     w = np.ascontiguousarray(np.asarray(w_f16, np.float16)).view(np.uint16)
     M, K = a.shape
     N = w.shape[0]
     cols = N // 2 if epilogue == 3 else N
     out = np.zeros((M, cols), np.float32) if c is None else np.array(c, np.float32, copy=True)
-    lib().ember_oracle_linear(_p(a, _U16P), _p(w, _U16P), M, N, K, epilogue, _p(out, _F32P), cols)
+    if threads > 1:
+        lib().ember_oracle_linear_mt(_p(a, _U16P), _p(w, _U16P), M, N, K, epilogue, _p(out, _F32P), cols, threads)
+    else:
+        lib().ember_oracle_linear(_p(a, _U16P), _p(w, _U16P), M, N, K, epilogue, _p(out, _F32P), cols)
     return out
+
+
+# ---- sampling ----
+
+def rng_mix(z: int) -> int:
+    return int(lib().ember_oracle_rng_mix(z & 0xFFFFFFFFFFFFFFFF))
+
+
+def gumbel(seed: int, counter: int, token: int) -> float:
+    return float(lib().ember_oracle_gumbel(seed & 0xFFFFFFFFFFFFFFFF, counter & 0xFFFFFFFFFFFFFFFF, token))
+
+
+def sampling_distribution(logits, temperature=1.0, top_p=1.0, top_k=0, min_p=0.0):
+    """(tokens, probabilities) of the kept set, most likely first (sampling_host.cpp:20-66)."""
+    x = _f32(logits)
+    toks = np.empty(x.size, np.int32)
+    probs = np.empty(x.size, np.float32)
+    n = lib().ember_oracle_sampling_distribution(_p(x, _F32P), x.size, temperature, top_p, top_k, min_p,
+                                                 _p(toks, _I32P), _p(probs, _F32P))
+    return toks[:n].copy(), probs[:n].copy()
+
+
+def sample(logits, temperature=1.0, top_p=1.0, top_k=0, min_p=0.0, seed=0, counter=0) -> int:
+    """One draw of the host sampler (sampling_host.cpp:68-85)."""
+    x = _f32(logits)
+    return int(lib().ember_oracle_sample(_p(x, _F32P), x.size, temperature, top_p, top_k, min_p,
+                                         seed & 0xFFFFFFFFFFFFFFFF, counter & 0xFFFFFFFFFFFFFFFF))
 
 
 def rope(x, pos: int, inv_freq_: np.ndarray) -> np.ndarray:

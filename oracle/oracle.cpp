@@ -377,6 +377,128 @@ void ember_oracle_linear(const uint16_t *A, const uint16_t *W, int32_t M, int32_
     }
 }
 
+// The same linear layer with the rows of W converted once and the (token,
+// feature) outputs spread over threads; every output is the same double sum in
+// k order, so the results are bit-identical to ember_oracle_linear's.
+void ember_oracle_linear_mt(const uint16_t *A, const uint16_t *W, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                            float *C, int32_t ldc, int32_t threads) {
+    std::vector<float> a(static_cast<size_t>(M) * K), w(static_cast<size_t>(N) * K), v(static_cast<size_t>(M) * N);
+    for (size_t i = 0; i < a.size(); i++) a[i] = ember_oracle_f16_to_f32(A[i]);
+    for (size_t i = 0; i < w.size(); i++) w[i] = ember_oracle_f16_to_f32(W[i]);
+    const int nt = std::max(1, std::min<int>(threads, 64));
+    std::vector<std::thread> pool;
+    for (int th = 0; th < nt; th++)
+        pool.emplace_back([&, th] {
+            for (int64_t i = th; i < static_cast<int64_t>(M) * N; i += nt) {
+                const float *ar = &a[static_cast<size_t>(i / N) * K], *wr = &w[static_cast<size_t>(i % N) * K];
+                double s = 0.0;
+                for (int32_t k = 0; k < K; k++) s += static_cast<double>(ar[k]) * wr[k];
+                v[static_cast<size_t>(i)] = static_cast<float>(s);
+            }
+        });
+    for (auto &t : pool) t.join();
+    for (int32_t m = 0; m < M; m++) {
+        const float *vr = &v[static_cast<size_t>(m) * N];
+        float *row = C + static_cast<size_t>(m) * ldc;
+        if (epilogue == 3) {
+            for (int32_t j = 0; j < N / 2; j++) row[j] = vr[2 * j] / (1.0f + std::exp(-vr[2 * j])) * vr[2 * j + 1];
+        } else if (epilogue == 2) {
+            for (int32_t n = 0; n < N; n++) row[n] += vr[n];
+        } else {
+            for (int32_t n = 0; n < N; n++) row[n] = vr[n];
+        }
+    }
+}
+
+// ---- sampling: src/backend/sampling_host.cpp:20-87, sampling_rng.hpp:22-33 ----
+
+uint64_t ember_oracle_rng_mix(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float ember_oracle_gumbel(uint64_t seed, uint64_t counter, uint32_t id) {
+    const uint64_t h = ember_oracle_rng_mix(seed ^ ember_oracle_rng_mix(counter * 0x632BE59BD9B4E019ull + id));
+    const float u = (static_cast<float>(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    return -std::log(-std::log(u));
+}
+
+// The kept tokens and their probabilities, most likely first: temperature,
+// then top-k (ties to the lower id), top-p over the top-k set's normalized
+// mass (the first prefix reaching top_p), then min-p against the top token;
+// greedy params give the first largest logit with p = 1. Returns how many.
+int32_t ember_oracle_sampling_distribution(const float *logits, int32_t vocab, float temperature, float top_p,
+                                           int32_t top_k, float min_p, int32_t *out_tokens, float *out_probs) {
+    if (temperature <= 1e-5f) {
+        int best = 0;
+        for (int i = 1; i < vocab; i++)
+            if (logits[i] > logits[best]) best = i;
+        out_tokens[0] = best;
+        out_probs[0] = 1.0f;
+        return 1;
+    }
+    std::vector<std::pair<float, int32_t>> cand(static_cast<size_t>(vocab));
+    for (int i = 0; i < vocab; i++) cand[static_cast<size_t>(i)] = {logits[i] / temperature, i};
+    auto higher = [](const std::pair<float, int32_t> &a, const std::pair<float, int32_t> &b) {
+        return a.first > b.first || (a.first == b.first && a.second < b.second);
+    };
+    if (top_k > 0 && top_k < vocab) {
+        std::nth_element(cand.begin(), cand.begin() + (top_k - 1), cand.end(), higher);
+        cand.resize(static_cast<size_t>(top_k));
+    }
+    std::sort(cand.begin(), cand.end(), higher);
+    std::vector<double> p(cand.size());
+    double total = 0.0;
+    for (size_t i = 0; i < cand.size(); i++) total += p[i] = std::exp(static_cast<double>(cand[i].first) - cand[0].first);
+    for (double &x : p) x /= total;
+    size_t n = cand.size();
+    if (top_p < 1.0f) {
+        double cum = 0.0;
+        for (size_t i = 0; i < n; i++) {
+            cum += p[i];
+            if (cum >= top_p) {
+                n = i + 1;
+                break;
+            }
+        }
+    }
+    if (min_p > 0.0f) {
+        size_t m = 1;
+        while (m < n && p[m] >= min_p * p[0]) m++;
+        n = m;
+    }
+    double kept = 0.0;
+    for (size_t i = 0; i < n; i++) kept += p[i];
+    for (size_t i = 0; i < n; i++) {
+        out_tokens[i] = cand[i].second;
+        out_probs[i] = static_cast<float>(p[i] / kept);
+    }
+    return static_cast<int32_t>(n);
+}
+
+// One draw: the kept set's argmax of logit / temperature + Gumbel noise.
+int32_t ember_oracle_sample(const float *logits, int32_t vocab, float temperature, float top_p, int32_t top_k,
+                            float min_p, uint64_t seed, uint64_t counter) {
+    std::vector<int32_t> toks(static_cast<size_t>(vocab));
+    std::vector<float> probs(static_cast<size_t>(vocab));
+    const int n = ember_oracle_sampling_distribution(logits, vocab, temperature, top_p, top_k, min_p, toks.data(),
+                                                     probs.data());
+    if (n == 1) return toks[0];
+    int32_t best = toks[0];
+    float best_score = -INFINITY;
+    for (int i = 0; i < n; i++) {
+        const int32_t t = toks[static_cast<size_t>(i)];
+        const float score = logits[t] / temperature + ember_oracle_gumbel(seed, counter, static_cast<uint32_t>(t));
+        if (score > best_score) {
+            best_score = score;
+            best = t;
+        }
+    }
+    return best;
+}
+
 float ember_oracle_dot(const float *a, const float *b, int32_t n) { return dot(a, b, n); }
 
 int64_t ember_oracle_cache_offset(const int32_t *tables, int32_t max_blocks, int32_t num_blocks, int32_t n_kv,

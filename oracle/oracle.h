@@ -43,6 +43,26 @@ void ember_oracle_rmsnorm(const float *x, const float *w, int32_t n, float eps, 
  * Pinned: numpy float64 matmul, the identity weight, silu's closed form. */
 void ember_oracle_linear(const uint16_t *A, const uint16_t *W, int32_t M, int32_t N, int32_t K, int32_t epilogue,
                          float *C, int32_t ldc);
+/* The same on `threads` threads; bit-identical results (each output is the
+ * same double sum in k order). Pinned: equality with ember_oracle_linear. */
+void ember_oracle_linear_mt(const uint16_t *A, const uint16_t *W, int32_t M, int32_t N, int32_t K, int32_t epilogue,
+                            float *C, int32_t ldc, int32_t threads);
+
+/* Sampling (src/backend/sampling_host.cpp:20-87, src/backend/sampling_rng.hpp:22-33).
+ * rng_mix: SplitMix64's output step, pinned by its published first outputs.
+ * gumbel: -log(-log(u)) of a 24-bit uniform from (seed, counter, id); pinned
+ * by the Gumbel(0, 1) mean (Euler-Mascheroni) and variance (pi^2 / 6).
+ * sampling_distribution: the kept tokens, most likely first, with their
+ * probabilities; pinned by numpy restatements of each filter on their own
+ * (greedy argmax, top-k by sort, top-p cumulative, min-p ratio) and by the
+ * probabilities summing to 1. sample: argmax of logit / T + gumbel over the
+ * kept set; pinned by its frequencies against the distribution. */
+uint64_t ember_oracle_rng_mix(uint64_t z);
+float ember_oracle_gumbel(uint64_t seed, uint64_t counter, uint32_t id);
+int32_t ember_oracle_sampling_distribution(const float *logits, int32_t vocab, float temperature, float top_p,
+                                           int32_t top_k, float min_p, int32_t *out_tokens, float *out_probs);
+int32_t ember_oracle_sample(const float *logits, int32_t vocab, float temperature, float top_p, int32_t top_k,
+                            float min_p, uint64_t seed, uint64_t counter);
 
 /* Rotate-half RoPE of one head vector in place (cpu_backend.cpp:262-272).
  * Pinned: transformers' apply_rotary_pos_emb; pos 0 is the identity; pair norms kept. */

@@ -1,0 +1,205 @@
+"""HipBackend (ember::Backend, device "hip") end to end against the oracle, on a synthetic Qwen3-shaped model.
+
+The model: config 1's Qwen3-0.6B attention shape (hidden 1024, 16 q / 8 kv heads, head_dim 128, QK-RMSNorm, RoPE
+theta 1e6) with the 0.6B model's MLP (intermediate 3072), 4 layers and an 8192-token tied vocabulary; N(0, 0.02)
+weights written with the safetensors package in three dtypes (F32 projections, BF16 gate/up, F16 the rest), so the
+backend's load-time conversions are exercised. The oracle composes its own pieces (rmsnorm, linear, append and
+attention, as oracle/ restates them from the reference's CPU backend) with the GPU path's f16 roundings (xn, qkv,
+attention output and the MLP activation stored as f16; cuda_backend.cu:350-366).
+
+The run mirrors the reference's model tests: one sequence, a 512-token prompt then 128 greedy decode steps
+(tests/test_model.cpp:95-101), and the uneven 300 / 37 / 363 chunks at block offset 3 with 8 greedy decodes
+(:124-157). Logits within 2e-2 of the oracle's (max |d| / max |oracle|; the reference allows 3e-2 between its CPU and
+CUDA backends); decode inputs follow the oracle's greedy tokens, and the GPU's greedy token equals the oracle's
+wherever the oracle's top-two margin exceeds the logit error.
+"""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from ember_amd.backend import BackendOptions, SampleRequest, SamplingParams, create_backend
+from ember_amd.paged_kv import StepBatch
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(model_type="qwen3", vocab_size=8192, hidden_size=1024, intermediate_size=3072, num_hidden_layers=4,
+           num_attention_heads=16, num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6,
+           max_position_embeddings=2048, tie_word_embeddings=True, eos_token_id=2)
+H, I, L, V = 1024, 3072, 4, 8192
+NH, NKV, D = 16, 8, 128
+Q, KV = NH * D, NKV * D
+PAGE = 16
+
+
+@pytest.fixture(scope="module")
+def model(tmp_path_factory):
+    """Writes the model directory; returns (dir, the oracle's f16 / f32 copies of every weight)."""
+    from safetensors.torch import save_file
+
+    d = tmp_path_factory.mktemp("qwen3_synthetic")
+    g = torch.Generator().manual_seed(20261005)
+    n = lambda *s: torch.randn(*s, generator=g) * 0.02  # noqa: E731
+    t = {"model.embed_tokens.weight": n(V, H).to(torch.float16), "model.norm.weight": 1 + 0.1 * torch.randn(H, generator=g)}
+    for layer in range(L):
+        p = f"model.layers.{layer}."
+        t[p + "self_attn.q_proj.weight"] = n(Q, H)
+        t[p + "self_attn.k_proj.weight"] = n(KV, H)
+        t[p + "self_attn.v_proj.weight"] = n(KV, H)
+        t[p + "self_attn.o_proj.weight"] = n(H, Q).to(torch.float16)
+        t[p + "mlp.gate_proj.weight"] = n(I, H).to(torch.bfloat16)
+        t[p + "mlp.up_proj.weight"] = n(I, H).to(torch.bfloat16)
+        t[p + "mlp.down_proj.weight"] = n(H, I).to(torch.float16)
+        t[p + "input_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
+        t[p + "post_attention_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
+        t[p + "self_attn.q_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
+        t[p + "self_attn.k_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
+    save_file({k: v.contiguous() for k, v in t.items()}, str(d / "model.safetensors"))
+    (d / "config.json").write_text(json.dumps(CFG))
+    f16 = lambda k: t[k].to(torch.float16).numpy()  # noqa: E731  (the backend's conversion: round to nearest f16)
+    f32 = lambda k: t[k].float().numpy()  # noqa: E731
+    w = {"embed": f16("model.embed_tokens.weight"), "norm": f32("model.norm.weight"), "layers": []}
+    for layer in range(L):
+        p = f"model.layers.{layer}."
+        gate, up = f16(p + "mlp.gate_proj.weight"), f16(p + "mlp.up_proj.weight")
+        gu = np.empty((2 * I, H), np.float16)
+        gu[0::2], gu[1::2] = gate, up  # interleaved rows, the silu_mul epilogue's layout
+        w["layers"].append(dict(
+            qkv=np.concatenate([f16(p + "self_attn.q_proj.weight"), f16(p + "self_attn.k_proj.weight"),
+                                f16(p + "self_attn.v_proj.weight")]),
+            o=f16(p + "self_attn.o_proj.weight"), gate_up=gu, down=f16(p + "mlp.down_proj.weight"),
+            in_norm=f32(p + "input_layernorm.weight"), post_norm=f32(p + "post_attention_layernorm.weight"),
+            q_norm=f32(p + "self_attn.q_norm.weight"), k_norm=f32(p + "self_attn.k_norm.weight")))
+    return d, w
+
+
+class OracleModel:
+    """The forward pass composed from the oracle's pieces, f16 K/V pages in the oracle's own pool."""
+
+    def __init__(self, w, num_blocks=64):
+        self.w, self.NB = w, num_blocks
+        self.k = [np.zeros((num_blocks, NKV, PAGE, D), np.uint16) for _ in range(L)]
+        self.v = [np.zeros_like(self.k[0]) for _ in range(L)]
+        self.inv = oracle.inv_freq(1e6, D)
+
+    def _norm(self, h, wt):
+        return np.stack([oracle.rmsnorm(r, wt, 1e-6) for r in h]).astype(np.float16)
+
+    def forward(self, tokens, positions, table, logit_rows):
+        T = len(tokens)
+        h = self.w["embed"][np.asarray(tokens)].astype(np.float32)
+        qs = np.array([0, T], np.int32)
+        for layer, lw in enumerate(self.w["layers"]):
+            xn = self._norm(h, lw["in_norm"])
+            qkv = oracle.linear(xn, lw["qkv"], 0, threads=16).astype(np.float16).astype(np.float32)
+            q = oracle.append_layer(qkv, positions, qs, table, self.k[layer], self.v[layer], n_heads=NH, n_kv=NKV,
+                                    inv_freq_=self.inv, eps=1e-6, q_norm=lw["q_norm"], k_norm=lw["k_norm"],
+                                    num_blocks=self.NB, kv_f16=True)
+            att = oracle.attention_layer(q, positions, qs, table, self.k[layer], self.v[layer], n_heads=NH, n_kv=NKV,
+                                         num_blocks=self.NB, kv_f16=True, q_f16=True, threads=16)
+            h = oracle.linear(att.reshape(T, Q).astype(np.float16), lw["o"], 2, h, threads=16)
+            xn = self._norm(h, lw["post_norm"])
+            act = oracle.linear(xn, lw["gate_up"], 3, threads=16).astype(np.float16)
+            h = oracle.linear(act, lw["down"], 2, h, threads=16)
+        xn = self._norm(h[np.asarray(logit_rows)], self.w["norm"])
+        return oracle.linear(xn, self.w["embed"], 1, threads=16)
+
+
+def _batch(tokens, start, first_block, n_pages, logit_rows):
+    T = len(tokens)
+    return StepBatch(tokens=list(tokens), positions=list(range(start, start + T)), query_start=[0, T],
+                     context_len=[start + T], block_tables=list(range(first_block, first_block + n_pages)),
+                     max_blocks=n_pages), np.arange(start, start + T, dtype=np.int32)
+
+
+def _rel(got, want):
+    return float(np.abs(got - want).max() / np.abs(want).max())
+
+
+def _greedy_run(be, om, chunks, n_decode, first_block, rng):
+    """Runs the prompt chunks then greedy decodes on both; returns (worst logit error, decisive agreements)."""
+    greedy = [SampleRequest(SamplingParams(temperature=0.0))]
+    prompt = rng.integers(3, V, sum(chunks)).tolist()
+    n_pages = (sum(chunks) + n_decode + PAGE - 1) // PAGE
+    otab = np.arange(n_pages, dtype=np.int32)[None, :]
+    worst, decisive, length = 0.0, 0, 0
+    steps = [prompt[sum(chunks[:i]):sum(chunks[:i + 1])] for i in range(len(chunks))]
+    nxt = None
+    for i in range(len(steps) + n_decode):
+        toks = steps[i] if i < len(steps) else [nxt]
+        b, pos = _batch(toks, length, first_block, (length + len(toks) + PAGE - 1) // PAGE, [len(toks) - 1])
+        b.logit_rows = [len(toks) - 1]
+        be.forward(b)
+        got = be.logits(0)
+        want = om.forward(toks, pos, otab, [len(toks) - 1])[0]
+        err = _rel(got, want)
+        worst = max(worst, err)
+        srt = np.sort(want)
+        gpu_tok = be.sample(greedy)[0]
+        if srt[-1] - srt[-2] > 2 * np.abs(got - want).max():  # the oracle's choice is decisive at this error
+            assert gpu_tok == int(np.argmax(want)), f"step {i}: greedy {gpu_tok} vs oracle {int(np.argmax(want))}"
+            decisive += 1
+        assert gpu_tok == int(np.argmax(got)), "sample(temperature 0) is the argmax of the backend's own logits"
+        nxt = int(np.argmax(want))  # both follow the oracle's greedy token
+        length += len(toks)
+    return worst, decisive
+
+
+def test_prefill_512_then_128_greedy_decodes(model):
+    d, w = model
+    be = create_backend(str(d), BackendOptions(max_batch_tokens=1024, max_seqs=8, kv_cache_tokens=64 * PAGE))
+    assert be.num_kv_blocks() == 64 and be.vocab_size == V
+    worst, decisive = _greedy_run(be, OracleModel(w), [512], 128, 0, np.random.default_rng(5))
+    assert worst < 2e-2, f"logits differ from the oracle by {worst:.2e}"
+    assert decisive >= 100, f"only {decisive} of 129 greedy choices were decisive"
+    be.close()
+
+
+def test_uneven_chunks_at_block_offset_3(model):
+    """tests/test_model.cpp:124-157: chunks of 300, 37 (ending mid-page) and 363 on blocks from 3 (the oracle's
+    sequence on blocks from 0), then 8 greedy decodes."""
+    d, w = model
+    be = create_backend(str(d), BackendOptions(max_batch_tokens=512, max_seqs=8, kv_cache_tokens=64 * PAGE))
+    worst, decisive = _greedy_run(be, OracleModel(w), [300, 37, 363], 8, 3, np.random.default_rng(6))
+    assert worst < 2e-2, f"logits differ from the oracle by {worst:.2e}"
+    assert decisive >= 6
+    be.close()
+
+
+def test_capture_hidden_and_token_probs(model):
+    d, w = model
+    be = create_backend(str(d), BackendOptions(max_batch_tokens=64, max_seqs=4, kv_cache_tokens=8 * PAGE))
+    be.set_capture_hidden(True)
+    toks = [5, 17, 300, 4000, 8191]
+    b, pos = _batch(toks, 0, 0, 1, [4])
+    b.logit_rows = [2, 4]
+    be.forward(b)
+    hid = be.captured_hidden().reshape(L + 1, H)
+    np.testing.assert_array_equal(hid[0], w["embed"][toks[-1]].astype(np.float32))  # the embedding, exactly
+    assert np.isfinite(hid).all() and not np.array_equal(hid[1], hid[0])
+    reqs = [SampleRequest(SamplingParams(temperature=0.7, top_k=50), counter=9), SampleRequest(SamplingParams(0.0))]
+    lg = [be.logits(0), be.logits(1)]
+    toks_, probs_ = oracle.sampling_distribution(lg[0], 0.7, 1.0, 50, 0.0)
+    got = be.token_probs(reqs, [0, 0, 0, 1], [int(toks_[0]), int(toks_[10]), int(np.argsort(lg[0])[0]),
+                                              int(np.argmax(lg[1]))])
+    np.testing.assert_allclose(got[:2], probs_[[0, 10]], rtol=1e-4)
+    assert got[2] == 0.0 and got[3] == 1.0  # outside the top-50; greedy row's argmax
+    be.close()
+
+
+def test_errors_raise(model, tmp_path):
+    from ember_amd import EmberError
+
+    d, _ = model
+    with pytest.raises(EmberError, match="config.json"):
+        create_backend(str(tmp_path), BackendOptions(kv_cache_tokens=256))
+    be = create_backend(str(d), BackendOptions(max_batch_tokens=16, max_seqs=2, kv_cache_tokens=4 * PAGE))
+    b, _ = _batch([1, V + 5], 0, 0, 1, [1])
+    b.logit_rows = [1]
+    with pytest.raises(EmberError, match="outside the vocabulary"):
+        be.forward(b)
+    with pytest.raises(EmberError, match="requests for"):
+        be.sample([SampleRequest(), SampleRequest()])
+    be.close()

@@ -40,3 +40,14 @@ def test_silu_mul_closed_form():
     g, u = a[:, 0::2][:, :2].astype(np.float64), a[:, 1::2][:, :2].astype(np.float64)
     want = g / (1 + np.exp(-g)) * u
     np.testing.assert_allclose(got, want, rtol=2e-7, atol=1e-7)
+
+
+@pytest.mark.parametrize("epilogue", [0, 1, 2, 3])
+def test_threaded_linear_is_bit_identical(epilogue):
+    """The threaded form spreads the same double sums over threads: every epilogue, bit for bit."""
+    rng = np.random.default_rng(12)
+    a, w = _f16(rng, (37, 96), 1.0), _f16(rng, (64, 96), 0.1)
+    c = rng.standard_normal((37, 32 if epilogue == 3 else 64)).astype(np.float32)
+    one = oracle.linear(a, w, epilogue, c if epilogue == 2 else None)
+    many = oracle.linear(a, w, epilogue, c if epilogue == 2 else None, threads=7)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))
