@@ -32,6 +32,14 @@ def _built_libraries():
 
     if not b.LIB.exists():
         b.build()
+    driver = ROOT / "tests" / "cpp" / "_build" / "hip_engine_test"
+    if not driver.exists():
+        import importlib.util
+
+        spec = importlib.util.spec_from_file_location("cpp_drivers", ROOT / "tests" / "cpp" / "build.py")
+        drivers = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(drivers)
+        drivers.build()
     yield
 
 

@@ -13,8 +13,6 @@ The run mirrors the reference's model tests: one sequence, a 512-token prompt th
 CUDA backends); decode inputs follow the oracle's greedy tokens, and the GPU's greedy token equals the oracle's
 wherever the oracle's top-two margin exceeds the logit error.
 """
-import json
-
 import numpy as np
 import pytest
 import torch
@@ -22,12 +20,10 @@ import torch
 import oracle
 from ember_amd.backend import BackendOptions, SampleRequest, SamplingParams, create_backend
 from ember_amd.paged_kv import StepBatch
+from synthetic_model import write_model
 
 pytestmark = pytest.mark.gpu
 
-CFG = dict(model_type="qwen3", vocab_size=8192, hidden_size=1024, intermediate_size=3072, num_hidden_layers=4,
-           num_attention_heads=16, num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, rope_theta=1e6,
-           max_position_embeddings=2048, tie_word_embeddings=True, eos_token_id=2)
 H, I, L, V = 1024, 3072, 4, 8192
 NH, NKV, D = 16, 8, 128
 Q, KV = NH * D, NKV * D
@@ -37,42 +33,8 @@ PAGE = 16
 @pytest.fixture(scope="module")
 def model(tmp_path_factory):
     """Writes the model directory; returns (dir, the oracle's f16 / f32 copies of every weight)."""
-    from safetensors.torch import save_file
-
     d = tmp_path_factory.mktemp("qwen3_synthetic")
-    g = torch.Generator().manual_seed(20261005)
-    n = lambda *s: torch.randn(*s, generator=g) * 0.02  # noqa: E731
-    t = {"model.embed_tokens.weight": n(V, H).to(torch.float16), "model.norm.weight": 1 + 0.1 * torch.randn(H, generator=g)}
-    for layer in range(L):
-        p = f"model.layers.{layer}."
-        t[p + "self_attn.q_proj.weight"] = n(Q, H)
-        t[p + "self_attn.k_proj.weight"] = n(KV, H)
-        t[p + "self_attn.v_proj.weight"] = n(KV, H)
-        t[p + "self_attn.o_proj.weight"] = n(H, Q).to(torch.float16)
-        t[p + "mlp.gate_proj.weight"] = n(I, H).to(torch.bfloat16)
-        t[p + "mlp.up_proj.weight"] = n(I, H).to(torch.bfloat16)
-        t[p + "mlp.down_proj.weight"] = n(H, I).to(torch.float16)
-        t[p + "input_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
-        t[p + "post_attention_layernorm.weight"] = 1 + 0.1 * torch.randn(H, generator=g)
-        t[p + "self_attn.q_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
-        t[p + "self_attn.k_norm.weight"] = 1 + 0.1 * torch.randn(D, generator=g)
-    save_file({k: v.contiguous() for k, v in t.items()}, str(d / "model.safetensors"))
-    (d / "config.json").write_text(json.dumps(CFG))
-    f16 = lambda k: t[k].to(torch.float16).numpy()  # noqa: E731  (the backend's conversion: round to nearest f16)
-    f32 = lambda k: t[k].float().numpy()  # noqa: E731
-    w = {"embed": f16("model.embed_tokens.weight"), "norm": f32("model.norm.weight"), "layers": []}
-    for layer in range(L):
-        p = f"model.layers.{layer}."
-        gate, up = f16(p + "mlp.gate_proj.weight"), f16(p + "mlp.up_proj.weight")
-        gu = np.empty((2 * I, H), np.float16)
-        gu[0::2], gu[1::2] = gate, up  # interleaved rows, the silu_mul epilogue's layout
-        w["layers"].append(dict(
-            qkv=np.concatenate([f16(p + "self_attn.q_proj.weight"), f16(p + "self_attn.k_proj.weight"),
-                                f16(p + "self_attn.v_proj.weight")]),
-            o=f16(p + "self_attn.o_proj.weight"), gate_up=gu, down=f16(p + "mlp.down_proj.weight"),
-            in_norm=f32(p + "input_layernorm.weight"), post_norm=f32(p + "post_attention_layernorm.weight"),
-            q_norm=f32(p + "self_attn.q_norm.weight"), k_norm=f32(p + "self_attn.k_norm.weight")))
-    return d, w
+    return d, write_model(d, layers=L, vocab=V)
 
 
 class OracleModel:
