@@ -627,21 +627,25 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             QSlice<T> qrow;
             if constexpr (Q_LDS) load_q(qrow, &q_lds[src_row(row)][8 * c]);
             else qrow = q[row];
-            float s[4];
+            float s[4];  // raw dot products; the softmax scale is applied in the exponent
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                s[i] = row16_sum(dot8(qrow, pr.k[i])) * p.scale_log2;
+                s[i] = row16_sum(dot8(qrow, pr.k[i]));
                 if constexpr (MASKED) {
                     vis[row][i] = key0 + 4 * i <= row_pos[row];
                     if (!vis[row][i]) s[i] = -INFINITY;
                 }
             }
-            // m starts at kNoMax, not -inf, so mn is always finite: no select guards
-            // the subtraction, and corr is 2^0 = 1 exactly when the max stays.
-            const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
-            const float corr = exp2_hw(m[row] - mn);
+            // The running max m is in scaled units: round(scale * max s) is the
+            // max of the rounded scaled scores (scale > 0, rounding monotonic).
+            // m starts at kNoMax, not -inf, so mn is always finite: no select
+            // guards the subtraction, and corr is 2^0 = 1 exactly when the max
+            // stays.
+            const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * p.scale_log2);
 #pragma unroll
-            for (int i = 0; i < 4; i++) pj[row][i] = exp2_hw(s[i] - mn);  // 2^-inf = 0 for hidden keys
+            for (int i = 0; i < 4; i++)  // 2^-inf = 0 for hidden keys
+                pj[row][i] = exp2_hw(__builtin_fmaf(s[i], p.scale_log2, -mn));
+            const float corr = exp2_hw(m[row] - mn);
             l[row] = l[row] * corr + ((pj[row][0] + pj[row][1]) + (pj[row][2] + pj[row][3]));
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
