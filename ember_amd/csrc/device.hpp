@@ -23,10 +23,11 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // DPP move of a float (row_mask, bank_mask all on; every source lane exists
-// for the quad/mirror patterns used here).
+// for the quad / mirror / row broadcast patterns used here, so no lane keeps
+// an old value and none needs initialising).
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 
 constexpr int kDppQuadXor1 = 0xb1;     // quad_perm [1,0,3,2]

@@ -254,6 +254,44 @@ __device__ __forceinline__ void unpack8(const float4 (&v)[2], float (&out)[8]) {
 // weights that cannot move an f32 sum.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// The page's scores in a DPP row (16 lanes, c = lane % 16, each holding an
+// 8-dim partial dot product for the row's keys i = 0..3): reduced so that
+// the lanes of quad q = c / 4 hold key q's full score, with 11 instructions
+// instead of the 16 that give every lane all four. Two exchange steps halve
+// the keys a lane carries (c pairs with 15 - c, keys {0,1} staying with c < 8;
+// then c with its row-half mirror, keys q staying with quad q), and two quad
+// steps finish the sums. The 16 lanes' partials of a key meet in a fixed tree,
+// and the quad steps add values both partners hold, so the four lanes of a
+// quad end bit-identical.
+__device__ __forceinline__ float key_sums(const float (&x)[4], bool upper_half, bool odd_quad) {
+    const float keep0 = upper_half ? x[2] : x[0], give0 = upper_half ? x[0] : x[2];
+    const float keep1 = upper_half ? x[3] : x[1], give1 = upper_half ? x[1] : x[3];
+    const float a0 = keep0 + dpp_mov<kDppRowMirror>(give0);
+    const float a1 = keep1 + dpp_mov<kDppRowMirror>(give1);
+    const float keep = odd_quad ? a1 : a0, give = odd_quad ? a0 : a1;
+    float b = keep + dpp_mov<kDppRowHalfMirror>(give);
+    b = b + dpp_mov<kDppQuadXor1>(b);
+    return b + dpp_mov<kDppQuadXor2>(b);
+}
+
+// Max and sum over the four quads of a DPP row; every lane gets the same bits
+// (quads q and q ^ 1 meet first, then the pairs, and both operations are
+// commutative). The sum is (v0 + v1) + (v2 + v3).
+__device__ __forceinline__ float quads_max(float v) {
+    v = fmaxf(v, dpp_mov<kDppRowHalfMirror>(v));
+    return fmaxf(v, dpp_mov<kDppRowMirror>(v));
+}
+__device__ __forceinline__ float quads_sum(float v) {
+    v = v + dpp_mov<kDppRowHalfMirror>(v);
+    return v + dpp_mov<kDppRowMirror>(v);
+}
+
+// Lane 4 q of each DPP row to every lane of the row: quad q's value (row_newbcast).
+template <int Q>
+__device__ __forceinline__ float quad_value(float v) {
+    return dpp_mov<0x150 + 4 * Q>(v);
+}
+
 // Merges this lane's (m, l, acc) with the lane `mask` away; both lanes end
 // with the same values.
 // The running max of a row before any visible key: finite and far below any
@@ -619,6 +657,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     // for a fully visible page both forms compute the same bits. The two halves
     // read only pr.k and only pr.v, so a wave can load the next page's keys
     // between them.
+    const int quad = c >> 2;
+    const bool upper_half = c >= 8, odd_quad = (c & 4) != 0;
     auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, float (&pj)[ROWS][4], bool (&vis)[ROWS][4]) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
@@ -627,26 +667,30 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             QSlice<T> qrow;
             if constexpr (Q_LDS) load_q(qrow, &q_lds[src_row(row)][8 * c]);
             else qrow = q[row];
-            float s[4];  // raw dot products; the softmax scale is applied in the exponent
+            float x[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                s[i] = row16_sum(dot8(qrow, pr.k[i]));
-                if constexpr (MASKED) {
-                    vis[row][i] = key0 + 4 * i <= row_pos[row];
-                    if (!vis[row][i]) s[i] = -INFINITY;
-                }
+            for (int i = 0; i < 4; i++) x[i] = dot8(qrow, pr.k[i]);
+            // This lane's key (quad q of the DPP row: key 4 q + r of the page),
+            // its raw score; the softmax scale is applied in the exponent.
+            float sq = key_sums(x, upper_half, odd_quad);
+            if constexpr (MASKED) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) vis[row][i] = key0 + 4 * i <= row_pos[row];
+                if (key0 + 4 * quad > row_pos[row]) sq = -INFINITY;
             }
             // The running max m is in scaled units: round(scale * max s) is the
             // max of the rounded scaled scores (scale > 0, rounding monotonic).
             // m starts at kNoMax, not -inf, so mn is always finite: no select
             // guards the subtraction, and corr is 2^0 = 1 exactly when the max
-            // stays.
-            const float mn = fmaxf(m[row], fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * p.scale_log2);
-#pragma unroll
-            for (int i = 0; i < 4; i++)  // 2^-inf = 0 for hidden keys
-                pj[row][i] = exp2_hw(__builtin_fmaf(s[i], p.scale_log2, -mn));
+            // stays. One exponential per lane: its own key's weight.
+            const float mn = fmaxf(m[row], quads_max(sq) * p.scale_log2);
+            const float pq = exp2_hw(__builtin_fmaf(sq, p.scale_log2, -mn));  // 2^-inf = 0 for a hidden key
+            pj[row][0] = quad_value<0>(pq);
+            pj[row][1] = quad_value<1>(pq);
+            pj[row][2] = quad_value<2>(pq);
+            pj[row][3] = quad_value<3>(pq);
             const float corr = exp2_hw(m[row] - mn);
-            l[row] = l[row] * corr + ((pj[row][0] + pj[row][1]) + (pj[row][2] + pj[row][3]));
+            l[row] = l[row] * corr + quads_sum(pq);
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
             m[row] = mn;
