@@ -168,6 +168,20 @@ __device__ __forceinline__ void put_key(PageRegs<T> &pr, int i, bool take, const
     }
 }
 
+// A row's weights for the page's four keys (of this lane's DPP row): f32 for
+// f32 pages; for f16 pages f16 values packed in key pairs (0, 1), (2, 3), the
+// operands of the value products' v_dot2_f32_f16.
+template <typename T>
+struct Weights;
+template <>
+struct Weights<f16> {
+    f16x2 w[2];
+};
+template <>
+struct Weights<float> {
+    float w[4];
+};
+
 // The query slice a lane needs: dims [8c, 8c + 8) of one row.
 template <typename T>
 struct QSlice;
@@ -659,7 +673,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     // between them.
     const int quad = c >> 2;
     const bool upper_half = c >= 8, odd_quad = (c & 4) != 0;
-    auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, float (&pj)[ROWS][4], bool (&vis)[ROWS][4]) {
+    auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, Weights<T> (&pj)[ROWS], bool (&vis)[ROWS][4]) {
         constexpr bool MASKED = decltype(masked_tag)::value;
         const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
 #pragma unroll
@@ -684,11 +698,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             // guards the subtraction, and corr is 2^0 = 1 exactly when the max
             // stays. One exponential per lane: its own key's weight.
             const float mn = fmaxf(m[row], quads_max(sq) * p.scale_log2);
-            const float pq = exp2_hw(__builtin_fmaf(sq, p.scale_log2, -mn));  // 2^-inf = 0 for a hidden key
-            pj[row][0] = quad_value<0>(pq);
-            pj[row][1] = quad_value<1>(pq);
-            pj[row][2] = quad_value<2>(pq);
-            pj[row][3] = quad_value<3>(pq);
+            float pq = exp2_hw(__builtin_fmaf(sq, p.scale_log2, -mn));  // 2^-inf = 0 for a hidden key
+            // f16 pages: the weight rounded to f16 (to nearest), for the value
+            // products on key pairs (v_dot2_f32_f16) and the row sum alike, so
+            // numerator and denominator use the same weights.
+            if constexpr (sizeof(T) == 2) {
+                pq = static_cast<float>(static_cast<_Float16>(pq));
+                pj[row].w[0] = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(quad_value<0>(pq), quad_value<1>(pq)));
+                pj[row].w[1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(quad_value<2>(pq), quad_value<3>(pq)));
+            } else {
+                pj[row].w[0] = quad_value<0>(pq);
+                pj[row].w[1] = quad_value<1>(pq);
+                pj[row].w[2] = quad_value<2>(pq);
+                pj[row].w[3] = quad_value<3>(pq);
+            }
             const float corr = exp2_hw(m[row] - mn);
             l[row] = l[row] * corr + quads_sum(pq);
 #pragma unroll
@@ -696,21 +719,59 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             m[row] = mn;
         }
     };
-    auto values = [&](const PageRegs<T> &pr, auto masked_tag, const float (&pj)[ROWS][4], const bool (&vis)[ROWS][4]) {
+    auto values = [&](const PageRegs<T> &pr, auto masked_tag, const Weights<T> (&pj)[ROWS], const bool (&vis)[ROWS][4]) {
         constexpr bool MASKED = decltype(masked_tag)::value;
+        if constexpr (sizeof(T) == 2) {
+            // f16 pages: keys in pairs (0, 1), (2, 3), one v_dot2_f32_f16 per
+            // pair and dim: V regrouped once per page into (key a, key b)
+            // halves per dim, shared by every row. A masked pair with one key
+            // hidden takes the visible key alone (a single FMA), so no product
+            // ever meets a slot past a row's position, which may hold anything.
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float vf[8];
-            unpack8(pr.v[i], vf);
+            for (int pair = 0; pair < 2; pair++) {
+                const uint4 va = pr.v[2 * pair], vb = pr.v[2 * pair + 1];
+                const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
+                f16x2 vv[8];
 #pragma unroll
-            for (int row = 0; row < ROWS; row++) {
-                if constexpr (!MASKED) {
+                for (int w = 0; w < 4; w++) {
+                    vv[2 * w] = as_f16x2(__builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u));      // dim 2w of keys a, b
+                    vv[2 * w + 1] = as_f16x2(__builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u));  // dim 2w + 1
+                }
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[row][i], vf[e], acc[row][e]);
-                } else {
+                for (int row = 0; row < ROWS; row++) {
+                    const f16x2 pp = pj[row].w[pair];
+                    if constexpr (!MASKED) {
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        acc[row][e] = vis[row][i] ? fmaf(pj[row][i], vf[e], acc[row][e]) : acc[row][e];
+                        for (int e = 0; e < 8; e++) acc[row][e] = __builtin_amdgcn_fdot2(pp, vv[e], acc[row][e], false);
+                    } else {
+                        const bool v0 = vis[row][2 * pair], v1 = vis[row][2 * pair + 1];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) {
+                            const float both = __builtin_amdgcn_fdot2(pp, vv[e], acc[row][e], false);
+                            const float only0 =
+                                fmaf(static_cast<float>(pp.x), static_cast<float>(vv[e].x), acc[row][e]);
+                            const float only1 =
+                                fmaf(static_cast<float>(pp.y), static_cast<float>(vv[e].y), acc[row][e]);
+                            acc[row][e] = v0 ? (v1 ? both : only0) : (v1 ? only1 : acc[row][e]);
+                        }
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float vf[8];
+                unpack8(pr.v[i], vf);
+#pragma unroll
+                for (int row = 0; row < ROWS; row++) {
+                    if constexpr (!MASKED) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[row][e] = fmaf(pj[row].w[i], vf[e], acc[row][e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; e++)
+                            acc[row][e] = vis[row][i] ? fmaf(pj[row].w[i], vf[e], acc[row][e]) : acc[row][e];
+                    }
                 }
             }
         }
@@ -731,7 +792,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
                 }
             }
         }
-        float pj[ROWS][4];
+        Weights<T> pj[ROWS];
         bool vis[ROWS][4];
         scores(pr, page, Masked{}, pj, vis);
         values(pr, Masked{}, pj, vis);
@@ -752,7 +813,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     __builtin_amdgcn_s_setprio(0);
     int j = 0;
     for (; j < n_fast; j++) {
-        float pj[ROWS][4];
+        Weights<T> pj[ROWS];
         bool vis[ROWS][4];
         scores(A, page_of(j), Fast{}, pj, vis);
         phase_break();
