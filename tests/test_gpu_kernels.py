@@ -348,6 +348,36 @@ def test_in_kernel_merge_leaves_counters_zero_and_matches(rng, device):
         assert int(keep[-1].abs().sum()) == 0, "merge counters not reset"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_in_kernel_merge_of_runs_across_a_split_boundary(rng, device, dtype):
+    """Runs of 5 tokens whose positions straddle a split boundary (their rows merge 1 or 2 splits, 8 or 9):
+    the in-kernel merge equals the merge kernel to the bit, launch after launch on the same buffers, and
+    leaves the counters zero."""
+    f16 = dtype == torch.float16
+    NB = 1500
+    cached = [508, 1021, 4094, 3, 512]
+    new = [5, 5, 5, 5, 5]
+    step = make_step(rng, [c + n for c, n in zip(cached, new)], new, NB)
+    k, v = _random_pools(rng, step, NB, f16=f16)
+    kp, vp = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float16 if f16 else np.float32)
+    runs = (step.query_start[:-1], np.diff(step.query_start))
+    bits = lambda t: t.cpu().numpy().view(np.uint16 if f16 else np.uint32)  # noqa: E731
+    want = bits(_run_decode(q, kp, vp, step, NB, device, runs=runs, use_work_list=True, merge_in_kernel=False))
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    out = torch.empty((step.T, H, D), dtype=dtype, device=device)
+    qd = torch.from_numpy(q).to(device)  # alive for every launch below: the arguments hold only its address
+    a, keep = K._attn_args(qd, kp, vp, out, ints, n_heads=H, n_kv=KVH, token_list=None, runs=runs, split_len=512,
+                           num_splits=None, scratch=None, use_work_list=True, merge_in_kernel=True)
+    from ember_amd import _lib
+    for _ in range(3):
+        out.fill_(float("nan"))
+        _lib.check(_lib.lib().ember_hip_paged_decode(a, torch.cuda.current_stream().cuda_stream), "paged_decode")
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(out), want)
+        assert int(keep[-1].abs().sum()) == 0, "merge counters not reset"
+
+
 # ---- MFMA prefill tiles ----
 
 def _tiles_of(step, tile=64):
