@@ -68,9 +68,17 @@ def common_flags() -> list[str]:
     ]
 
 
+# Per-source additions. The decode kernel rescales its MFMA accumulators on the
+# VALU every page: they stay in VGPRs (the VGPR form of v_mfma) instead of
+# being copied out of and back into AGPRs around each rescale.
+EXTRA_FLAGS = {
+    "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.relative_to(CSRC).as_posix().replace("/", "__") + ".o")
-    cmd = [hipcc(), *common_flags(), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *common_flags(), *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd[1:1] = ["-x", "hip"]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,4 +1,5 @@
-// Paged decode attention on gfx950 VALU (no MFMA): a bandwidth-bound gather.
+// Paged decode attention on gfx950: a bandwidth-bound gather whose page
+// arithmetic runs on MFMA for f16 pages (VALU for f32 pages).
 //
 // Replaces the reference's paged_attention_kernel + combine_splits_kernel
 // (src/backend/cuda/k_attention.cu:29-201), and in its fused form also its
@@ -10,27 +11,44 @@
 //
 // Work-group = 4 waves per (query run, kv head, context split). A run is 1..8
 // consecutive tokens of one sequence (decode: 1; speculative verify: k + 1);
-// all of them are served by the same page reads.
+// all of them are served by the same page reads. Its query rows (token, head
+// of the kv head's G) number at most 16.
 //
 // Page walk: wave w takes pages first + w, first + w + 4, ... A page of one kv
-// head is 16 keys x 128 dims, contiguous (4 KiB in f16). Its load is four
-// dwordx4 instructions per lane, instruction i covering bytes [1024 i, 1024 i
-// + 1024) with lane l at offset 16 l: fully coalesced. So lane l = 16 r + c
-// holds dims [8c, 8c + 8) of keys 4i + r (i = 0..3), for K and for V.
-//   scores: an 8-dim partial dot per key (v_dot2_f32_f16 in the f16 path),
-//           summed over the 16 lanes of DPP row r - every lane of the row then
-//           holds the full score of its 4 keys;
-//   softmax: each DPP row keeps its own running max / sum over the keys it
-//           holds (no cross-row traffic in the loop);
+// head is 16 keys x 128 dims, contiguous (4 KiB in f16), read with four
+// dwordx4 loads per lane for K and four for V.
+//
+// f16 pages (MFMA): lane l = 16 g + c serves query column c, the run's row c
+// (columns past the last row repeat it).
+//   scores: S^T = K Q^T, four v_mfma_f32_16x16x32_f16 over 32 dims each. The A
+//           operand is K (lane l: key c, dims 32 s + 8 g .. + 7 of step s), the
+//           B operand q (lane l: row c, the same dims), so lane l ends with
+//           row c's raw scores of keys 4 g .. 4 g + 3.
+//   softmax: per column, the max over the 16 keys (its four lane groups meet
+//           through v_permlane16_swap / v_permlane32_swap), then one
+//           exponential per score; the weights, rounded to f16, are already
+//           the B operand of the value products, and each lane keeps the sum
+//           of its own four (the groups' sums meet once, at the end).
+//   values: O^T += V^T P^T, eight v_mfma_f32_16x16x16_f16, one per dim tile
+//           t: lane l loads keys 4 g .. 4 g + 3, dims 8 c .. 8 c + 7 of V
+//           (each load instruction reads four whole 256-byte key rows), and
+//           two v_perm per tile give it the A operand (dim 8 c + t of its four
+//           keys). Lane l accumulates row c's dims 32 g .. 32 g + 31.
+// f32 pages (VALU): lane l = 16 r + c holds dims [8c, 8c + 8) of keys 4i + r
+// (i = 0..3), for K and for V, and computes every row itself:
+//   scores: an 8-dim partial dot per key, reduced over the 16 lanes of DPP row
+//           r so that quad q of the row holds key q's score;
+//   softmax: each DPP row keeps its own running max / sum over its keys;
 //   values: each lane accumulates its 8 dims over its 4 keys.
 // Latency: a work-group's first page loads depend on one descriptor load only
 // (the descriptor carries the first block ids), the split's other block ids
 // arrive in one vector load next to them, and each wave loads the next page's
 // keys while it computes the current page's values, and the next page's values
 // while it computes the next page's scores.
-// At the end: rows merge through two lane exchanges, waves through LDS, and
-// splits either in the separate merge kernel or, with merge counters, in the
-// last work-group of the (run, kv head) to finish - all in one fixed order.
+// At the end: lanes merge (f32: two lane exchanges; f16: the row sums over
+// the lane groups), waves through LDS, and splits either in the separate merge
+// kernel or, with merge counters, in the last work-group of the (run, kv head)
+// to finish - all in one fixed order.
 //
 // Fused form (decode steps): the work-group computes its rows' q from qkv
 // (QK-RMSNorm + RoPE, the append kernel's arithmetic), and the K/V of the
@@ -39,12 +57,17 @@
 // reads those slots in this launch, so nothing waits for another work-group.
 //
 // Exactness of runs: a query row's arithmetic is the same whether its token is
-// alone or in a run. Pages entirely below the run's lowest position take a
-// path with no masking at all; later pages mask per row with selects, so a key
-// past a row's position leaves that row's state bit-for-bit unchanged, and a
-// page with no visible key for a row is an exact no-op for it (correction
-// factor 1 exactly, zero weights). Hence verify of k + 1 tokens equals k + 1
-// single-token decode steps bit-exactly.
+// alone or in a run: each MFMA output element is its own row's dot product,
+// and every per-row step is done per column. Pages entirely below the run's
+// lowest position take a path with no masking at all; later pages set the
+// scores of keys past a row's position to -inf (weight 0, and the max ignores
+// them), which gives a fully visible page the same bits as the fast path and
+// makes a page with no visible key an exact no-op for that row (correction
+// factor 1 exactly, zero weights). On those pages the V slots past the run's
+// last position, which may hold anything (pool slots never written), are read
+// as 0, so a zero weight never meets an inf or NaN. Hence verify of k + 1
+// tokens equals k + 1 single-token decode steps bit-exactly (f16 pages written
+// by the append kernels are finite: it clamps them).
 #include <climits>
 #include <type_traits>
 
@@ -92,13 +115,15 @@ __device__ __forceinline__ T uniform_load(const T *p) {
 
 __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// One page of K and V as this lane holds it: 4 keys x 8 dims each.
+// One page of K and V as this lane holds it: 4 x 8 dims of K and of V (which
+// keys and dims depends on the path: see the top of the file).
 template <typename T>
 struct PageRegs;
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <>
-struct PageRegs<f16> {
-    uint4 k[4], v[4];
+struct PageRegs<f16> {  // V only: f16 pages stage K in LDS
+    u32x4 v[4];
 };
 
 template <>
@@ -118,27 +143,23 @@ struct PageRegs<float> {
 constexpr int kDescWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
 constexpr int kNonTemporal = 2;         // cache-policy bit nt of a gfx950 buffer load
 
-__device__ __forceinline__ uint4 load_desc(__amdgpu_buffer_rsrc_t d, uint32_t off) {
-    typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-    const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(d, off, 0, kNonTemporal);
-    return make_uint4(v.x, v.y, v.z, v.w);
+__device__ __forceinline__ u32x4 load_desc(__amdgpu_buffer_rsrc_t d, uint32_t off) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(d, off, 0, kNonTemporal));
 }
 
 // One half of a page of one kv head (its 16 keys, or its 16 values) into
-// regs[4]: four loads per lane, load i covering bytes [1024 i, 1024 i + 1024)
-// of the half (f16), lane l at offset 16 l.
+// regs[4]: four loads per lane, load i at byte lane_off + step * i of the half.
 template <typename T, typename R>
-__device__ __forceinline__ void load_half(R (&regs)[4], const T *base, uint32_t lane_off, bool live) {
-    constexpr uint32_t kStep = 512 * sizeof(T);        // bytes between a lane's four slices of the half
+__device__ __forceinline__ void load_half(R (&regs)[4], const T *base, uint32_t lane_off, uint32_t step, bool live) {
     constexpr int kBytes = kPage * kHeadDim * sizeof(T);  // one half-page of one kv head
     const __amdgpu_buffer_rsrc_t d = __builtin_amdgcn_make_buffer_rsrc(const_cast<T *>(base), 0, live ? kBytes : 0,
                                                                        kDescWord3);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if constexpr (sizeof(T) == 2) {
-            regs[i] = load_desc(d, lane_off + kStep * i);
+            regs[i] = load_desc(d, lane_off + step * i);
         } else {
-            const uint4 x = load_desc(d, lane_off + kStep * i), y = load_desc(d, lane_off + kStep * i + 16);
+            const u32x4 x = load_desc(d, lane_off + step * i), y = load_desc(d, lane_off + step * i + 16);
             regs[i][0] = make_float4(__uint_as_float(x.x), __uint_as_float(x.y), __uint_as_float(x.z), __uint_as_float(x.w));
             regs[i][1] = make_float4(__uint_as_float(y.x), __uint_as_float(y.y), __uint_as_float(y.z), __uint_as_float(y.w));
         }
@@ -148,86 +169,42 @@ __device__ __forceinline__ void load_half(R (&regs)[4], const T *base, uint32_t 
 // Replaces key i of a page with the 8 dims this lane holds, read from LDS, in
 // the lanes where `take` holds: the LDS rows are read by every lane (the
 // caller passes an in-range row) and kept by selects, with no divergent branch.
-__device__ __forceinline__ uint4 select4(bool take, const uint4 &a, const uint4 &b) {
-    return make_uint4(take ? a.x : b.x, take ? a.y : b.y, take ? a.z : b.z, take ? a.w : b.w);
-}
+__device__ __forceinline__ u32x4 select4(bool take, const u32x4 &a, const u32x4 &b) { return take ? a : b; }
 __device__ __forceinline__ float4 select4(bool take, const float4 &a, const float4 &b) {
     return make_float4(take ? a.x : b.x, take ? a.y : b.y, take ? a.z : b.z, take ? a.w : b.w);
 }
 
-template <typename T>
-__device__ __forceinline__ void put_key(PageRegs<T> &pr, int i, bool take, const T *k8, const T *v8) {
-    if constexpr (sizeof(T) == 2) {
-        pr.k[i] = select4(take, *reinterpret_cast<const uint4 *>(k8), pr.k[i]);
-        pr.v[i] = select4(take, *reinterpret_cast<const uint4 *>(v8), pr.v[i]);
-    } else {
-        pr.k[i][0] = select4(take, *reinterpret_cast<const float4 *>(k8), pr.k[i][0]);
-        pr.k[i][1] = select4(take, *reinterpret_cast<const float4 *>(k8 + 4), pr.k[i][1]);
-        pr.v[i][0] = select4(take, *reinterpret_cast<const float4 *>(v8), pr.v[i][0]);
-        pr.v[i][1] = select4(take, *reinterpret_cast<const float4 *>(v8 + 4), pr.v[i][1]);
-    }
+// f32 pages: key i of a page replaced by the 8 dims this lane holds.
+__device__ __forceinline__ void put_key(PageRegs<float> &pr, int i, bool take, const float *k8, const float *v8) {
+    pr.k[i][0] = select4(take, *reinterpret_cast<const float4 *>(k8), pr.k[i][0]);
+    pr.k[i][1] = select4(take, *reinterpret_cast<const float4 *>(k8 + 4), pr.k[i][1]);
+    pr.v[i][0] = select4(take, *reinterpret_cast<const float4 *>(v8), pr.v[i][0]);
+    pr.v[i][1] = select4(take, *reinterpret_cast<const float4 *>(v8 + 4), pr.v[i][1]);
 }
 
-// A row's weights for the page's four keys (of this lane's DPP row): f32 for
-// f32 pages; for f16 pages f16 values packed in key pairs (0, 1), (2, 3), the
-// operands of the value products' v_dot2_f32_f16.
-template <typename T>
-struct Weights;
-template <>
-struct Weights<f16> {
-    f16x2 w[2];
-};
-template <>
-struct Weights<float> {
+// f32 pages: a row's weights for the page's four keys of this lane's DPP row,
+// and the query slice a lane needs (dims [8c, 8c + 8) of one row).
+struct Weights {
     float w[4];
 };
-
-// The query slice a lane needs: dims [8c, 8c + 8) of one row.
-template <typename T>
-struct QSlice;
-template <>
-struct QSlice<f16> {
-    f16x2 h[4];
-};
-template <>
-struct QSlice<float> {
+struct QSlice {
     float f[8];
 };
 
-__device__ __forceinline__ f16x2 as_f16x2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
-
-template <typename T>
-__device__ __forceinline__ void load_q(QSlice<T> &q, const T *qp) {
-    if constexpr (sizeof(T) == 2) {
-        const uint4 raw = *reinterpret_cast<const uint4 *>(qp);
-        q.h[0] = as_f16x2(raw.x);
-        q.h[1] = as_f16x2(raw.y);
-        q.h[2] = as_f16x2(raw.z);
-        q.h[3] = as_f16x2(raw.w);
-    } else {
-        const float4 a = *reinterpret_cast<const float4 *>(qp);
-        const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
-        q.f[0] = a.x;
-        q.f[1] = a.y;
-        q.f[2] = a.z;
-        q.f[3] = a.w;
-        q.f[4] = b.x;
-        q.f[5] = b.y;
-        q.f[6] = b.z;
-        q.f[7] = b.w;
-    }
+__device__ __forceinline__ void load_q(QSlice &q, const float *qp) {
+    const float4 a = *reinterpret_cast<const float4 *>(qp);
+    const float4 b = *reinterpret_cast<const float4 *>(qp + 4);
+    q.f[0] = a.x;
+    q.f[1] = a.y;
+    q.f[2] = a.z;
+    q.f[3] = a.w;
+    q.f[4] = b.x;
+    q.f[5] = b.y;
+    q.f[6] = b.z;
+    q.f[7] = b.w;
 }
 
-__device__ __forceinline__ float dot8(const QSlice<f16> &q, const uint4 &k) {
-    float s = 0.0f;
-    s = __builtin_amdgcn_fdot2(q.h[0], as_f16x2(k.x), s, false);
-    s = __builtin_amdgcn_fdot2(q.h[1], as_f16x2(k.y), s, false);
-    s = __builtin_amdgcn_fdot2(q.h[2], as_f16x2(k.z), s, false);
-    s = __builtin_amdgcn_fdot2(q.h[3], as_f16x2(k.w), s, false);
-    return s;
-}
-
-__device__ __forceinline__ float dot8(const QSlice<float> &q, const float4 (&k)[2]) {
+__device__ __forceinline__ float dot8(const QSlice &q, const float4 (&k)[2]) {
     float s = 0.0f;
     s = fmaf(q.f[0], k[0].x, s);
     s = fmaf(q.f[1], k[0].y, s);
@@ -238,18 +215,6 @@ __device__ __forceinline__ float dot8(const QSlice<float> &q, const float4 (&k)[
     s = fmaf(q.f[6], k[1].z, s);
     s = fmaf(q.f[7], k[1].w, s);
     return s;
-}
-
-__device__ __forceinline__ void unpack8(const uint4 &v, float (&out)[8]) {
-    const f16x2 a = as_f16x2(v.x), b = as_f16x2(v.y), c = as_f16x2(v.z), d = as_f16x2(v.w);
-    out[0] = static_cast<float>(a.x);
-    out[1] = static_cast<float>(a.y);
-    out[2] = static_cast<float>(b.x);
-    out[3] = static_cast<float>(b.y);
-    out[4] = static_cast<float>(c.x);
-    out[5] = static_cast<float>(c.y);
-    out[6] = static_cast<float>(d.x);
-    out[7] = static_cast<float>(d.y);
 }
 
 __device__ __forceinline__ void unpack8(const float4 (&v)[2], float (&out)[8]) {
@@ -305,6 +270,39 @@ template <int Q>
 __device__ __forceinline__ float quad_value(float v) {
     return dpp_mov<0x150 + 4 * Q>(v);
 }
+
+// f16 pages: max and sum over the four lane groups of a query column (lanes
+// c, c + 16, c + 32, c + 48). Groups 0 and 1, and 2 and 3, meet through
+// v_permlane16_swap, then the pairs through v_permlane32_swap. Both operations
+// are commutative, so every lane of the column gets the same bits; the sum is
+// (x0 + x1) + (x2 + x3).
+__device__ __forceinline__ float groups_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float groups_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// f16 pages: the A operand of the value products' dim tile TILE, dim
+// 8 c + TILE of this lane's keys 4 g .. 4 g + 3 (its four 8-dim slices of V,
+// one per key): two v_perm, each pairing one half of a word of two keys.
+template <int TILE>
+__device__ __forceinline__ f16x4 value_tile(const u32x4 (&v)[4]) {
+    constexpr uint32_t sel = (TILE & 1) ? 0x07060302u : 0x05040100u;  // high or low halves of (b, a)
+    constexpr int w = TILE / 2;
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 pair = {__builtin_amdgcn_perm(v[1][w], v[0][w], sel),   // keys 4g, 4g + 1
+                        __builtin_amdgcn_perm(v[3][w], v[2][w], sel)};  // keys 4g + 2, 4g + 3
+    return __builtin_bit_cast(f16x4, pair);
+}
+
+__device__ __forceinline__ f16x8 as_f16x8(const u32x4 &x) { return __builtin_bit_cast(f16x8, x); }
 
 // Merges this lane's (m, l, acc) with the lane `mask` away; both lanes end
 // with the same values.
@@ -454,12 +452,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         split = blockIdx.z;
     }
 
-    __shared__ float red_acc[ROWS][kWaves][D];
+    // f16 pages run on MFMA (MF); f32 pages on the VALU.
+    constexpr bool MF = sizeof(T) == 2;
+    // Each wave's region of LDS: its partial (ROWS x D floats) at the end of
+    // its page walk, and on f16 pages, before that, the staged keys of its
+    // current page (16 x 128 f16 = 4 KiB).
+    constexpr int RW = MF && ROWS * D < 1024 ? 1024 : ROWS * D;  // floats per wave
+    __shared__ __align__(16) float red_acc[kWaves * RW];
     __shared__ float red_m[ROWS][kWaves], red_l[ROWS][kWaves];
-    // With many rows (a verify run), q stays in LDS and each row's slice is read
-    // again per page: holding every row's q in registers as well would push the
-    // kernel past 256 VGPRs (one wave per SIMD).
-    constexpr bool Q_LDS = ROWS > 4;
+    auto red_row = [&](int row, int w) { return &red_acc[w * RW + row * D]; };
+    // q passes through LDS for MF (each lane then loads its column's operand),
+    // and for f32 pages with many rows (a verify run), where each row's slice is
+    // read again per page: holding every row's q in registers as well would
+    // push the kernel past 256 VGPRs (one wave per SIMD).
+    constexpr bool Q_LDS = MF || ROWS > 4;
     __shared__ __align__(16) T q_lds[(FUSED || Q_LDS) ? ROWS : 1][D];
     __shared__ __align__(16) T new_k[NEW][D], new_v[NEW][D];
     __shared__ int merge_here;
@@ -519,7 +525,36 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     const int n = first_page + wave <= last_page ? (last_page - first_page - wave) / kWaves + 1 : 0;
     auto page_of = [&](int j) { return first_page + wave + j * kWaves; };
     auto in_pool = [&](int blk) { return blk >= 0 && blk < p.num_blocks; };
-    const uint32_t lane_off = 8u * sizeof(T) * static_cast<uint32_t>(lane);
+    // Lane offsets and load steps within a half page. f32: lane l at 32 l,
+    // loads 2 KiB apart (keys 4 i + r, dims 8 c .. 8 c + 7), K and V alike.
+    // f16: V four whole key rows per load (keys 4 r + i, dims 8 c .. 8 c + 7).
+    const uint32_t k_off = 32u * lane, k_step = 2048u;
+    const uint32_t v_off = MF ? 1024u * r + 16u * c : 32u * lane, v_step = MF ? 256u : 2048u;
+    // f16 keys go through this wave's LDS region, 16-byte chunks swizzled so
+    // that both sides are conflict-free: LDS slot 16 k + (q ^ k) holds chunk q
+    // (dims 8 q .. 8 q + 7) of key k. Load i (buffer_load_dwordx4 ... lds,
+    // lane l to slot 64 i + l) then reads four whole key rows (keys 4 i + r,
+    // each row's 16 chunks in a permuted order), and the scores' A operand of
+    // step s (key c, chunk 4 s + r) is one ds_read_b128 whose 16 lanes of a
+    // given r hit 16 different slots modulo 16.
+    uint32_t *const kstage = reinterpret_cast<uint32_t *>(&red_acc[wave * RW]);
+    uint32_t k_dma[4], k_rd[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        k_dma[i] = 1024u * i + 256u * r + 16u * ((c ^ (4 * i + r)) & 15);
+        k_rd[i] = 64u * c + 4u * (((4 * i + r) ^ c) & 15);  // dwords
+    }
+    // Keys of one page of one kv head into kstage: four loads, each writing
+    // 1 KiB of LDS (lane l's 16 bytes at 16 l); a descriptor with no records
+    // (live = false) writes zeros.
+    auto stage_keys = [&](const T *base, bool live) {
+        const __amdgpu_buffer_rsrc_t d = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<T *>(base), 0, live ? kPage * D * static_cast<int>(sizeof(T)) : 0, kDescWord3);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d, (__attribute__((address_space(3))) void *)(kstage + 256 * i),
+                                                     16, k_dma[i], 0, 0, kNonTemporal);
+    };
     // The split's block ids, lane k holding page first_page + k: one vector
     // load, issued before any page load and read back per page with
     // v_readlane, so no page load waits on a scalar load of the table (under a
@@ -531,8 +566,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     auto fetch_block = [&](PageRegs<T> &pr, int j, int blk, bool keys, bool values) {
         const bool live = j < n && in_pool(blk);
         const int64_t off = static_cast<int64_t>(live ? blk : 0) * block_stride + head_off;
-        if (keys) load_half(pr.k, kbase + off, lane_off, live);
-        if (values) load_half(pr.v, vbase + off, lane_off, live);
+        if constexpr (MF) {
+            if (keys) stage_keys(kbase + off, live);
+        } else {
+            if (keys) load_half(pr.k, kbase + off, k_off, k_step, live);
+        }
+        if (values) load_half(pr.v, vbase + off, v_off, v_step, live);
     };
     auto block_of = [&](int j) { return block_at(min(page_of(j), last_page)); };
     auto fetch = [&](PageRegs<T> &pr, int j) { fetch_block(pr, j, block_of(j), true, true); };
@@ -550,10 +589,14 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         fetch_block(pr, 0, blk, true, true);
     };
 
-    QSlice<T> q[Q_LDS ? 1 : ROWS];
-    float m[ROWS], l[ROWS], acc[ROWS][8];
+    // f32 pages: every row's state in every lane (its q slice when q is not in
+    // LDS, running max, sum and 8 accumulated dims). f16 pages keep one
+    // column's state per lane, declared with their page walk below.
+    constexpr int FR = MF ? 1 : ROWS;
+    QSlice q[Q_LDS ? 1 : FR];
+    float m[FR], l[FR], acc[FR][8];
 #pragma unroll
-    for (int row = 0; row < ROWS; row++) {
+    for (int row = 0; row < FR; row++) {
         m[row] = kNoMax;
         l[row] = 0.0f;
 #pragma unroll
@@ -662,102 +705,202 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         }
     }
 
-    // One page: scores and online softmax for every row, then the values key by
-    // key (each key's 8 dims converted once, used by every row). Per row the
-    // operations and their order are: rescale by corr, then fma over keys 0..3.
-    // MASKED = false: every key of the page is visible to every row (the page
-    // lies below the run's lowest position). MASKED = true: per-row visibility,
-    // with selects, so a hidden key leaves a row's state bit-for-bit unchanged;
-    // for a fully visible page both forms compute the same bits. The two halves
-    // read only pr.k and only pr.v, so a wave can load the next page's keys
-    // between them.
-    const int quad = c >> 2;
-    const bool upper_half = c >= 8, odd_quad = (c & 4) != 0;
-    auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, Weights<T> (&pj)[ROWS], bool (&vis)[ROWS][4]) {
-        constexpr bool MASKED = decltype(masked_tag)::value;
-        const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
+    // The page walk: each wave holds one page in registers and loads the next
+    // page's keys once this page's scores are done, its values once this
+    // page's values are done, so half a page is in flight while the wave
+    // computes. With 16 waves per CU that keeps the memory system as busy as
+    // two whole pages per wave did, with shorter queues.
+    // The wave's fast pages come first (pages below min_pos / 16 hold no new key
+    // and only keys every row sees); they run through a loop with no masking.
+    // The rest (the run's positions, at most EMBER_MAX_RUN and consecutive, lie
+    // in at most two adjacent pages, of which a wave at stride 4 gets at most
+    // one) goes through the masked path.
+    const int fast_end = min_pos / kPage;
+    const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
+    using Fast = std::false_type;
+    using Masked = std::true_type;
+    __builtin_amdgcn_s_setprio(0);
+    if constexpr (MF) {
+        // Lane (r, c) serves query column c, the run's row src_row(c): its q
+        // operand (dims 32 i + 8 r .. + 7 for score step i), its position, and
+        // its running max m, its own keys' weight sum l and 32 accumulated dims
+        // (o[t][v]: dim 32 r + 8 v + t).
+        u32x4 qf[4];
 #pragma unroll
-        for (int row = 0; row < ROWS; row++) {
-            QSlice<T> qrow;
-            if constexpr (Q_LDS) load_q(qrow, &q_lds[src_row(row)][8 * c]);
-            else qrow = q[row];
-            float x[4];
+        for (int i = 0; i < 4; i++) qf[i] = *reinterpret_cast<const u32x4 *>(&q_lds[src_row(c)][32 * i + 8 * r]);
+        int my_pos = row_pos[0];
 #pragma unroll
-            for (int i = 0; i < 4; i++) x[i] = dot8(qrow, pr.k[i]);
-            // This lane's key (quad q of the DPP row: key 4 q + r of the page),
-            // its raw score; the softmax scale is applied in the exponent.
-            float sq = key_sums(x, upper_half, odd_quad);
+        for (int k = 1; k < ROWS; k++) my_pos = src_row(c) == k ? row_pos[k] : my_pos;
+        float mc = kNoMax, lc = 0.0f;
+        f32x4 o[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) o[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+        // One page: the scores and the online softmax (which rescales o), then
+        // the value products with the page's weights. MASKED = false: every key
+        // is visible to every row (the page lies below the run's lowest
+        // position). MASKED = true: a key past the column's position scores
+        // -inf, so it weighs 0 and leaves the max alone; for a fully visible
+        // page both forms compute the same bits. The two halves read only pr.k
+        // and only pr.v, so a wave can load the next page's keys between them.
+        // The staged keys as the scores' A operand: key c, dims 32 i + 8 r .. + 7.
+        auto read_keys = [&](u32x4 (&kf)[4]) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) kf[i] = *reinterpret_cast<const u32x4 *>(kstage + k_rd[i]);
+        };
+        auto scores = [&](const u32x4 (&kf)[4], int page, auto masked_tag) {
+            constexpr bool MASKED = decltype(masked_tag)::value;
+            // s[v]: the raw score of key 4 r + v against row src_row(c); the
+            // softmax scale is applied in the exponent.
+            f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < 4; i++) s = __builtin_amdgcn_mfma_f32_16x16x32_f16(as_f16x8(kf[i]), as_f16x8(qf[i]), s, 0, 0, 0);
             if constexpr (MASKED) {
+                const int key0 = page * kPage + 4 * r;
 #pragma unroll
-                for (int i = 0; i < 4; i++) vis[row][i] = key0 + 4 * i <= row_pos[row];
-                if (key0 + 4 * quad > row_pos[row]) sq = -INFINITY;
+                for (int v = 0; v < 4; v++) s[v] = key0 + v > my_pos ? -INFINITY : s[v];
             }
-            // The running max m is in scaled units: round(scale * max s) is the
+            // The running max is in scaled units: round(scale * max s) is the
             // max of the rounded scaled scores (scale > 0, rounding monotonic).
-            // m starts at kNoMax, not -inf, so mn is always finite: no select
-            // guards the subtraction, and corr is 2^0 = 1 exactly when the max
-            // stays. One exponential per lane: its own key's weight.
-            const float mn = fmaxf(m[row], quads_max(sq) * p.scale_log2);
-            float pq = exp2_hw(__builtin_fmaf(sq, p.scale_log2, -mn));  // 2^-inf = 0 for a hidden key
-            // f16 pages: the weight rounded to f16 (to nearest), for the value
-            // products on key pairs (v_dot2_f32_f16) and the row sum alike, so
-            // numerator and denominator use the same weights.
-            if constexpr (sizeof(T) == 2) {
-                pq = static_cast<float>(static_cast<_Float16>(pq));
-                pj[row].w[0] = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(quad_value<0>(pq), quad_value<1>(pq)));
-                pj[row].w[1] = __builtin_bit_cast(f16x2, __builtin_amdgcn_cvt_pkrtz(quad_value<2>(pq), quad_value<3>(pq)));
-            } else {
+            // m starts at kNoMax, not -inf, so mn is always finite, and corr is
+            // 2^0 = 1 exactly when the max stays. The weights are rounded to
+            // f16 (to nearest), the value products' operand; the sum takes the
+            // same rounded weights, so numerator and denominator agree.
+            const float mn = fmaxf(mc, groups_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]))) * p.scale_log2);
+            f16x4 w;
+#pragma unroll
+            for (int v = 0; v < 4; v++) w[v] = static_cast<f16>(exp2_hw(__builtin_fmaf(s[v], p.scale_log2, -mn)));
+            const float corr = exp2_hw(mc - mn);
+            const f16x2 ones = {static_cast<f16>(1.0f), static_cast<f16>(1.0f)};
+            lc = __builtin_amdgcn_fdot2(w.zw, ones, __builtin_amdgcn_fdot2(w.xy, ones, lc * corr, false), false);
+#pragma unroll
+            for (int t = 0; t < 8; t++) o[t] = o[t] * corr;
+            mc = mn;
+            return w;
+        };
+        auto values = [&](const PageRegs<T> &pr, f16x4 w) {
+            o[0] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<0>(pr.v), w, o[0], 0, 0, 0);
+            o[1] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<1>(pr.v), w, o[1], 0, 0, 0);
+            o[2] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<2>(pr.v), w, o[2], 0, 0, 0);
+            o[3] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<3>(pr.v), w, o[3], 0, 0, 0);
+            o[4] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<4>(pr.v), w, o[4], 0, 0, 0);
+            o[5] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<5>(pr.v), w, o[5], 0, 0, 0);
+            o[6] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<6>(pr.v), w, o[6], 0, 0, 0);
+            o[7] = __builtin_amdgcn_mfma_f32_16x16x16f16(value_tile<7>(pr.v), w, o[7], 0, 0, 0);
+        };
+        // A page of the masked part: the fused form first puts this launch's
+        // new keys into the page they land in (in place: the registers are
+        // reloaded after use anyway); then V slots past the run's last
+        // position read as 0.
+        auto consume = [&](PageRegs<T> &pr, int page) {
+            u32x4 kf[4];
+            read_keys(kf);
+            if constexpr (FUSED) {
+                if (page * kPage <= max_pos && (page + 1) * kPage > min_pos) {
+                    const int jk = page * kPage + c - min_pos;  // this lane's key; the run's positions are consecutive
+                    const int jkc = min(max(jk, 0), nq - 1);
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        kf[i] = select4(jk >= 0 && jk < nq, *reinterpret_cast<const u32x4 *>(&new_k[jkc][32 * i + 8 * r]), kf[i]);
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        const int jv = page * kPage + 4 * r + i - min_pos;  // this lane's value key i
+                        const int jvc = min(max(jv, 0), nq - 1);
+                        pr.v[i] = select4(jv >= 0 && jv < nq, *reinterpret_cast<const u32x4 *>(&new_v[jvc][8 * c]), pr.v[i]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) pr.v[i] = select4(page * kPage + 4 * r + i > max_pos, u32x4{0, 0, 0, 0}, pr.v[i]);
+            const f16x4 w = scores(kf, page, Masked{});
+            values(pr, w);
+        };
+
+        int j = 0;
+        for (; j < n_fast; j++) {
+            u32x4 kf[4];
+            read_keys(kf);
+            const f16x4 w = scores(kf, page_of(j), Fast{});
+            phase_break();
+            fetch_keys(A, j + 1);
+            phase_break();
+            values(A, w);
+            phase_break();
+            fetch_values(A, j + 1);
+            phase_break();
+        }
+        for (; j < n; j++) {
+            consume(A, page_of(j));
+            phase_break();
+            fetch(A, j + 1);
+            phase_break();
+        }
+
+        // The column's sum over its lane groups; its lanes write its partial.
+        lc = groups_sum(lc);
+        if (c < nrows) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                float *dst = red_row(c, wave) + 32 * r + 8 * v;
+                *reinterpret_cast<float4 *>(dst) = make_float4(o[0][v], o[1][v], o[2][v], o[3][v]);
+                *reinterpret_cast<float4 *>(dst + 4) = make_float4(o[4][v], o[5][v], o[6][v], o[7][v]);
+            }
+            if (r == 0) {
+                red_m[c][wave] = mc;
+                red_l[c][wave] = lc;
+            }
+        }
+    } else {
+        // One page: scores and online softmax for every row, then the values key by
+        // key (each key's 8 dims converted once, used by every row). Per row the
+        // operations and their order are: rescale by corr, then fma over keys 0..3.
+        // MASKED = false: every key of the page is visible to every row (the page
+        // lies below the run's lowest position). MASKED = true: per-row visibility,
+        // with selects, so a hidden key leaves a row's state bit-for-bit unchanged;
+        // for a fully visible page both forms compute the same bits. The two halves
+        // read only pr.k and only pr.v, so a wave can load the next page's keys
+        // between them.
+        const int quad = c >> 2;
+        const bool upper_half = c >= 8, odd_quad = (c & 4) != 0;
+        auto scores = [&](const PageRegs<T> &pr, int page, auto masked_tag, Weights (&pj)[ROWS], bool (&vis)[ROWS][4]) {
+            constexpr bool MASKED = decltype(masked_tag)::value;
+            const int key0 = page * kPage + r;  // position of this lane's key i = 0; key i is key0 + 4 i
+#pragma unroll
+            for (int row = 0; row < ROWS; row++) {
+                QSlice qrow;
+                if constexpr (Q_LDS) load_q(qrow, &q_lds[src_row(row)][8 * c]);
+                else qrow = q[row];
+                float x[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) x[i] = dot8(qrow, pr.k[i]);
+                // This lane's key (quad q of the DPP row: key 4 q + r of the page),
+                // its raw score; the softmax scale is applied in the exponent.
+                float sq = key_sums(x, upper_half, odd_quad);
+                if constexpr (MASKED) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) vis[row][i] = key0 + 4 * i <= row_pos[row];
+                    if (key0 + 4 * quad > row_pos[row]) sq = -INFINITY;
+                }
+                // The running max m is in scaled units: round(scale * max s) is the
+                // max of the rounded scaled scores (scale > 0, rounding monotonic).
+                // m starts at kNoMax, not -inf, so mn is always finite: no select
+                // guards the subtraction, and corr is 2^0 = 1 exactly when the max
+                // stays. One exponential per lane: its own key's weight.
+                const float mn = fmaxf(m[row], quads_max(sq) * p.scale_log2);
+                const float pq = exp2_hw(__builtin_fmaf(sq, p.scale_log2, -mn));  // 2^-inf = 0 for a hidden key
                 pj[row].w[0] = quad_value<0>(pq);
                 pj[row].w[1] = quad_value<1>(pq);
                 pj[row].w[2] = quad_value<2>(pq);
                 pj[row].w[3] = quad_value<3>(pq);
+                const float corr = exp2_hw(m[row] - mn);
+                l[row] = l[row] * corr + quads_sum(pq);
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
+                m[row] = mn;
             }
-            const float corr = exp2_hw(m[row] - mn);
-            l[row] = l[row] * corr + quads_sum(pq);
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[row][e] = acc[row][e] * corr;
-            m[row] = mn;
-        }
-    };
-    auto values = [&](const PageRegs<T> &pr, auto masked_tag, const Weights<T> (&pj)[ROWS], const bool (&vis)[ROWS][4]) {
-        constexpr bool MASKED = decltype(masked_tag)::value;
-        if constexpr (sizeof(T) == 2) {
-            // f16 pages: keys in pairs (0, 1), (2, 3), one v_dot2_f32_f16 per
-            // pair and dim: V regrouped once per page into (key a, key b)
-            // halves per dim, shared by every row. A masked pair with one key
-            // hidden takes the visible key alone (a single FMA), so no product
-            // ever meets a slot past a row's position, which may hold anything.
-#pragma unroll
-            for (int pair = 0; pair < 2; pair++) {
-                const uint4 va = pr.v[2 * pair], vb = pr.v[2 * pair + 1];
-                const uint32_t wa[4] = {va.x, va.y, va.z, va.w}, wb[4] = {vb.x, vb.y, vb.z, vb.w};
-                f16x2 vv[8];
-#pragma unroll
-                for (int w = 0; w < 4; w++) {
-                    vv[2 * w] = as_f16x2(__builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u));      // dim 2w of keys a, b
-                    vv[2 * w + 1] = as_f16x2(__builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u));  // dim 2w + 1
-                }
-#pragma unroll
-                for (int row = 0; row < ROWS; row++) {
-                    const f16x2 pp = pj[row].w[pair];
-                    if constexpr (!MASKED) {
-#pragma unroll
-                        for (int e = 0; e < 8; e++) acc[row][e] = __builtin_amdgcn_fdot2(pp, vv[e], acc[row][e], false);
-                    } else {
-                        const bool v0 = vis[row][2 * pair], v1 = vis[row][2 * pair + 1];
-#pragma unroll
-                        for (int e = 0; e < 8; e++) {
-                            const float both = __builtin_amdgcn_fdot2(pp, vv[e], acc[row][e], false);
-                            const float only0 =
-                                fmaf(static_cast<float>(pp.x), static_cast<float>(vv[e].x), acc[row][e]);
-                            const float only1 =
-                                fmaf(static_cast<float>(pp.y), static_cast<float>(vv[e].y), acc[row][e]);
-                            acc[row][e] = v0 ? (v1 ? both : only0) : (v1 ? only1 : acc[row][e]);
-                        }
-                    }
-                }
-            }
-        } else {
+        };
+        auto values = [&](const PageRegs<T> &pr, auto masked_tag, const Weights (&pj)[ROWS], const bool (&vis)[ROWS][4]) {
+            constexpr bool MASKED = decltype(masked_tag)::value;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 float vf[8];
@@ -774,75 +917,60 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
                     }
                 }
             }
-        }
-    };
-    using Fast = std::false_type;
-    using Masked = std::true_type;
-    // A page of the masked part: the fused form first puts this launch's new
-    // keys into the page they land in (in place: the registers are reloaded
-    // after use anyway).
-    auto consume = [&](PageRegs<T> &pr, int page) {
-        if constexpr (FUSED) {
-            if (page * kPage <= max_pos && (page + 1) * kPage > min_pos) {
+        };
+        // A page of the masked part: the fused form first puts this launch's new
+        // keys into the page they land in (in place: the registers are reloaded
+        // after use anyway).
+        auto consume = [&](PageRegs<T> &pr, int page) {
+            if constexpr (FUSED) {
+                if (page * kPage <= max_pos && (page + 1) * kPage > min_pos) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int j = page * kPage + r + 4 * i - min_pos;  // the run's positions are consecutive
-                    const int jc = min(max(j, 0), nq - 1);
-                    put_key(pr, i, j >= 0 && j < nq, &new_k[jc][8 * c], &new_v[jc][8 * c]);
+                    for (int i = 0; i < 4; i++) {
+                        const int j = page * kPage + r + 4 * i - min_pos;  // the run's positions are consecutive
+                        const int jc = min(max(j, 0), nq - 1);
+                        put_key(pr, i, j >= 0 && j < nq, &new_k[jc][8 * c], &new_v[jc][8 * c]);
+                    }
                 }
             }
+            Weights pj[ROWS];
+            bool vis[ROWS][4];
+            scores(pr, page, Masked{}, pj, vis);
+            values(pr, Masked{}, pj, vis);
+        };
+
+        int j = 0;
+        for (; j < n_fast; j++) {
+            Weights pj[ROWS];
+            bool vis[ROWS][4];
+            scores(A, page_of(j), Fast{}, pj, vis);
+            phase_break();
+            fetch_keys(A, j + 1);
+            phase_break();
+            values(A, Fast{}, pj, vis);
+            phase_break();
+            fetch_values(A, j + 1);
+            phase_break();
         }
-        Weights<T> pj[ROWS];
-        bool vis[ROWS][4];
-        scores(pr, page, Masked{}, pj, vis);
-        values(pr, Masked{}, pj, vis);
-    };
+        for (; j < n; j++) {
+            consume(A, page_of(j));
+            phase_break();
+            fetch(A, j + 1);
+            phase_break();
+        }
 
-    // The page walk: each wave holds one page in registers and loads the next
-    // page's keys once this page's scores are done, its values once this
-    // page's values are done, so half a page is in flight while the wave
-    // computes. With 16 waves per CU that keeps the memory system as busy as
-    // two whole pages per wave did, with shorter queues (and 32 fewer VGPRs).
-    // The wave's fast pages come first (pages below min_pos / 16 hold no new key
-    // and only keys every row sees); they run through a loop with no masking.
-    // The rest (the run's positions, at most EMBER_MAX_RUN and consecutive, lie
-    // in at most two adjacent pages, of which a wave at stride 4 gets at most
-    // one) goes through the masked path.
-    const int fast_end = min_pos / kPage;
-    const int n_fast = first_page + wave < fast_end ? min(n, (fast_end - 1 - first_page - wave) / kWaves + 1) : 0;
-    __builtin_amdgcn_s_setprio(0);
-    int j = 0;
-    for (; j < n_fast; j++) {
-        Weights<T> pj[ROWS];
-        bool vis[ROWS][4];
-        scores(A, page_of(j), Fast{}, pj, vis);
-        phase_break();
-        fetch_keys(A, j + 1);
-        phase_break();
-        values(A, Fast{}, pj, vis);
-        phase_break();
-        fetch_values(A, j + 1);
-        phase_break();
-    }
-    for (; j < n; j++) {
-        consume(A, page_of(j));
-        phase_break();
-        fetch(A, j + 1);
-        phase_break();
-    }
-
-    // Merge the four DPP rows of the wave (rows 0+1 and 2+3, then the pairs).
+        // Merge the four DPP rows of the wave (rows 0+1 and 2+3, then the pairs).
 #pragma unroll
-    for (int row = 0; row < ROWS; row++) {
-        if (row >= nrows) continue;
-        merge_lanes(m[row], l[row], acc[row], 16);
-        merge_lanes(m[row], l[row], acc[row], 32);
-        if (r == 0) {
+        for (int row = 0; row < ROWS; row++) {
+            if (row >= nrows) continue;
+            merge_lanes(m[row], l[row], acc[row], 16);
+            merge_lanes(m[row], l[row], acc[row], 32);
+            if (r == 0) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) red_acc[row][wave][8 * c + e] = acc[row][e];
-            if (c == 0) {
-                red_m[row][wave] = m[row];
-                red_l[row][wave] = l[row];
+                for (int e = 0; e < 8; e++) red_row(row, wave)[8 * c + e] = acc[row][e];
+                if (c == 0) {
+                    red_m[row][wave] = m[row];
+                    red_l[row][wave] = l[row];
+                }
             }
         }
     }
@@ -862,7 +990,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             const float mw = red_m[row][w];
             const float f = mw == -INFINITY ? 0.0f : exp2_hw(mw - M);
             L = L + red_l[row][w] * f;
-            O = O + red_acc[row][w][d] * f;
+            O = O + red_row(row, w)[d] * f;
         }
         const int li = first + row / G;
         const int head = kvh * G + row % G;

@@ -49,7 +49,6 @@ constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
 constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), halves: 18 dwords, rows 2 apart 4 banks apart
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 // How far a block's max may pass the running reference max (base 2) before
