@@ -836,6 +836,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
             phase_break();
         }
 
+        // The wave's last key fetch (past its last page: a descriptor with no
+        // records) still writes zeros into its stage, the LDS its partial goes
+        // to next, so every load of the wave completes first.
+        __builtin_amdgcn_s_waitcnt(0);
         // The column's sum over its lane groups; its lanes write its partial.
         lc = groups_sum(lc);
         if (c < nrows) {
