@@ -88,7 +88,7 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     ints_capacity_ = 4 * pad32(T) + 4 * pad32(T) + 3 * pad32(T / 16 + static_cast<size_t>(opt_.max_seqs)) +
                      static_cast<size_t>(opt_.max_seqs) * max_blocks_per_seq_ + pad32(2 * items) +
                      pad32(static_cast<size_t>(kDescInts) * items) + 64;
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kStages; i++) {
         dev_ints_[i] = device_alloc<int32_t>(ints_capacity_);
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming));
@@ -100,11 +100,12 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&cow_host_[i]), 2 * kCowPairs * sizeof(int32_t), 0));
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&cow_done_[i], hipEventDisableTiming));
     }
-    for (int i = 0; i < 2; i++) {  // every event starts out recorded, so the first plans wait on nothing pending
+    // every event starts out recorded, so the first plans wait on nothing pending
+    for (int i = 0; i < kStages; i++) {
         EMBER_HIP_CHECK(hipEventRecord(staged_[i], stream_));
         EMBER_HIP_CHECK(hipEventRecord(consumed_[i], stream_));
-        EMBER_HIP_CHECK(hipEventRecord(cow_done_[i], stream_));
     }
+    for (int i = 0; i < 2; i++) EMBER_HIP_CHECK(hipEventRecord(cow_done_[i], stream_));
     EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
 }
 
@@ -118,11 +119,13 @@ HipPagedKv::~HipPagedKv() {
     }
     for (const Timing *t : {&decode_timing_, &prefill_timing_})
         for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < kStages; i++) {
         if (staged_[i]) (void)hipEventDestroy(staged_[i]);
         if (consumed_[i]) (void)hipEventDestroy(consumed_[i]);
         if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
         if (dev_ints_[i]) (void)hipFree(dev_ints_[i]);
+    }
+    for (int i = 0; i < 2; i++) {
         if (cow_done_[i]) (void)hipEventDestroy(cow_done_[i]);
         if (cow_host_[i]) (void)hipHostFree(cow_host_[i]);
         if (cow_dev_[i]) (void)hipFree(cow_dev_[i]);
@@ -276,9 +279,9 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.
     // Everything enqueued on stream_ so far reads the previous plan's buffer;
-    // that buffer is reused two plans from now, after this event.
+    // that buffer is reused kStages plans from now, after this event.
     EMBER_HIP_CHECK(hipEventRecord(consumed_[stage_], stream_));
-    stage_ ^= 1;
+    stage_ = (stage_ + 1) % kStages;
     EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));  // its staging buffer is free again
     int32_t *hp = host_ints_[stage_];
     int32_t *dp = dev_ints_[stage_];
@@ -306,9 +309,9 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     EMBER_CHECK(b.logit_rows.size() <= static_cast<size_t>(T), "{} logit rows for {} tokens", b.logit_rows.size(), T);
     put(b.logit_rows.data(), b.logit_rows.size());
     EMBER_CHECK(off <= ints_capacity_, "internal: step buffer too small ({} > {})", off, ints_capacity_);
-    // The copy waits for the kernels that last read this buffer (two plans ago),
-    // then runs beside stream_'s work. The host, not stream_, waits for it:
-    // the host is normally a step ahead, so the wait costs it little, while a
+    // The copy waits for the kernels that last read this buffer (kStages plans
+    // ago), then runs beside stream_'s work. The host, not stream_, waits for
+    // it: the host is normally steps ahead, so the wait costs it little, while a
     // cross-stream wait on stream_ idles the GPU for about 10 us per step.
     EMBER_HIP_CHECK(hipStreamWaitEvent(upload_stream_, consumed_[stage_], 0));
     EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, upload_stream_));
@@ -507,7 +510,7 @@ bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
     const int splits = (WB * kBlockSize + opt_.split_len - 1) / opt_.split_len;
     plan(p, splits);
 
-    const uint64_t key = (static_cast<uint64_t>(TB) << 33) | (static_cast<uint64_t>(WB) << 1) | static_cast<uint64_t>(stage_);
+    const uint64_t key = (static_cast<uint64_t>(TB) << 34) | (static_cast<uint64_t>(WB) << 2) | static_cast<uint64_t>(stage_);
     auto it = graphs_.find(key);
     auto same_io = [&](const std::vector<LayerIo> &kept) {
         for (size_t l = 0; l < io.size(); l++)

@@ -122,13 +122,16 @@ private:
     void *k_ = nullptr, *v_ = nullptr, *q_ = nullptr;
     float *inv_freq_ = nullptr, *part_acc_ = nullptr, *part_ml_ = nullptr;
     uint32_t *merge_counters_ = nullptr;  // [max_batch_tokens * n_kv], zero between launches
-    // A step's integers, double-buffered: plan() packs them into pinned staging
-    // and copies them up on upload_stream_, so the copy overlaps the previous
-    // step's kernels instead of sitting between the steps on stream_.
-    int32_t *dev_ints_[2] = {nullptr, nullptr};
-    int32_t *host_ints_[2] = {nullptr, nullptr};  // pinned staging, alternating with dev_ints_
-    hipEvent_t staged_[2] = {nullptr, nullptr};   // the upload into each buffer has run
-    hipEvent_t consumed_[2] = {nullptr, nullptr}; // the kernels that read each buffer have run
+    // A step's integers in a ring of kStages buffers: plan() packs them into
+    // pinned staging and copies them up on upload_stream_, so the copy overlaps
+    // earlier steps' kernels instead of sitting between the steps on stream_. A
+    // buffer is reused kStages plans later, so the host can run kStages - 1
+    // steps ahead of the GPU.
+    static constexpr int kStages = 3;
+    int32_t *dev_ints_[kStages] = {};
+    int32_t *host_ints_[kStages] = {};  // pinned staging, one per dev_ints_ buffer
+    hipEvent_t staged_[kStages] = {};   // the upload into each buffer has run
+    hipEvent_t consumed_[kStages] = {}; // the kernels that read each buffer have run
     hipStream_t upload_stream_ = nullptr;
     int stage_ = 0;
     // copy_blocks' pair lists, double-buffered: pinned staging, the device list
