@@ -48,6 +48,7 @@ constexpr int kThreadsFor = 512 * HG;  // two key groups of 4 waves per query he
 constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's partial: O (8), l, m
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
 constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), halves: 18 dwords, rows 2 apart 4 banks apart
+constexpr int kVAhead = 2;                        // V^T operand reads in flight ahead of their MFMAs
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
@@ -264,14 +265,26 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
             for (int i = 0; i < 8; i++) pa[i] = static_cast<f16>(exp2_fast(fmaf(sv[i], scale_log2, neg_ref)));
             l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
-#pragma unroll
-            for (int dt = 0; dt < 8; dt++) {
+            // The V^T operand of dim tile dt; reads run kVAhead tiles ahead of
+            // their MFMAs. Left to itself the scheduler issues each read next to
+            // its MFMA, one LDS round trip per tile; the scheduling barriers keep
+            // the reads ahead (3-4% of the launch at configs 3 and 4).
+            auto vread = [&](int dt) {
                 const f16 *vrow = &vl[(16 * dt + ql) * kVRow];
                 const int gs = g ^ (dt & 1);  // the staging swizzle: bit 4 of the dim is dt's low bit
                 const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * gs);
                 const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * gs);
-                const f16x8 vb = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o_acc[dt], 0, 0, 0);
+                return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            };
+            f16x8 vb[kVAhead];
+#pragma unroll
+            for (int i = 0; i < kVAhead; i++) vb[i] = vread(i);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int dt = 0; dt < 8; dt++) {
+                o_acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb[dt % kVAhead], o_acc[dt], 0, 0, 0);
+                if (dt + kVAhead < 8) vb[dt % kVAhead] = vread(dt + kVAhead);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
         if (kb + 2 < n_blocks) stage(buf ^ 1, nk, nv);
