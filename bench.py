@@ -123,7 +123,9 @@ class Workload:
             self.h = torch.randn((BATCH, HID), generator=g, device="cuda")
             self.xn = torch.empty((BATCH, HID), device="cuda", dtype=torch.float16)
             self.qkv_buf = torch.empty((BATCH, NQKV), device="cuda", dtype=torch.float16)
-        self.stream.synchronize()
+        ws_bytes = max(int(_lib.lib().ember_hip_gemv_workspace_bytes(BATCH, n, HID)) for n in (NQKV, HID))
+        self.gemv_ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")  # both GEMVs, one stream
+        torch.cuda.synchronize()  # the zero fill ran on torch's stream
         self.block_args = []
         for layer in range(N_LAYERS):
             n = _lib.NormArgs()
@@ -135,6 +137,8 @@ class Workload:
             go = _lib.GemvArgs()
             go.A, go.lda, go.W, go.M, go.N, go.K = self.out.data_ptr(), HID, self.w_o[layer].data_ptr(), BATCH, HID, HID
             go.C, go.ldc, go.epilogue = self.h.data_ptr(), HID, _lib.EPILOGUE_ADD_F32
+            for ga in (gq, go):
+                ga.workspace, ga.workspace_bytes = self.gemv_ws.data_ptr(), ws_bytes
             self.block_args.append((ctypes.byref(n), ctypes.byref(gq), ctypes.byref(go), n, gq, go,
                                     self.qn[layer].data_ptr(), self.kn[layer].data_ptr()))
         self.block_weight_bytes = N_LAYERS * (NQKV * HID * 2 + HID * HID * 2)
@@ -451,6 +455,9 @@ def run_linear(args) -> dict:
     xn = torch.empty((M, HID), device=dev, dtype=torch.float16)
     qkv = torch.empty((M, NQKV), device=dev, dtype=torch.float16)
     att = torch.randn((M, HID), generator=g, device=dev).half()
+    # One zeroed workspace for both projections (they never overlap): the o projection's 2048 features split K.
+    ws = max((K.gemv_workspace(M, n, HID, dev) for n in (NQKV, HID)),
+             key=lambda t: 0 if t is None else t.numel(), default=None)
     torch.cuda.synchronize()
     names = ["rmsnorm_rows", "gemv qkv (store_f16)", "gemv o (add_f32)"]
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in names]
@@ -458,8 +465,8 @@ def run_linear(args) -> dict:
 
     def layer(l, timed):
         ops = [lambda: K.rmsnorm_rows(h, norm_w[l], xn, 1e-6),
-               lambda: K.gemv(xn, w_qkv[l], qkv, 0),
-               lambda: K.gemv(att, w_o[l], h, 2)]
+               lambda: K.gemv(xn, w_qkv[l], qkv, 0, workspace=ws),
+               lambda: K.gemv(att, w_o[l], h, 2, workspace=ws)]
         for i, op in enumerate(ops):
             if timed:
                 ev[l][i][0].record()

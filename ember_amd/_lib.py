@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 4
+ABI_VERSION = 5
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
@@ -97,7 +97,7 @@ class LayerIo(ctypes.Structure):
 class GemvArgs(ctypes.Structure):
     _fields_ = [
         ("A", c_void_p), ("lda", c_int32), ("W", c_void_p), ("M", c_int32), ("N", c_int32), ("K", c_int32),
-        ("C", c_void_p), ("ldc", c_int32), ("epilogue", c_int32),
+        ("C", c_void_p), ("ldc", c_int32), ("epilogue", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_int64),
     ]
 
 
@@ -151,6 +151,7 @@ PROTOTYPES = {
     "ember_hip_prefill_attn": (c_int32, [POINTER(PrefillArgs), c_void_p]),
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
     "ember_hip_gemv": (c_int32, [POINTER(GemvArgs), c_void_p]),
+    "ember_hip_gemv_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
     "ember_hip_rmsnorm_rows": (c_int32, [POINTER(NormArgs), c_void_p]),
     "ember_hip_embed": (c_int32, [POINTER(EmbedArgs), c_void_p]),
     "ember_hip_sample": (c_int32, [POINTER(SampleArgs), c_void_p]),

@@ -223,7 +223,14 @@ int ember_hip_gemv(const EmberGemvArgs *a, void *stream) {
     if (!a->A || !a->W || !a->C) return set_error(EMBER_ERR_INVALID, "gemv: a required pointer is null");
     if (reinterpret_cast<uintptr_t>(a->A) % 16 != 0 || reinterpret_cast<uintptr_t>(a->W) % 16 != 0)
         return set_error(EMBER_ERR_INVALID, "gemv: A and W must be 16-byte aligned");
+    if (a->workspace_bytes < 0 || reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv: the workspace must be 16-byte aligned with a size >= 0");
     return hip_status(launch_gemv(*a, static_cast<hipStream_t>(stream)), "gemv");
+}
+
+int64_t ember_hip_gemv_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+    if (M < 1 || M > 64 || N < 1 || K < 32 || K % 32 != 0) return 0;
+    return gemv_workspace_bytes(M, N, K);
 }
 
 int ember_hip_embed(const EmberEmbedArgs *a, void *stream) {

@@ -325,6 +325,8 @@ private:
             g.C = static_cast<char *>(C) + static_cast<size_t>(m0) * ldc * out_elem;
             g.ldc = ldc;
             g.epilogue = ep;
+            g.workspace = gemv_ws_.get();
+            g.workspace_bytes = static_cast<int64_t>(gemv_ws_.bytes());
             check_abi(ember_hip_gemv(&g, stream_), "gemv");
         }
     }
@@ -473,7 +475,20 @@ private:
         dev_probs_ = DeviceMem(R * sizeof(float));
         HIPB_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_params_), R * sizeof(EmberSampleParams), 0));
         HIPB_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_), 2 * R * sizeof(int32_t), 0));
-        act_bytes_ = h_.bytes() + xn_.bytes() + qkv_.bytes() + att_.bytes() + act_.bytes() + logits_.bytes();
+        // One zeroed GEMV workspace, for the largest split among the model's projections at 64 tokens;
+        // the projections run one after another on stream_, so they share it.
+        int64_t ws = 0;
+        const int64_t shapes[][2] = {{static_cast<int64_t>(Q + 2 * KV), static_cast<int64_t>(H)},
+                                     {static_cast<int64_t>(H), static_cast<int64_t>(Q)},
+                                     {static_cast<int64_t>(2 * I), static_cast<int64_t>(H)},
+                                     {static_cast<int64_t>(H), static_cast<int64_t>(I)},
+                                     {static_cast<int64_t>(c.vocab_size), static_cast<int64_t>(H)}};
+        for (const auto &sh : shapes)
+            ws = std::max(ws, ember_hip_gemv_workspace_bytes(64, static_cast<int32_t>(sh[0]), static_cast<int32_t>(sh[1])));
+        gemv_ws_ = DeviceMem(static_cast<size_t>(ws));
+        HIPB_CHECK(hipMemset(gemv_ws_.get(), 0, gemv_ws_.bytes()));
+        act_bytes_ = h_.bytes() + xn_.bytes() + qkv_.bytes() + att_.bytes() + act_.bytes() + logits_.bytes() +
+                     gemv_ws_.bytes();
     }
 
     void create_kv() {
@@ -509,7 +524,7 @@ private:
     Linear lm_head_;
     const float *final_norm_ = nullptr;
     std::vector<LayerWeights> layers_;
-    DeviceMem h_, xn_, qkv_, att_, act_, logits_, captured_;
+    DeviceMem h_, xn_, qkv_, att_, act_, logits_, captured_, gemv_ws_;
     DeviceMem dev_params_, dev_tokens_, dev_queries_, dev_probs_;
     EmberSampleParams *host_params_ = nullptr;
     int32_t *host_ints_ = nullptr;

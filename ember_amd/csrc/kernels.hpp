@@ -39,6 +39,7 @@ int prefill_attn(const EmberPrefillArgs *a, hipStream_t stream, hipEvent_t start
 hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
 
 hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream);
+int64_t gemv_workspace_bytes(int M, int N, int K);  // 0: no K split for this shape
 
 hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream);
 

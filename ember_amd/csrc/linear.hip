@@ -18,6 +18,14 @@
 // activations as the B operand (lane l: token l % 16, the same k), so
 // D = W X^T holds C^T: lane l ends with token l % 16 and features 4 (l / 16)
 // + 0..3. The waves' partial sums meet in LDS and are added in wave order.
+//
+// A launch wants one work-group per CU at least: with few features (N / 16
+// below 256, e.g. the output projection's 2048), and a caller workspace, KS =
+// 2 or 4 work-groups share each 16 features, each taking a K slice (grid y).
+// Each stores its slice sum; the last to count in adds the KS sums in slice
+// order and applies the epilogue. KS depends on N and K only.
+#include <type_traits>
+
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -27,6 +35,21 @@ namespace {
 constexpr int kGemvWaves = 8;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kGemvUnroll = 8;  // k steps whose W loads are in flight together, per wave
+constexpr int kGemvTargetGroups = 256;  // work-groups a launch should reach: one per CU
+constexpr int kGemvMaxSplit = 4;
+
+// Split slices are written and read with device-scope relaxed atomics (sc1
+// global stores and loads on gfx950, coherent across the XCDs' L2s), under
+// the same protocol as the decode kernel's split merge: each work-group waits
+// for its slice stores (s_waitcnt vmcnt(0), then a barrier) before it counts
+// in, and the merging work-group loads the slices only after its count has
+// returned. So every slice counted before the last count is visible.
+__device__ __forceinline__ void put_slice(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_slice(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 __device__ __forceinline__ f16x8 load_w(const f16 *p) {
     return __builtin_nontemporal_load(reinterpret_cast<const f16x8 *>(p));  // W is read once per launch
@@ -34,52 +57,73 @@ __device__ __forceinline__ f16x8 load_w(const f16 *p) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-template <int MT, int EP>  // MT tiles of 16 tokens (M <= 16 MT); EP an EMBER_EPILOGUE_*
+// MT tiles of 16 tokens (M <= 16 MT); EP an EMBER_EPILOGUE_*; SPLIT: K split
+// over gridDim.y work-groups (a separate instance, so the unsplit one keeps
+// its constant-stride loads and no merge code).
+template <int MT, int EP, bool SPLIT>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restrict__ A, int lda,
                                                             const f16 *__restrict__ W, int M, int N, int K,
-                                                            void *__restrict__ C, int ldc) {
+                                                            void *__restrict__ C, int ldc,
+                                                            float *__restrict__ slices, uint32_t *__restrict__ counters) {
     __shared__ f32x4 red[kGemvWaves - 1][MT][kWave];
-    const int lane = static_cast<int>(threadIdx.x) % kWave, wave = static_cast<int>(threadIdx.x) / kWave;
+    __shared__ int merge_here;
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid % kWave, wave = tid / kWave;
     const int c = lane % 16, g = lane / 16;
-    const int n0 = static_cast<int>(blockIdx.x) * 16;
-    const f16 *w = W + static_cast<int64_t>(min(n0 + c, N - 1)) * K + 8 * g;  // rows past N repeat the last
+    const int fb = static_cast<int>(blockIdx.x), nfb = static_cast<int>(gridDim.x);
+    const int ks = SPLIT ? static_cast<int>(blockIdx.y) : 0, KS = SPLIT ? static_cast<int>(gridDim.y) : 1;
+    const int n0 = fb * 16;
+    const int k0 = ks * (K / KS);  // this work-group's K slice: K / KS, a multiple of 32
+    const f16 *w = W + static_cast<int64_t>(min(n0 + c, N - 1)) * K + k0 + 8 * g;  // rows past N repeat the last
     const f16 *x[MT];
     bool xok[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const int tok = 16 * mt + c;
         xok[mt] = tok < M;
-        x[mt] = A + static_cast<int64_t>(min(tok, M - 1)) * lda + 8 * g;
+        x[mt] = A + static_cast<int64_t>(min(tok, M - 1)) * lda + k0 + 8 * g;
     }
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Wave w takes k steps w, w + 8, ...; kGemvUnroll of them per round, every
-    // W load of the round issued before its MFMAs.
-    const int steps = K / 32;
-    int s = wave;
-    for (; s + (kGemvUnroll - 1) * kGemvWaves < steps; s += kGemvUnroll * kGemvWaves) {
-        f16x8 wv[kGemvUnroll], xv[kGemvUnroll][MT];
+    // Up to kGemvUnroll k steps per round, every W load of the round issued
+    // before its MFMAs.
+    auto round = [&](auto unroll, int s0, int stride) {
+        constexpr int U = decltype(unroll)::value;
+        f16x8 wv[U], xv[U][MT];
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; u++) wv[u] = load_w(w + 32 * (s + u * kGemvWaves));
+        for (int u = 0; u < U; u++) wv[u] = load_w(w + 32 * (s0 + u * stride));
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; u++)
+        for (int u = 0; u < U; u++)
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
-                xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s + u * kGemvWaves)) : f16x8{};
+                xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s0 + u * stride)) : f16x8{};
 #pragma unroll
-        for (int u = 0; u < kGemvUnroll; u++)
+        for (int u = 0; u < U; u++)
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
-    }
-    for (; s < steps; s += kGemvWaves) {
-        const f16x8 wv = load_w(w + 32 * s);
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            const f16x8 xv = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * s) : f16x8{};
-            acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv, xv, acc[mt], 0, 0, 0);
+    };
+    using Full = std::integral_constant<int, kGemvUnroll>;
+    using Half = std::integral_constant<int, kGemvUnroll / 2>;
+    using One = std::integral_constant<int, 1>;
+    const int steps = K / KS / 32;
+    if constexpr (SPLIT) {
+        // A slice has few steps per wave: each wave takes a contiguous run, so
+        // its consecutive loads read whole 128-byte lines of W.
+        int s = wave * steps / kGemvWaves;
+        const int end = (wave + 1) * steps / kGemvWaves;
+        for (; s + kGemvUnroll <= end; s += kGemvUnroll) round(Full{}, s, 1);
+        if (s + kGemvUnroll / 2 <= end) {
+            round(Half{}, s, 1);
+            s += kGemvUnroll / 2;
         }
+        for (; s < end; s++) round(One{}, s, 1);
+    } else {
+        // Wave w takes k steps w, w + 8, ...
+        int s = wave;
+        for (; s + (kGemvUnroll - 1) * kGemvWaves < steps; s += kGemvUnroll * kGemvWaves) round(Full{}, s, kGemvWaves);
+        for (; s < steps; s += kGemvWaves) round(One{}, s, kGemvWaves);
     }
 
     if (wave > 0) {
@@ -87,11 +131,51 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
         for (int mt = 0; mt < MT; mt++) red[wave - 1][mt][lane] = acc[mt];
     }
     __syncthreads();
-    if (wave != 0) return;
+    if (wave == 0) {
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+        for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int v = 0; v < kGemvWaves - 1; v++) acc[mt] = acc[mt] + red[v][mt][lane];
+            for (int v = 0; v < kGemvWaves - 1; v++) acc[mt] = acc[mt] + red[v][mt][lane];
+    }
+    if constexpr (SPLIT) {
+        // Slice sums: [ks][fb][mt][element i][lane], one 256-byte row per store.
+        auto slice = [&](int q, int mt) { return slices + ((static_cast<int64_t>(q) * nfb + fb) * MT + mt) * 256 + lane; };
+        if (wave == 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) put_slice(slice(ks, mt) + 64 * i, acc[mt][i]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t before = __hip_atomic_fetch_add(counters + fb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            merge_here = before + 1 == static_cast<uint32_t>(KS);
+            if (merge_here) __hip_atomic_store(counters + fb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!merge_here || wave != 0) return;
+        // The slices in slice order, this work-group's own included, so the sum
+        // does not depend on which work-group merges.
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            float part[kGemvMaxSplit][4];
+#pragma unroll
+            for (int q = 0; q < kGemvMaxSplit; q++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) part[q][i] = q < KS ? get_slice(slice(q, mt) + 64 * i) : 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float t = part[0][i];
+#pragma unroll
+                for (int q = 1; q < kGemvMaxSplit; q++)
+                    if (q < KS) t += part[q][i];
+                acc[mt][i] = t;
+            }
+        }
+    } else if (wave != 0) {
+        return;
+    }
 
     // acc[mt][i] = C[token 16 mt + c][feature n0 + 4 g + i].
 #pragma unroll
@@ -124,19 +208,53 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     }
 }
 
+// Work-groups per 16 features: doubled while the launch has fewer than
+// kGemvTargetGroups and each slice keeps at least one 32-wide k step per wave.
+int gemv_split(int N, int K) {
+    const int nfb = (N + 15) / 16;
+    int ks = 1;
+    while (ks < kGemvMaxSplit && nfb * ks < kGemvTargetGroups && K % (2 * ks * 32) == 0 &&
+           K / (2 * ks) >= 32 * kGemvWaves)
+        ks *= 2;
+    return ks;
+}
+
+// Workspace of a split launch: the merge counters (one per 16 features,
+// padded to 256 bytes), then the slice sums.
+int64_t gemv_workspace(int M, int N, int K) {
+    const int ks = gemv_split(N, K);
+    if (ks == 1) return 0;
+    const int64_t nfb = (N + 15) / 16, mt = (M + 15) / 16;
+    return (nfb * 4 + 255) / 256 * 256 + ks * nfb * mt * 256 * 4;
+}
+
 template <int EP>
 hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
-    const dim3 grid(static_cast<unsigned>((a.N + 15) / 16));
+    const int64_t need = gemv_workspace(a.M, a.N, a.K);
+    const bool split = need > 0 && a.workspace && a.workspace_bytes >= need;
+    const int nfb = (a.N + 15) / 16;
+    const dim3 grid(static_cast<unsigned>(nfb), static_cast<unsigned>(split ? gemv_split(a.N, a.K) : 1));
+    uint32_t *counters = split ? static_cast<uint32_t *>(a.workspace) : nullptr;
+    float *slices = split ? reinterpret_cast<float *>(static_cast<char *>(a.workspace) + (nfb * 4 + 255) / 256 * 256)
+                          : nullptr;
     const f16 *A = static_cast<const f16 *>(a.A);
     const f16 *W = static_cast<const f16 *>(a.W);
-    switch ((a.M + 15) / 16) {
-        case 1: hipLaunchKernelGGL((gemv_kernel<1, EP>), grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc); break;
-        case 2: hipLaunchKernelGGL((gemv_kernel<2, EP>), grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc); break;
-        case 3: hipLaunchKernelGGL((gemv_kernel<3, EP>), grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc); break;
-        case 4: hipLaunchKernelGGL((gemv_kernel<4, EP>), grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc); break;
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc, slices,
+                           counters);
+        return hipGetLastError();
+    };
+    switch ((a.M + 15) / 16 + (split ? 4 : 0)) {
+        case 1: return go(gemv_kernel<1, EP, false>);
+        case 2: return go(gemv_kernel<2, EP, false>);
+        case 3: return go(gemv_kernel<3, EP, false>);
+        case 4: return go(gemv_kernel<4, EP, false>);
+        case 5: return go(gemv_kernel<1, EP, true>);
+        case 6: return go(gemv_kernel<2, EP, true>);
+        case 7: return go(gemv_kernel<3, EP, true>);
+        case 8: return go(gemv_kernel<4, EP, true>);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
 }
 
 constexpr int kNormThreads = 256;
@@ -165,6 +283,8 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float 
 }
 
 }  // namespace
+
+int64_t gemv_workspace_bytes(int M, int N, int K) { return gemv_workspace(M, N, K); }
 
 hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream) {
     switch (a.epilogue) {

@@ -350,11 +350,19 @@ def copy_pages(k_pool, v_pool, src, dst, *, n_layers, layer_stride, n_kv, num_bl
     return (sd, dd)
 
 
-def gemv(a, w, c, epilogue: int, stream=None):
+def gemv_workspace(M: int, N: int, K: int, device="cuda"):
+    """A zeroed workspace for gemv at this shape (uint8 tensor), or None when the shape does not split K."""
+    n = int(_lib.lib().ember_hip_gemv_workspace_bytes(M, N, K))
+    return torch.zeros(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def gemv(a, w, c, epilogue: int, stream=None, workspace=None):
     """C = A . W^T for decode-sized batches (≙ cuda::gemm with GemmKernel::gemv_tc, k_gemm.cu:302-425).
 
     a: f16 [M, K] (M <= 64, K a multiple of 32); w: f16 [N, K]; c: per epilogue, f16 [M, N] (store_f16),
     f32 [M, N] (store_f32; add_f32 adds into it) or f16 [M, N / 2] (silu_mul, W rows interleaving gate and up).
+    workspace: None, or a zeroed device tensor of at least gemv_workspace's size, which lets a shape with few
+    output features split K over more work-groups (not shared by launches that overlap in time).
     """
     if a.dtype != torch.float16 or w.dtype != torch.float16 or a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
         raise EmberError("gemv: a [M, K] and w [N, K] must be f16 with the same K")
@@ -367,6 +375,8 @@ def gemv(a, w, c, epilogue: int, stream=None):
     g = _lib.GemvArgs()
     g.A, g.lda, g.W, g.M, g.N, g.K = _dev(a, "a"), K, _dev(w, "w"), M, N, K
     g.C, g.ldc, g.epilogue = _dev(c, "c"), cols, epilogue
+    if workspace is not None:
+        g.workspace, g.workspace_bytes = _dev(workspace, "workspace"), workspace.numel() * workspace.element_size()
     check(_lib.lib().ember_hip_gemv(g, _stream_handle(stream)), "gemv")
 
 

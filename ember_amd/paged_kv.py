@@ -119,10 +119,15 @@ class PagedKv:
         T = h.shape[0]
         if T > 64:
             raise EmberError("attention_block: at most 64 tokens (decode-sized GEMV)")
+        # One workspace, sized for 64 tokens, serves both projections: they run one after the other on the stream.
+        need = max(int(L.lib().ember_hip_gemv_workspace_bytes(64, w.shape[0], w.shape[1])) for w in (w_qkv, w_o))
+        if need > 0 and (getattr(self, "_gemv_ws", None) is None or self._gemv_ws.numel() < need):
+            self._gemv_ws = torch.zeros(need, dtype=torch.uint8, device=h.device)
+        ws = getattr(self, "_gemv_ws", None) if need > 0 else None
         K.rmsnorm_rows(h, in_norm, xn, self.cfg.rms_eps, stream=self.stream)
-        K.gemv(xn, w_qkv, qkv, L.EPILOGUE_STORE_F16, stream=self.stream)
+        K.gemv(xn, w_qkv, qkv, L.EPILOGUE_STORE_F16, stream=self.stream, workspace=ws)
         self.layer(layer, qkv, att, q_norm, k_norm, bias)
-        K.gemv(att.view(T, -1), w_o, h, L.EPILOGUE_ADD_F32, stream=self.stream)
+        K.gemv(att.view(T, -1), w_o, h, L.EPILOGUE_ADD_F32, stream=self.stream, workspace=ws)
 
     def copy_blocks(self, src, dst) -> None:
         s, d = _arr(src), _arr(dst)

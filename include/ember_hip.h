@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 4
+#define EMBER_ABI_VERSION 5
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
@@ -230,13 +230,29 @@ typedef struct EmberGemvArgs {
     void *C;                      /* [M, ldc], f16 or f32 by epilogue */
     int32_t ldc;
     int32_t epilogue;             /* EMBER_EPILOGUE_* */
+    /* Optional scratch for splitting K over work-groups when N alone gives
+     * too few of them (no counterpart in the reference; its gemv_tc does not
+     * split). NULL, or fewer bytes than ember_hip_gemv_workspace_bytes(M, N,
+     * K), means no split. Zero-filled by the caller once after allocation;
+     * every launch leaves it reusable. Launches that overlap in time must
+     * not share one. */
+    void *workspace;
+    int64_t workspace_bytes;
 } EmberGemvArgs;
 
 /* C[M, N] = A[M, K] . W[N, K]^T, f16 in, f32 accumulation, then the epilogue
  * (silu_mul: N even, C has N / 2 columns). MFMA tiles of 16 features x 16
- * tokens, 8 waves splitting K. Replaces cuda::gemm with GemmKernel::gemv_tc
- * (kernels.cuh:40-41; k_gemm.cu:302-425, :462-485). */
+ * tokens, 8 waves splitting K; with a workspace and few features, 2 or 4
+ * work-groups per 16 features each take a K slice, and the last to finish
+ * adds the slices in slice order (deterministic; the split depends on N and
+ * K only, so a token's result does not depend on the batch). Replaces
+ * cuda::gemm with GemmKernel::gemv_tc (kernels.cuh:40-41; k_gemm.cu:302-425,
+ * :462-485). */
 int ember_hip_gemv(const EmberGemvArgs *args, void *stream);
+
+/* Bytes of workspace ember_hip_gemv uses for this shape (0: it would not
+ * split). No counterpart in the reference. */
+int64_t ember_hip_gemv_workspace_bytes(int32_t M, int32_t N, int32_t K);
 
 /* The arguments of cuda::rmsnorm_rows (kernels.cuh:70-72). */
 typedef struct EmberNormArgs {

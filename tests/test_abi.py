@@ -68,6 +68,12 @@ def test_launchers_reject_bad_arguments_without_a_gpu():
     assert "even N" in _lib.last_error()
     g.N, g.epilogue = 16, 0  # null pointers
     assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    g.A, g.W, g.C = 16, 16, 16  # (never dereferenced: the workspace check comes first)
+    g.workspace, g.workspace_bytes = 16, -1
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    assert "workspace" in _lib.last_error()
+    g.workspace, g.workspace_bytes = 8, 64  # misaligned
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
     assert lib.ember_hip_rmsnorm_rows(None, None) == _lib.ERR_INVALID
     n = _lib.NormArgs()
     n.R, n.hidden = 2, 0
@@ -84,3 +90,16 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(ImportError):
         _lib.lib()
+
+
+def test_gemv_workspace_sizes():
+    """The K split is taken only when N / 16 gives fewer than 256 work-groups, in powers of two up to 4, with at
+    least 256 of K per slice; its workspace is the 16-feature counters (padded to 256 bytes) plus the slice sums."""
+    lib = _lib.lib()
+    size = lib.ember_hip_gemv_workspace_bytes
+    assert size(32, 4096, 2048) == 0  # 256 work-groups already: no split
+    assert size(32, 2048, 2048) == 512 + 2 * 128 * 2 * 1024  # the o projection: 2 slices of 1024
+    assert size(64, 1024, 2048) == 256 + 4 * 64 * 4 * 1024  # 4 slices of 512
+    assert size(1, 256, 512) == 256 + 2 * 16 * 1 * 1024  # 512 / 4 = 128 would leave a wave without a k step
+    assert size(3, 130, 256) == 0  # K too short to split
+    assert size(65, 2048, 2048) == 0 and size(32, 2048, 40) == 0  # invalid shapes: no workspace

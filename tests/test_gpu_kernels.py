@@ -495,9 +495,11 @@ def _linear_err(got, want):
 @pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (8, 512, 1024), (13, 200, 128), (31, 384, 512),
                                    (64, 256, 1024), (32, 4096, 2048), (32, 2048, 2048), (17, 48, 32)])
 @pytest.mark.parametrize("ep", [0, 1, 2, 3])
-def test_gemv_matches_oracle(device, M, N, KD, ep):
+@pytest.mark.parametrize("split", [False, True])
+def test_gemv_matches_oracle(device, M, N, KD, ep, split):
     """Every epilogue on the reference test's decode-sized shapes (K a multiple of 32) and the Qwen3-1.7B
-    projections; ragged M and N exercise the clamped rows. Bound 2e-3 as in the reference's test."""
+    projections; ragged M and N exercise the clamped rows. With a workspace, the shapes with few features take
+    the K split. Bound 2e-3 as in the reference's test."""
     from ember_amd import _lib
     rng = np.random.default_rng(M * 7919 + N * 31 + KD + ep)
     a = (rng.standard_normal((M, KD))).astype(np.float16)
@@ -507,12 +509,43 @@ def test_gemv_matches_oracle(device, M, N, KD, ep):
     c0 = np.ones((M, cols), np.float32)
     c = torch.from_numpy(c0).to(device) if f32 else torch.full((M, cols), float("nan"), dtype=torch.float16,
                                                                  device=device)
-    K.gemv(torch.from_numpy(a).to(device), torch.from_numpy(w).to(device), c, ep)
+    ws = K.gemv_workspace(M, N, KD, device) if split else None
+    K.gemv(torch.from_numpy(a).to(device), torch.from_numpy(w).to(device), c, ep, workspace=ws)
     torch.cuda.synchronize()
     got = c.float().cpu().numpy()
     want = oracle.linear(a, w, ep, c0 if ep == _lib.EPILOGUE_ADD_F32 else None)
     assert np.isfinite(got).all()
     assert _linear_err(got, want) < 2e-3
+
+
+def test_gemv_split_is_deterministic_and_leaves_counters_zero(device):
+    """The K-split merge: the o projection's shape (2048 features, 2 slices) gives the same bits on every launch
+    (the slices are added in slice order, whichever work-group merges), agrees with the unsplit launch within
+    f32 reassociation, leaves its counters at zero, and a smaller batch right after reuses the workspace."""
+    from ember_amd import _lib
+    rng = np.random.default_rng(5)
+    M, N, KD = 32, 2048, 2048
+    a = torch.from_numpy(rng.standard_normal((M, KD)).astype(np.float16)).to(device)
+    w = torch.from_numpy((rng.standard_normal((N, KD)) * 0.05).astype(np.float16)).to(device)
+    ws = K.gemv_workspace(M, N, KD, device)
+    assert ws is not None
+    outs = []
+    for _ in range(3):
+        c = torch.zeros((M, N), dtype=torch.float32, device=device)
+        K.gemv(a, w, c, _lib.EPILOGUE_ADD_F32, workspace=ws)
+        outs.append(c.cpu().numpy())
+    torch.cuda.synchronize()
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
+    plain = torch.zeros((M, N), dtype=torch.float32, device=device)
+    K.gemv(a, w, plain, _lib.EPILOGUE_ADD_F32)
+    np.testing.assert_allclose(outs[0], plain.cpu().numpy(), rtol=1e-5, atol=1e-4)
+    assert not ws[: (N // 16) * 4].any(), "a merge counter was left non-zero"
+    want = oracle.linear(a.cpu().numpy(), w.cpu().numpy(), _lib.EPILOGUE_STORE_F16, None)
+    small = torch.full((5, N), float("nan"), dtype=torch.float16, device=device)
+    K.gemv(a[:5].contiguous(), w, small, _lib.EPILOGUE_STORE_F16, workspace=ws)
+    torch.cuda.synchronize()
+    assert _linear_err(small.float().cpu().numpy(), want[:5]) < 2e-3
+    assert not ws[: (N // 16) * 4].any()
 
 
 def test_gemv_saturates_f16_outputs(device):
