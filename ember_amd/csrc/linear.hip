@@ -258,28 +258,51 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
 }
 
 constexpr int kNormThreads = 256;
+constexpr int kNormPer = 16;  // elements of a row per thread held in registers (hidden <= 4096)
 
 // One work-group per row: the sum of squares in double, reduced in a fixed
-// order (each thread's stride, then the wave, then the waves in order).
+// order (each thread's elements t, t + 256, ..., then the wave, then the
+// waves in order). Rows up to kNormThreads * kNormPer wide keep the thread's
+// elements of x and w in registers, all loaded up front: one memory round
+// trip per row instead of one for x and another for w and x again.
+template <bool HELD>
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float *__restrict__ x,
                                                                     const int32_t *__restrict__ rows, int hidden,
                                                                     const float *__restrict__ w, float eps,
                                                                     f16 *__restrict__ out) {
     __shared__ double part[kNormThreads / kWave];
-    const int r = static_cast<int>(blockIdx.x);
+    const int r = static_cast<int>(blockIdx.x), t = static_cast<int>(threadIdx.x);
     const float *xr = x + static_cast<int64_t>(rows ? rows[r] : r) * hidden;
+    f16 *o = out + static_cast<int64_t>(r) * hidden;
+    float xv[HELD ? kNormPer : 1], wv[HELD ? kNormPer : 1];
     double ss = 0.0;
-    for (int i = static_cast<int>(threadIdx.x); i < hidden; i += kNormThreads)
-        ss += static_cast<double>(xr[i]) * xr[i];
-    for (int o = kWave / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o, kWave);
-    if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = ss;
+    if constexpr (HELD) {
+#pragma unroll
+        for (int j = 0; j < kNormPer; j++) {
+            const int i = t + j * kNormThreads;
+            xv[j] = i < hidden ? xr[i] : 0.0f;
+            wv[j] = i < hidden ? w[i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < kNormPer; j++) ss += static_cast<double>(xv[j]) * xv[j];  // + 0.0 past the row: exact
+    } else {
+        for (int i = t; i < hidden; i += kNormThreads) ss += static_cast<double>(xr[i]) * xr[i];
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, kWave);
+    if (t % kWave == 0) part[t / kWave] = ss;
     __syncthreads();
     double total = part[0];
     for (int v = 1; v < kNormThreads / kWave; v++) total += part[v];
     const float scale = static_cast<float>(1.0 / sqrt(total / hidden + static_cast<double>(eps)));
-    f16 *o = out + static_cast<int64_t>(r) * hidden;
-    for (int i = static_cast<int>(threadIdx.x); i < hidden; i += kNormThreads)
-        o[i] = static_cast<f16>(clamp_half(w[i] * (xr[i] * scale)));
+    if constexpr (HELD) {
+#pragma unroll
+        for (int j = 0; j < kNormPer; j++) {
+            const int i = t + j * kNormThreads;
+            if (i < hidden) o[i] = static_cast<f16>(clamp_half(wv[j] * (xv[j] * scale)));
+        }
+    } else {
+        for (int i = t; i < hidden; i += kNormThreads) o[i] = static_cast<f16>(clamp_half(w[i] * (xr[i] * scale)));
+    }
 }
 
 }  // namespace
@@ -297,8 +320,12 @@ hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream) {
-    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream, a.x,
-                       a.rows, a.hidden, a.w, a.eps, static_cast<f16 *>(a.out));
+    if (a.hidden <= kNormThreads * kNormPer)
+        hipLaunchKernelGGL(rmsnorm_rows_kernel<true>, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream,
+                           a.x, a.rows, a.hidden, a.w, a.eps, static_cast<f16 *>(a.out));
+    else
+        hipLaunchKernelGGL(rmsnorm_rows_kernel<false>, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream,
+                           a.x, a.rows, a.hidden, a.w, a.eps, static_cast<f16 *>(a.out));
     return hipGetLastError();
 }
 

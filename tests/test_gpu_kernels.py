@@ -559,7 +559,7 @@ def test_gemv_saturates_f16_outputs(device):
     assert c.float().cpu().numpy()[0, :2].tolist() == [65504.0, -65504.0]
 
 
-@pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (3, 4096)])
+@pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (3, 4096), (2, 5120)])
 def test_rmsnorm_rows_matches_oracle(device, R, hidden):
     """f16 outputs within one f16 ulp of the oracle's f32 rows (cpu_backend.cpp:34-39; the GPU's double sum of
     squares runs in another order), through a row list."""
