@@ -130,7 +130,7 @@ class ProbArgs(ctypes.Structure):
 class BackendOptions(ctypes.Structure):
     _fields_ = [("max_batch_tokens", c_int32), ("max_seqs", c_int32), ("max_logit_rows", c_int32),
                 ("kv_cache_bytes", c_int64), ("kv_cache_tokens", c_int32), ("memory_fraction", c_double),
-                ("gpu", c_int32)]
+                ("gpu", c_int32), ("graphs", c_int32)]
 
 
 class ModelInfo(ctypes.Structure):
@@ -195,6 +195,7 @@ PROTOTYPES = {
     "ember_kv_prefill_timing": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_double)]),
     "ember_backend_create": (c_void_p, [c_char_p, POINTER(BackendOptions)]),
     "ember_backend_destroy": (None, [c_void_p]),
+    "ember_backend_graph_replays": (c_int64, []),
     "ember_backend_info": (c_int32, [c_void_p, POINTER(ModelInfo)]),
     "ember_backend_forward": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(c_int32), c_int32]),
     "ember_backend_sample": (c_int32, [c_void_p, POINTER(SampleParams), c_int32, POINTER(c_int32)]),

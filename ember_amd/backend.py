@@ -49,6 +49,7 @@ class BackendOptions:
     kv_cache_tokens: int = 0
     memory_fraction: float = 0.0
     gpu: int = 0
+    cuda_graphs: bool = True  # pure decode steps replay one graph of the whole step (backend.hpp:46)
 
 
 def _params(reqs) -> ctypes.Array:
@@ -67,6 +68,7 @@ class Backend:
         c.max_batch_tokens, c.max_seqs, c.max_logit_rows = o.max_batch_tokens, o.max_seqs, o.max_logit_rows
         c.kv_cache_bytes, c.kv_cache_tokens, c.memory_fraction, c.gpu = (o.kv_cache_bytes, o.kv_cache_tokens,
                                                                         o.memory_fraction, o.gpu)
+        c.graphs = 1 if o.cuda_graphs else -1
         self._h = _lib.lib().ember_backend_create(str(model_dir).encode(), c)
         if not self._h:
             raise EmberError(last_error())

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <initializer_list>
@@ -26,6 +27,7 @@
 #include <string>
 #include <tuple>
 #include <utility>
+#include <unordered_map>
 #include <vector>
 
 #include "backend/backend.hpp"
@@ -43,6 +45,8 @@
 namespace ember {
 
 namespace {
+
+std::atomic<int64_t> g_graph_replays{0};  // whole-step graphs launched, every backend of the process
 
 void check_abi(int code, const char *what) {
     if (code != EMBER_OK) fail("{}: {}", what, ember_hip_last_error());
@@ -174,6 +178,7 @@ public:
 
     ~HipBackend() override {
         if (stream_) (void)hipStreamSynchronize(stream_);
+        for (auto &[key, exec] : graphs_) (void)hipGraphExecDestroy(exec);
         kv_.reset();
         if (host_params_) (void)hipHostFree(host_params_);
         if (host_ints_) (void)hipHostFree(host_ints_);
@@ -208,34 +213,17 @@ public:
         for (int32_t t : b.tokens) EMBER_CHECK(t >= 0 && t < c.vocab_size, "token id {} outside the vocabulary", t);
         for (int32_t r : b.logit_rows) EMBER_CHECK(r >= 0 && r < T, "logit row {} outside the batch", r);
         rows_ = 0;  // until this step's logits exist
+        // A pure decode step (one token per sequence, every token a logit row in
+        // order) replays one hipGraph of the whole step, as the reference does
+        // (cuda_backend.cu:145-149): the step's ~200 launches become one.
+        bool decode_only = opt_.cuda_graphs && !capture_ && R == T && T == S;
+        for (int i = 0; decode_only && i < R; i++) decode_only = b.logit_rows[static_cast<size_t>(i)] == i;
+        if (decode_only && forward_graph(b)) {
+            rows_ = R;
+            return;
+        }
         kv_->plan(b);  // validates the tables, uploads tokens, positions, tables and logit rows in one copy
-        const int H = c.hidden, Q = c.q_dim(), KV = c.kv_dim(), I = c.intermediate;
-
-        EmberEmbedArgs e{};
-        e.tokens = kv_->d_tokens();
-        e.T = T;
-        e.table = embed_;
-        e.vocab = c.vocab_size;
-        e.hidden = H;
-        e.out = h_.get<float>();
-        check_abi(ember_hip_embed(&e, stream_), "embed");
-        capture(0, T);
-
-        for (int l = 0; l < c.n_layers; l++) {
-            const LayerWeights &L = layers_[static_cast<size_t>(l)];
-            rmsnorm(nullptr, T, L.in_norm);
-            gemm(xn_.get(), H, L.qkv, T, qkv_.get(), Q + 2 * KV, EMBER_EPILOGUE_STORE_F16);
-            kv_->layer(l, qkv_.get(), L.q_norm, L.k_norm, L.qkv_bias, att_.get());
-            gemm(att_.get(), Q, L.o, T, h_.get(), H, EMBER_EPILOGUE_ADD_F32);
-            rmsnorm(nullptr, T, L.post_norm);
-            gemm(xn_.get(), H, L.gate_up, T, act_.get(), I, EMBER_EPILOGUE_SILU_MUL);
-            gemm(act_.get(), I, L.down, T, h_.get(), H, EMBER_EPILOGUE_ADD_F32);
-            capture(l + 1, T);
-        }
-        if (R > 0) {
-            rmsnorm(kv_->d_logit_rows(), R, final_norm_);
-            gemm(xn_.get(), H, lm_head_, R, logits_.get(), c.vocab_size, EMBER_EPILOGUE_STORE_F32);
-        }
+        enqueue_step(T, R, kv_->d_logit_rows());
         rows_ = R;
     }
 
@@ -312,6 +300,74 @@ public:
 
 private:
     // C[M, N] (+)= A[M, K] . W^T with an epilogue, 64 rows per GEMV launch.
+    // Every launch of a planned step of T tokens: embedding, the layers, then
+    // the final norm and LM head of R logit rows (rows: the planned step's
+    // logit rows on the device, or null for rows 0..R-1).
+    void enqueue_step(int T, int R, const int32_t *rows) {
+        const ModelConfig &c = cfg_;
+        const int H = c.hidden, Q = c.q_dim(), KV = c.kv_dim(), I = c.intermediate;
+        EmberEmbedArgs e{};
+        e.tokens = kv_->d_tokens();
+        e.T = T;
+        e.table = embed_;
+        e.vocab = c.vocab_size;
+        e.hidden = H;
+        e.out = h_.get<float>();
+        check_abi(ember_hip_embed(&e, stream_), "embed");
+        capture(0, T);
+
+        for (int l = 0; l < c.n_layers; l++) {
+            const LayerWeights &L = layers_[static_cast<size_t>(l)];
+            rmsnorm(nullptr, T, L.in_norm);
+            gemm(xn_.get(), H, L.qkv, T, qkv_.get(), Q + 2 * KV, EMBER_EPILOGUE_STORE_F16);
+            kv_->layer(l, qkv_.get(), L.q_norm, L.k_norm, L.qkv_bias, att_.get());
+            gemm(att_.get(), Q, L.o, T, h_.get(), H, EMBER_EPILOGUE_ADD_F32);
+            rmsnorm(nullptr, T, L.post_norm);
+            gemm(xn_.get(), H, L.gate_up, T, act_.get(), I, EMBER_EPILOGUE_SILU_MUL);
+            gemm(act_.get(), I, L.down, T, h_.get(), H, EMBER_EPILOGUE_ADD_F32);
+            capture(l + 1, T);
+        }
+        if (R > 0) {
+            rmsnorm(rows, R, final_norm_);
+            gemm(xn_.get(), H, lm_head_, R, logits_.get(), c.vocab_size, EMBER_EPILOGUE_STORE_F32);
+        }
+    }
+
+    // The step padded to the path's token bucket and planned once
+    // (HipPagedKv::plan_graph: padding tokens sit at position 0 on the spare
+    // block), then every launch of the padded step, logits for all its rows,
+    // replayed from a graph kept per planned layout (cuda_backend.cu:402-454).
+    // The per-token arithmetic is the eager step's, so the real rows' logits
+    // are the same bits. False, with nothing enqueued, when the padded step
+    // would not fit the activation buffers.
+    bool forward_graph(const StepBatch &b) {
+        const int TB = kv_->graph_bucket(b);
+        if (TB == 0 || TB > opt_.max_logit_rows || TB > opt_.max_batch_tokens) return false;
+        EMBER_CHECK(kv_->plan_graph(b) == TB, "internal: the graph bucket changed while planning");
+        const uint64_t key = kv_->graph_key();
+        auto it = graphs_.find(key);
+        if (it == graphs_.end()) {
+            hipGraph_t graph = nullptr;
+            HIPB_CHECK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            try {
+                enqueue_step(TB, TB, nullptr);
+            } catch (...) {
+                (void)hipStreamEndCapture(stream_, &graph);
+                if (graph) (void)hipGraphDestroy(graph);
+                throw;
+            }
+            HIPB_CHECK(hipStreamEndCapture(stream_, &graph));
+            hipGraphExec_t exec = nullptr;
+            const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(graph);
+            HIPB_CHECK(inst);
+            it = graphs_.emplace(key, exec).first;
+        }
+        HIPB_CHECK(hipGraphLaunch(it->second, stream_));
+        g_graph_replays.fetch_add(1, std::memory_order_relaxed);
+        return true;
+    }
+
     void gemm(const void *A, int lda, const Linear &W, int M, void *C, int ldc, int ep) {
         const size_t out_elem = ep == EMBER_EPILOGUE_STORE_F32 || ep == EMBER_EPILOGUE_ADD_F32 ? 4 : 2;
         for (int m0 = 0; m0 < M; m0 += 64) {
@@ -533,10 +589,13 @@ private:
     int num_blocks_ = 0;
     int rows_ = 0;
     bool capture_ = false;
+    std::unordered_map<uint64_t, hipGraphExec_t> graphs_;  // whole decode steps, per planned layout
     std::unique_ptr<HipPagedKv> kv_;
 };
 
 }  // namespace
+
+int64_t hip_backend_graph_replays() { return g_graph_replays.load(std::memory_order_relaxed); }
 
 std::unique_ptr<Backend> create_hip_backend(const std::string &dir, const BackendOptions &opt) {
     return std::make_unique<HipBackend>(dir, opt);

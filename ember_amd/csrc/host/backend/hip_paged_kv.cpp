@@ -464,53 +464,10 @@ int HipPagedKv::width_bucket(int w) const {
 }
 
 bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
-    const int T = b.num_tokens(), S = b.num_seqs();
-    if (T < 1 || T > kGraphMaxTokens || S != T || static_cast<int>(b.query_start.size()) != S + 1) return false;
-    for (int s = 0; s <= S; s++)
-        if (b.query_start[static_cast<size_t>(s)] != s) return false;  // one new token per sequence
-    const int TB = token_bucket(T), WB = width_bucket(std::max(b.max_blocks, 1));
-    if (TB > opt_.max_batch_tokens || TB > opt_.max_seqs || b.max_blocks > WB) return false;
     EMBER_CHECK(static_cast<int>(io.size()) == cfg_.n_layers, "decode_graph: {} layer buffers for {} layers", io.size(),
                 cfg_.n_layers);
-    EMBER_CHECK(!timing_, "decode_graph: kernel timing is not available inside a graph");
-    EMBER_CHECK(static_cast<int64_t>(b.block_tables.size()) == static_cast<int64_t>(S) * b.max_blocks &&
-                    static_cast<int>(b.positions.size()) == T,
-                "decode_graph: malformed batch");
-    // The real rows are checked as plan() checks them, before padding widens
-    // their tables with the spare block: a position past the caller's own
-    // table would otherwise land in the spare block instead of failing.
-    for (int t = 0; t < T; t++) {
-        const int pos = b.positions[static_cast<size_t>(t)];
-        EMBER_CHECK(pos >= 0 && pos < b.max_blocks * kBlockSize, "token {} at position {} is beyond its block table", t,
-                    pos);
-        const int32_t *row = &b.block_tables[static_cast<size_t>(t) * b.max_blocks];
-        for (int p = 0; p <= pos / kBlockSize; p++)
-            EMBER_CHECK(row[p] >= 0 && row[p] <= opt_.num_blocks, "sequence {} page {} names block {} (pool of {})", t, p,
-                        row[p], opt_.num_blocks);
-    }
-
-    // The padded step: real rows keep their table and continue with the spare
-    // block; padding rows are sequences of one token at position 0 whose whole
-    // table is the spare block.
-    StepBatch p;
-    p.max_blocks = WB;
-    p.tokens.assign(static_cast<size_t>(TB), 0);
-    p.positions.assign(static_cast<size_t>(TB), 0);
-    p.query_start.resize(static_cast<size_t>(TB) + 1);
-    p.context_len.assign(static_cast<size_t>(TB), 1);
-    p.block_tables.assign(static_cast<size_t>(TB) * WB, spare_block());
-    for (int t = 0; t <= TB; t++) p.query_start[static_cast<size_t>(t)] = t;
-    for (int t = 0; t < T; t++) {
-        p.tokens[static_cast<size_t>(t)] = b.tokens.empty() ? 0 : b.tokens[static_cast<size_t>(t)];
-        p.positions[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)];
-        p.context_len[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)] + 1;
-        std::copy_n(b.block_tables.begin() + static_cast<ptrdiff_t>(t) * b.max_blocks, b.max_blocks,
-                    p.block_tables.begin() + static_cast<ptrdiff_t>(t) * WB);
-    }
-    const int splits = (WB * kBlockSize + opt_.split_len - 1) / opt_.split_len;
-    plan(p, splits);
-
-    const uint64_t key = (static_cast<uint64_t>(TB) << 34) | (static_cast<uint64_t>(WB) << 2) | static_cast<uint64_t>(stage_);
+    if (plan_graph(b) == 0) return false;
+    const uint64_t key = graph_key();
     auto it = graphs_.find(key);
     auto same_io = [&](const std::vector<LayerIo> &kept) {
         for (size_t l = 0; l < io.size(); l++)
@@ -552,6 +509,68 @@ bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
     }
     EMBER_HIP_CHECK(hipGraphLaunch(it->second.exec, stream_));
     return true;
+}
+
+int HipPagedKv::graph_bucket(const StepBatch &b) const {
+    const int T = b.num_tokens(), S = b.num_seqs();
+    if (T < 1 || T > kGraphMaxTokens || S != T || static_cast<int>(b.query_start.size()) != S + 1) return 0;
+    for (int s = 0; s <= S; s++)
+        if (b.query_start[static_cast<size_t>(s)] != s) return 0;  // one new token per sequence
+    const int TB = token_bucket(T), WB = width_bucket(std::max(b.max_blocks, 1));
+    if (TB > opt_.max_batch_tokens || TB > opt_.max_seqs || b.max_blocks > WB) return 0;
+    return TB;
+}
+
+uint64_t HipPagedKv::graph_key() const {
+    return (static_cast<uint64_t>(graph_tb_) << 34) | (static_cast<uint64_t>(graph_wb_) << 2) |
+           static_cast<uint64_t>(stage_);
+}
+
+int HipPagedKv::plan_graph(const StepBatch &b) {
+    const int TB = graph_bucket(b);
+    if (TB == 0) return 0;
+    const int T = b.num_tokens(), S = b.num_seqs();
+    const int WB = width_bucket(std::max(b.max_blocks, 1));
+    EMBER_CHECK(!timing_, "decode_graph: kernel timing is not available inside a graph");
+    EMBER_CHECK(static_cast<int64_t>(b.block_tables.size()) == static_cast<int64_t>(S) * b.max_blocks &&
+                    static_cast<int>(b.positions.size()) == T,
+                "decode_graph: malformed batch");
+    // The real rows are checked as plan() checks them, before padding widens
+    // their tables with the spare block: a position past the caller's own
+    // table would otherwise land in the spare block instead of failing.
+    for (int t = 0; t < T; t++) {
+        const int pos = b.positions[static_cast<size_t>(t)];
+        EMBER_CHECK(pos >= 0 && pos < b.max_blocks * kBlockSize, "token {} at position {} is beyond its block table", t,
+                    pos);
+        const int32_t *row = &b.block_tables[static_cast<size_t>(t) * b.max_blocks];
+        for (int p = 0; p <= pos / kBlockSize; p++)
+            EMBER_CHECK(row[p] >= 0 && row[p] <= opt_.num_blocks, "sequence {} page {} names block {} (pool of {})", t, p,
+                        row[p], opt_.num_blocks);
+    }
+
+    // The padded step: real rows keep their table and continue with the spare
+    // block; padding rows are sequences of one token at position 0 whose whole
+    // table is the spare block.
+    StepBatch p;
+    p.max_blocks = WB;
+    p.tokens.assign(static_cast<size_t>(TB), 0);
+    p.positions.assign(static_cast<size_t>(TB), 0);
+    p.query_start.resize(static_cast<size_t>(TB) + 1);
+    p.context_len.assign(static_cast<size_t>(TB), 1);
+    p.block_tables.assign(static_cast<size_t>(TB) * WB, spare_block());
+    for (int t = 0; t <= TB; t++) p.query_start[static_cast<size_t>(t)] = t;
+    for (int t = 0; t < T; t++) {
+        p.tokens[static_cast<size_t>(t)] = b.tokens.empty() ? 0 : b.tokens[static_cast<size_t>(t)];
+        p.positions[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)];
+        p.context_len[static_cast<size_t>(t)] = b.positions[static_cast<size_t>(t)] + 1;
+        std::copy_n(b.block_tables.begin() + static_cast<ptrdiff_t>(t) * b.max_blocks, b.max_blocks,
+                    p.block_tables.begin() + static_cast<ptrdiff_t>(t) * WB);
+    }
+    const int splits = (WB * kBlockSize + opt_.split_len - 1) / opt_.split_len;
+    plan(p, splits);
+    graph_tb_ = TB;
+    graph_wb_ = WB;
+    return TB;
 }
 
 void HipPagedKv::copy_blocks(std::span<const int32_t> src, std::span<const int32_t> dst) {

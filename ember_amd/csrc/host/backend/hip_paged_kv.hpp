@@ -69,6 +69,17 @@ public:
     // and captured again when the layer buffers change. Returns false, with
     // nothing enqueued, when the step is not a pure decode step of <= 64 tokens.
     bool decode_graph(const StepBatch &b, std::span<const LayerIo> io);
+    // The planning half of decode_graph, for a caller that captures more than
+    // the attention layers (a backend's whole model step): the token bucket
+    // the step pads to, or 0 when it is not a pure decode step of <= 64 tokens.
+    int graph_bucket(const StepBatch &b) const;
+    // Validates, pads and plans the step as decode_graph does; returns its
+    // token bucket (the planned step's tokens, rows past T padding), or 0 with
+    // nothing planned. graph_key() then names the planned layout: layer()
+    // launches of two plans with the same key take the same arguments, so one
+    // captured graph replays either.
+    int plan_graph(const StepBatch &b);
+    uint64_t graph_key() const;
     static int token_bucket(int T);
     int width_bucket(int w) const;
 
@@ -134,6 +145,7 @@ private:
     hipEvent_t consumed_[kStages] = {}; // the kernels that read each buffer have run
     hipStream_t upload_stream_ = nullptr;
     int stage_ = 0;
+    int graph_tb_ = 0, graph_wb_ = 0;  // the last plan_graph's buckets
     // copy_blocks' pair lists, double-buffered: pinned staging, the device list
     // the copy kernel reads, and an event recorded after that kernel.
     static constexpr int kCowPairs = 4096;

@@ -12,6 +12,10 @@
 #include "backend/backend.hpp"
 #include "backend/hip_paged_kv.hpp"
 #include "capi_errors.hpp"
+
+namespace ember {
+int64_t hip_backend_graph_replays();  // hip_backend.cpp
+}
 #include "common/error.hpp"
 #include "ember_hip.h"
 #include "kvcache/block_manager.hpp"
@@ -290,6 +294,7 @@ EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOpti
         opt.kv_cache_tokens = o->kv_cache_tokens;
         if (o->memory_fraction > 0.0) opt.memory_fraction = o->memory_fraction;
         opt.gpu = o->gpu;
+        if (o->graphs != 0) opt.cuda_graphs = o->graphs > 0;
         return new EmberBackend{ember::create_backend(model_dir, opt)};
     } catch (const std::exception &e) {
         set_error(EMBER_ERR_INVALID, "backend_create: %s", e.what());
@@ -298,6 +303,8 @@ EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOpti
 }
 
 void ember_backend_destroy(EmberBackend *h) { delete h; }
+
+int64_t ember_backend_graph_replays(void) { return ember::hip_backend_graph_replays(); }
 
 int32_t ember_backend_info(const EmberBackend *h, EmberModelInfo *out) {
     return guarded("backend_info", [&] {

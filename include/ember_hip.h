@@ -481,6 +481,7 @@ typedef struct EmberBackendOptions {
     int32_t kv_cache_tokens;      /* or the cache in tokens, or 0 (then memory_fraction of free memory) */
     double memory_fraction;       /* 0 = the default (0.92) */
     int32_t gpu;                  /* device index */
+    int32_t graphs;               /* BackendOptions::cuda_graphs: 1 on, -1 off, 0 the default (on) */
 } EmberBackendOptions;
 
 typedef struct EmberModelInfo {
@@ -495,6 +496,9 @@ typedef struct EmberBackend EmberBackend;
 EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOptions *options);
 void ember_backend_destroy(EmberBackend *backend);
 int32_t ember_backend_info(const EmberBackend *backend, EmberModelInfo *out);
+/* Whole-step decode graphs replayed so far by every backend of the process
+ * (no counterpart in the reference; a diagnostic for tests and benchmarks). */
+int64_t ember_backend_graph_replays(void);
 /* Backend::forward (backend.hpp:104-106): appends every token's K/V and keeps
  * the logits of the n_rows tokens logit_rows[] on the device. */
 int32_t ember_backend_forward(EmberBackend *backend, const EmberStepBatch *batch, const int32_t *logit_rows,

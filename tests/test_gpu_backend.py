@@ -165,3 +165,64 @@ def test_errors_raise(model, tmp_path):
     with pytest.raises(EmberError, match="requests for"):
         be.sample([SampleRequest(), SampleRequest()])
     be.close()
+
+
+def _multi_batch(seqs, lens, firsts, width, logit_rows):
+    """One step of several sequences: seqs[i] are sequence i's new tokens, lens[i] its length before the step, its
+    pages firsts[i], firsts[i] + 1, ... (table rows `width` wide, padded with page 0, never read past the context)."""
+    tokens, positions, qs, ctx, tables = [], [], [0], [], []
+    for toks, n, f in zip(seqs, lens, firsts):
+        tokens += list(toks)
+        positions += list(range(n, n + len(toks)))
+        qs.append(qs[-1] + len(toks))
+        ctx.append(n + len(toks))
+        tables += [f + p for p in range(width)]
+    return StepBatch(tokens=tokens, positions=positions, query_start=qs, context_len=ctx, block_tables=tables,
+                     max_blocks=width, logit_rows=list(logit_rows))
+
+
+def test_decode_steps_replay_one_graph_and_equal_eager(model):
+    """A pure decode step (one token per sequence, every token a logit row in order) replays one hipGraph of the whole
+    model step, as the reference's forward does (cuda_backend.cu:145-149, :402-454): padded to the token bucket with
+    spare-block rows. Its real rows' logits equal the eager step's bit for bit (graphs off, same model, same steps):
+    five sequences (bucket 6, one padding row), then four (bucket 4). A step whose logit rows are not every token in
+    order runs eagerly, and so does every step with graphs off (the replay counter shows which)."""
+    from ember_amd import _lib
+
+    d, _ = model
+    opts = dict(max_batch_tokens=256, max_seqs=8, kv_cache_tokens=64 * PAGE)
+    bg = create_backend(str(d), BackendOptions(**opts))  # graphs on: the reference's default
+    be = create_backend(str(d), BackendOptions(cuda_graphs=False, **opts))
+    replays = _lib.lib().ember_backend_graph_replays
+    rng = np.random.default_rng(11)
+    lens = [40, 70, 17, 33, 5]
+    width = 8  # pages per table row: room for every prompt plus the decodes
+    firsts = [i * width for i in range(len(lens))]
+    prompts = [rng.integers(3, V, n).tolist() for n in lens]
+    rows = np.cumsum(lens) - 1
+    b = _multi_batch(prompts, [0] * 5, firsts, width, rows)
+    for x in (bg, be):
+        x.forward(b)  # a prefill step: eager in both
+    nxt = [int(np.argmax(be.logits(r))) for r in range(5)]
+    assert nxt == [int(np.argmax(bg.logits(r))) for r in range(5)]
+    cur = list(lens)
+    graphs_run = 0
+    for step in range(9):
+        S = 5 if step < 6 else 4
+        logit_rows = [0, 2] if step == 3 else list(range(S))
+        b = _multi_batch([[t] for t in nxt[:S]], cur[:S], firsts[:S], width, logit_rows)
+        before = replays()
+        be.forward(b)
+        assert replays() == before, "graphs off: the step ran eagerly"
+        bg.forward(b)
+        graph_step = step != 3
+        assert replays() == before + (1 if graph_step else 0)
+        graphs_run += graph_step
+        for i in range(len(logit_rows)):
+            np.testing.assert_array_equal(bg.logits(i), be.logits(i), err_msg=f"step {step} row {i}")
+        got = {r: int(np.argmax(be.logits(i))) for i, r in enumerate(logit_rows)}
+        nxt = [got.get(r, 7) for r in range(S)] + nxt[S:]
+        cur = [c + 1 for c in cur[:S]] + cur[S:]
+    assert graphs_run == 8
+    bg.close()
+    be.close()
