@@ -512,6 +512,75 @@ def run_linear(args) -> dict:
     }
 
 
+def run_backend(args) -> dict:
+    """Whole-model decode through HipBackend (ember::Backend, device "hip"): a synthetic Qwen3-0.6B-shaped model
+    (28 layers, hidden 1024, 16 q / 8 kv heads, MLP 3072, tied 151,936-token vocabulary, N(0, 0.02) weights in the
+    safetensors layout the backend loads), 8 sequences with 128-token prompts, then greedy decode steps (forward +
+    sample). Each step is timed with the whole step replayed as one hipGraph (BackendOptions.cuda_graphs, the
+    reference's default) and, on a second backend over the same files, launched eagerly (~200 launches).
+    Bytes per step: every weight once plus the K/V of every context token."""
+    import tempfile
+
+    from ember_amd.backend import BackendOptions, SampleRequest, SamplingParams, create_backend
+    from ember_amd.paged_kv import StepBatch
+
+    sys.path.insert(0, str(ROOT / "tests"))
+    from synthetic_model import write_model
+
+    B, PROMPT, LAYERS, VOCAB, HID, INTER, QD, KVD = 8, 128, 28, 151936, 1024, 3072, 2048, 1024
+    weight_bytes = 2 * (LAYERS * ((QD + 2 * KVD) * HID + HID * QD + 2 * INTER * HID + HID * INTER) + VOCAB * HID)
+    kv_token_bytes = LAYERS * 2 * KVD * 2  # K and V of one token, every layer, f16
+    n_steps = args.warmup + args.steps
+    width = (PROMPT + n_steps + PAGE) // PAGE + 1
+    greedy = [SampleRequest(SamplingParams(temperature=0.0))] * B
+    rng = np.random.default_rng(SEED + 11)
+    prompts = rng.integers(3, VOCAB, (B, PROMPT)).tolist()
+
+    def batch(new_tokens, lens, rows):
+        toks, pos, qs, ctx, tab = [], [], [0], [], []
+        for i, (t, n) in enumerate(zip(new_tokens, lens)):
+            toks += t
+            pos += list(range(n, n + len(t)))
+            qs.append(qs[-1] + len(t))
+            ctx.append(n + len(t))
+            tab += [i * width + p for p in range(width)]
+        return StepBatch(tokens=toks, positions=pos, query_start=qs, context_len=ctx, block_tables=tab,
+                         max_blocks=width, logit_rows=list(rows))
+
+    results = {}
+    with tempfile.TemporaryDirectory() as td:
+        log(f"[bench] writing a synthetic {LAYERS}-layer Qwen3-0.6B-shaped model ({weight_bytes / 1e9:.2f} GB f16)")
+        write_model(Path(td), layers=LAYERS, vocab=VOCAB)
+        for graphs in (True, False):
+            be = create_backend(td, BackendOptions(max_batch_tokens=B * PROMPT, max_seqs=B, kv_cache_tokens=B * width * PAGE,
+                                                   cuda_graphs=graphs))
+            be.forward(batch(prompts, [0] * B, [PROMPT * (i + 1) - 1 for i in range(B)]))
+            nxt, lens = be.sample(greedy), [PROMPT] * B
+            ctx_sum = 0
+            for step in range(n_steps):
+                if step == args.warmup:
+                    t0, ctx_sum = time.perf_counter(), 0
+                be.forward(batch([[t] for t in nxt], lens, range(B)))
+                nxt = be.sample(greedy)  # waits for the step's logits
+                lens = [n + 1 for n in lens]
+                ctx_sum += sum(lens)
+            wall = time.perf_counter() - t0
+            be.close()
+            results[graphs] = (wall / args.steps, ctx_sum / args.steps)
+            log(f"[bench] backend decode, graphs {'on' if graphs else 'off'}: {wall / args.steps * 1e3:.3f} ms/step")
+    step_s, ctx = results[True]
+    step_bytes = weight_bytes + kv_token_bytes * ctx
+    return {
+        "metric": "whole-model greedy decode tokens/s through HipBackend (Qwen3-0.6B shape, batch 8)",
+        "value": round(B / step_s, 1), "unit": "tokens/s", "ms_per_step": round(step_s * 1e3, 4),
+        "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
+        "eager_ms_per_step": round(results[False][0] * 1e3, 4),
+        "config": {"workload": "synthetic Qwen3-0.6B-shaped model (28 layers, tied 151,936 vocabulary), 8 sequences, "
+                               "128-token prompts, greedy decode steps (forward + sample) as one replayed graph each; "
+                               "eager_ms_per_step: the same steps launched one by one"},
+    }
+
+
 def run_block(args) -> dict:
     """Config 2's decode step with the whole attention block per layer (input RMSNorm, qkv GEMV, the fused
     append + paged attention, o GEMV into the f32 residual), 28 layers: the attention half of a Qwen3-1.7B
@@ -757,6 +826,8 @@ def main() -> int:
                     help="config 2 with the whole attention block per layer (RMSNorm, qkv/o GEMVs); its own line")
     ap.add_argument("--linear", action="store_true",
                     help="time the layer either side of the path (input RMSNorm, qkv and o GEMVs); its own line")
+    ap.add_argument("--backend", action="store_true",
+                    help="whole-model decode through HipBackend on a synthetic Qwen3-0.6B-shaped model; its own line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only the known-size page copy used to scale the HBM byte counters")
     args = ap.parse_args()
@@ -766,7 +837,7 @@ def main() -> int:
         return 2
     if args.copy_calibration:
         return copy_calibration(args.steps)
-    if args.config != 2 or args.linear or args.block:
+    if args.config != 2 or args.linear or args.block or args.backend:
         import torch
 
         from ember_amd import lib
@@ -774,8 +845,8 @@ def main() -> int:
         lib()
         assert torch.cuda.is_available(), "bench.py needs a GPU"
         log("[bench] linear layers" if args.linear else "[bench] attention block" if args.block
-            else f"[bench] BASELINE config {args.config}")
-        fn = (run_linear if args.linear else run_block if args.block
+            else "[bench] whole-model decode" if args.backend else f"[bench] BASELINE config {args.config}")
+        fn = (run_linear if args.linear else run_block if args.block else run_backend if args.backend
               else {3: run_config3, 4: run_config4, 5: run_config5}[args.config])
         line = fn(args)
         line.update({"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
