@@ -104,9 +104,28 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
     };
+    // A tail of n < kGemvUnroll / 2 + 1 steps (n wave-uniform) as one round:
+    // the same steps in the same order, their loads issued together.
+    auto tail = [&](int s0, int stride, int n) {
+        constexpr int U = kGemvUnroll / 2;
+        f16x8 wv[U], xv[U][MT];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (u < n) wv[u] = load_w(w + 32 * (s0 + u * stride));
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                if (u < n)
+                    xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s0 + u * stride)) : f16x8{};
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+                if (u < n) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
+    };
     using Full = std::integral_constant<int, kGemvUnroll>;
     using Half = std::integral_constant<int, kGemvUnroll / 2>;
-    using One = std::integral_constant<int, 1>;
     const int steps = K / KS / 32;
     if constexpr (SPLIT) {
         // A slice has few steps per wave: each wave takes a contiguous run, so
@@ -118,12 +137,17 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
             round(Half{}, s, 1);
             s += kGemvUnroll / 2;
         }
-        for (; s < end; s++) round(One{}, s, 1);
+        if (s < end) tail(s, 1, end - s);
     } else {
         // Wave w takes k steps w, w + 8, ...
         int s = wave;
         for (; s + (kGemvUnroll - 1) * kGemvWaves < steps; s += kGemvUnroll * kGemvWaves) round(Full{}, s, kGemvWaves);
-        for (; s < steps; s += kGemvWaves) round(One{}, s, kGemvWaves);
+        for (int left = (steps - s + kGemvWaves - 1) / kGemvWaves; left > 0;) {
+            const int n = min(left, kGemvUnroll / 2);
+            tail(s, kGemvWaves, n);
+            s += n * kGemvWaves;
+            left -= n;
+        }
     }
 
     if (wave > 0) {
