@@ -104,28 +104,21 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
     };
-    // A tail of n < kGemvUnroll / 2 + 1 steps (n wave-uniform) as one round:
-    // the same steps in the same order, their loads issued together.
-    auto tail = [&](int s0, int stride, int n) {
-        constexpr int U = kGemvUnroll / 2;
-        f16x8 wv[U], xv[U][MT];
-#pragma unroll
-        for (int u = 0; u < U; u++)
-            if (u < n) wv[u] = load_w(w + 32 * (s0 + u * stride));
-#pragma unroll
-        for (int u = 0; u < U; u++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                if (u < n)
-                    xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s0 + u * stride)) : f16x8{};
-#pragma unroll
-        for (int u = 0; u < U; u++)
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                if (u < n) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
-    };
     using Full = std::integral_constant<int, kGemvUnroll>;
     using Half = std::integral_constant<int, kGemvUnroll / 2>;
+    // A tail of n = 1..4 steps (wave-uniform) as one round of exactly n: the
+    // same steps in the same order, their loads issued together. (A form with
+    // every step of the round guarded by u < n, its unused operands left
+    // unset, gave wrong sums in one accumulator element of some lanes at 4-way
+    // splits; rounds of a fixed size have no guarded MFMAs.)
+    auto tail = [&](int s0, int stride, int n) {
+        switch (n) {
+            case 1: round(std::integral_constant<int, 1>{}, s0, stride); break;
+            case 2: round(std::integral_constant<int, 2>{}, s0, stride); break;
+            case 3: round(std::integral_constant<int, 3>{}, s0, stride); break;
+            default: round(Half{}, s0, stride); break;
+        }
+    };
     const int steps = K / KS / 32;
     if constexpr (SPLIT) {
         // A slice has few steps per wave: each wave takes a contiguous run, so
