@@ -17,13 +17,19 @@ SOURCES = [HOST / "kvcache" / "block_manager.cpp", HOST / "model" / "config.cpp"
            HOST / "common" / "json.cpp", HOST / "common" / "mmap_file.cpp"]
 
 
-@pytest.fixture(scope="module")
-def boundary_binary(tmp_path_factory):
+# The plain build, and one with the undefined-behaviour sanitizer (every finding fatal) and libstdc++'s checked
+# containers and iterators, over the same host sources and scenarios.
+CHECKED = ["-fsanitize=undefined", "-fno-sanitize-recover=all", "-D_GLIBCXX_ASSERTIONS", "-g"]
+
+
+@pytest.fixture(scope="module", params=["plain", "checked"])
+def boundary_binary(request, tmp_path_factory):
     gxx = shutil.which("g++")
     if gxx is None:
         pytest.skip("g++ is not installed")
-    out = tmp_path_factory.mktemp("cpp") / "boundary_test"
-    cmd = [gxx, "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror", f"-I{HOST}", f"-I{ROOT / 'include'}",
+    out = tmp_path_factory.mktemp("cpp") / f"boundary_test_{request.param}"
+    extra = CHECKED if request.param == "checked" else []
+    cmd = [gxx, "-std=c++20", "-O1", "-Wall", "-Wextra", "-Werror", *extra, f"-I{HOST}", f"-I{ROOT / 'include'}",
            str(ROOT / "tests" / "cpp" / "boundary_test.cpp"), *map(str, SOURCES), "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stderr
