@@ -225,6 +225,95 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     }
 }
 
+// Very wide launches (an LM head's 151,936 features) at up to 16 tokens: each
+// work-group takes kWideTiles 16-feature tiles that share every activation
+// load, so the launch runs a quarter of the work-groups, each with four times
+// the W loads in flight. Per tile the arithmetic is gemv_kernel's (the same k
+// steps per wave in the same order, the waves summed in wave order), so the
+// results are the same bits.
+constexpr int kWideTiles = 4;
+constexpr int kWideMinTiles = 4096;  // 16-feature tiles at which a launch goes wide
+
+template <int EP>
+__global__ void __launch_bounds__(kGemvThreads) gemv_wide_kernel(const f16 *__restrict__ A, int lda,
+                                                                 const f16 *__restrict__ W, int M, int N, int K,
+                                                                 void *__restrict__ C, int ldc) {
+    __shared__ f32x4 red[kGemvWaves - 1][kWideTiles][kWave];
+    const int tid = static_cast<int>(threadIdx.x);
+    const int lane = tid % kWave, wave = tid / kWave;
+    const int c = lane % 16, g = lane / 16;
+    const int n0 = static_cast<int>(blockIdx.x) * 16 * kWideTiles;
+    const f16 *w[kWideTiles];
+#pragma unroll
+    for (int f = 0; f < kWideTiles; f++) w[f] = W + static_cast<int64_t>(min(n0 + 16 * f + c, N - 1)) * K + 8 * g;
+    const bool xok = c < M;
+    const f16 *x = A + static_cast<int64_t>(min(c, M - 1)) * lda + 8 * g;
+    f32x4 acc[kWideTiles];
+#pragma unroll
+    for (int f = 0; f < kWideTiles; f++) acc[f] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    // Wave w takes k steps w, w + 8, ..., up to four per round.
+    auto round = [&](auto unroll, int s0) {
+        constexpr int U = decltype(unroll)::value;
+        f16x8 wv[U][kWideTiles], xv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int f = 0; f < kWideTiles; f++) wv[u][f] = load_w(w[f] + 32 * (s0 + u * kGemvWaves));
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            xv[u] = xok ? *reinterpret_cast<const f16x8 *>(x + 32 * (s0 + u * kGemvWaves)) : f16x8{};
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int f = 0; f < kWideTiles; f++) acc[f] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u][f], xv[u], acc[f], 0, 0, 0);
+    };
+    const int steps = K / 32;
+    int s = wave;
+    for (; s + 3 * kGemvWaves < steps; s += 4 * kGemvWaves) round(std::integral_constant<int, 4>{}, s);
+    switch ((steps - s + kGemvWaves - 1) / kGemvWaves) {
+        case 1: round(std::integral_constant<int, 1>{}, s); break;
+        case 2: round(std::integral_constant<int, 2>{}, s); break;
+        case 3: round(std::integral_constant<int, 3>{}, s); break;
+        default: break;
+    }
+
+    if (wave > 0) {
+#pragma unroll
+        for (int f = 0; f < kWideTiles; f++) red[wave - 1][f][lane] = acc[f];
+    }
+    __syncthreads();
+    if (wave != 0 || !xok) return;
+#pragma unroll
+    for (int f = 0; f < kWideTiles; f++) {
+#pragma unroll
+        for (int v = 0; v < kGemvWaves - 1; v++) acc[f] = acc[f] + red[v][f][lane];
+        // acc[f][i] = C[token c][feature n0 + 16 f + 4 g + i].
+        if constexpr (EP == EMBER_EPILOGUE_SILU_MUL) {
+#pragma unroll
+            for (int i = 0; i < 4; i += 2) {
+                const int n = n0 + 16 * f + 4 * g + i;
+                if (n + 1 < N)
+                    static_cast<f16 *>(C)[static_cast<int64_t>(c) * ldc + n / 2] =
+                        static_cast<f16>(clamp_half(silu(acc[f][i]) * acc[f][i + 1]));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int n = n0 + 16 * f + 4 * g + i;
+                if (n >= N) continue;
+                const int64_t at = static_cast<int64_t>(c) * ldc + n;
+                if constexpr (EP == EMBER_EPILOGUE_STORE_F16)
+                    static_cast<f16 *>(C)[at] = static_cast<f16>(clamp_half(acc[f][i]));
+                else if constexpr (EP == EMBER_EPILOGUE_STORE_F32)
+                    static_cast<float *>(C)[at] = acc[f][i];
+                else
+                    static_cast<float *>(C)[at] += acc[f][i];
+            }
+        }
+    }
+}
+
 // Work-groups per 16 features: doubled while the launch has fewer than
 // kGemvTargetGroups and each slice keeps at least one 32-wide k step per wave.
 int gemv_split(int N, int K) {
@@ -261,6 +350,12 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
                            counters);
         return hipGetLastError();
     };
+    if (!split && a.M <= 16 && nfb >= kWideMinTiles) {
+        const dim3 wide(static_cast<unsigned>((nfb + kWideTiles - 1) / kWideTiles));
+        hipLaunchKernelGGL(gemv_wide_kernel<EP>, wide, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C,
+                           a.ldc);
+        return hipGetLastError();
+    }
     switch ((a.M + 15) / 16 + (split ? 4 : 0)) {
         case 1: return go(gemv_kernel<1, EP, false>);
         case 2: return go(gemv_kernel<2, EP, false>);

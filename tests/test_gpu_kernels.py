@@ -494,14 +494,16 @@ def _linear_err(got, want):
 
 @pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (8, 512, 1024), (13, 200, 128), (31, 384, 512),
                                    (64, 256, 1024), (32, 4096, 2048), (32, 2048, 2048), (17, 48, 32),
-                                   (16, 1024, 2048), (8, 1024, 3072), (5, 4096, 1024)])
+                                   (16, 1024, 2048), (8, 1024, 3072), (5, 4096, 1024),
+                                   (3, 70000, 256), (16, 66000, 1024)])
 @pytest.mark.parametrize("ep", [0, 1, 2, 3])
 @pytest.mark.parametrize("split", [False, True])
 def test_gemv_matches_oracle(device, M, N, KD, ep, split):
     """Every epilogue on the reference test's decode-sized shapes (K a multiple of 32) and the Qwen3-1.7B
     projections; ragged M and N exercise the clamped rows. With a workspace, the shapes with few features take
     the K split: 2 or 4 slices, with 1 to 4 k steps per wave in a slice (16 x 1024 x 2048 and 8 x 1024 x 3072
-    are 4-way splits with 2 and 3), and 5 x 4096 x 1024 unsplit with 4 steps per wave. Bound 2e-3 as in the
+    are 4-way splits with 2 and 3), and 5 x 4096 x 1024 unsplit with 4 steps per wave. 70,000 and 66,000
+    features take the wide form (four tiles per work-group; the last block ragged). Bound 2e-3 as in the
     reference's test."""
     from ember_amd import _lib
     rng = np.random.default_rng(M * 7919 + N * 31 + KD + ep)
