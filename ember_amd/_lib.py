@@ -97,7 +97,7 @@ class LayerIo(ctypes.Structure):
 class GemvArgs(ctypes.Structure):
     _fields_ = [
         ("A", c_void_p), ("lda", c_int32), ("W", c_void_p), ("M", c_int32), ("N", c_int32), ("K", c_int32),
-        ("C", c_void_p), ("ldc", c_int32), ("epilogue", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_int64),
+        ("C", c_void_p), ("ldc", c_int32), ("epilogue", c_int32), ("workspace", c_void_p), ("workspace_bytes", c_int64), ("w_packed", c_int32),
     ]
 
 
@@ -152,6 +152,8 @@ PROTOTYPES = {
     "ember_hip_copy_pages": (c_int32, [POINTER(CopyArgs), c_void_p]),
     "ember_hip_gemv": (c_int32, [POINTER(GemvArgs), c_void_p]),
     "ember_hip_gemv_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
+    "ember_hip_gemv_packed_bytes": (c_int64, [c_int32, c_int32]),
+    "ember_hip_gemv_pack": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
     "ember_hip_rmsnorm_rows": (c_int32, [POINTER(NormArgs), c_void_p]),
     "ember_hip_embed": (c_int32, [POINTER(EmbedArgs), c_void_p]),
     "ember_hip_sample": (c_int32, [POINTER(SampleArgs), c_void_p]),

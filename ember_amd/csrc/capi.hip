@@ -223,9 +223,25 @@ int ember_hip_gemv(const EmberGemvArgs *a, void *stream) {
     if (!a->A || !a->W || !a->C) return set_error(EMBER_ERR_INVALID, "gemv: a required pointer is null");
     if (reinterpret_cast<uintptr_t>(a->A) % 16 != 0 || reinterpret_cast<uintptr_t>(a->W) % 16 != 0)
         return set_error(EMBER_ERR_INVALID, "gemv: A and W must be 16-byte aligned");
+    if (a->w_packed != 0 && a->w_packed != 1) return set_error(EMBER_ERR_INVALID, "gemv: w_packed is 0 or 1");
     if (a->workspace_bytes < 0 || reinterpret_cast<uintptr_t>(a->workspace) % 16 != 0)
         return set_error(EMBER_ERR_INVALID, "gemv: the workspace must be 16-byte aligned with a size >= 0");
     return hip_status(launch_gemv(*a, static_cast<hipStream_t>(stream)), "gemv");
+}
+
+int64_t ember_hip_gemv_packed_bytes(int32_t N, int32_t K) {
+    if (N < 1 || K < 32 || K % 32 != 0) return 0;
+    return gemv_packed_bytes(N, K);
+}
+
+int ember_hip_gemv_pack(const void *W, int32_t N, int32_t K, void *out, void *stream) {
+    g_last_error.clear();
+    if (N < 1 || K < 32 || K % 32 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv_pack: N >= 1 and K a positive multiple of 32 (got N %d, K %d)", N, K);
+    if (!W || !out) return set_error(EMBER_ERR_INVALID, "gemv_pack: a required pointer is null");
+    if (reinterpret_cast<uintptr_t>(W) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0)
+        return set_error(EMBER_ERR_INVALID, "gemv_pack: W and out must be 16-byte aligned");
+    return hip_status(launch_gemv_pack(W, N, K, out, static_cast<hipStream_t>(stream)), "gemv_pack");
 }
 
 int64_t ember_hip_gemv_workspace_bytes(int32_t M, int32_t N, int32_t K) {

@@ -40,6 +40,8 @@ hipError_t launch_copy_pages(const EmberCopyArgs &a, hipStream_t stream);
 
 hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream);
 int64_t gemv_workspace_bytes(int M, int N, int K);  // 0: no K split for this shape
+int64_t gemv_packed_bytes(int N, int K);
+hipError_t launch_gemv_pack(const void *W, int N, int K, void *out, hipStream_t stream);
 
 hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream);
 

@@ -37,6 +37,11 @@ constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kGemvUnroll = 8;  // k steps whose W loads are in flight together, per wave
 constexpr int kGemvTargetGroups = 256;  // work-groups a launch should reach: one per CU
 constexpr int kGemvMaxSplit = 4;
+// Packed W (ember_hip_gemv_pack): for each 16-feature tile and 32-wide k step,
+// the MFMA A operand as the 64 lanes take it, 8 halves per lane (lane 16 g + c:
+// row 16 tile + c, k 32 step + 8 g ..): one contiguous 1 KiB per load
+// instruction of a wave instead of 16 rows of 64 bytes. Rows past N are zero.
+constexpr int kPackBlock = 64 * 8;  // halves per (tile, k step)
 
 // Split slices are written and read with device-scope relaxed atomics (sc1
 // global stores and loads on gfx950, coherent across the XCDs' L2s), under
@@ -60,7 +65,7 @@ __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 // MT tiles of 16 tokens (M <= 16 MT); EP an EMBER_EPILOGUE_*; SPLIT: K split
 // over gridDim.y work-groups (a separate instance, so the unsplit one keeps
 // its constant-stride loads and no merge code).
-template <int MT, int EP, bool SPLIT>
+template <int MT, int EP, bool SPLIT, bool PACKED>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restrict__ A, int lda,
                                                             const f16 *__restrict__ W, int M, int N, int K,
                                                             void *__restrict__ C, int ldc,
@@ -74,7 +79,11 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     const int ks = SPLIT ? static_cast<int>(blockIdx.y) : 0, KS = SPLIT ? static_cast<int>(gridDim.y) : 1;
     const int n0 = fb * 16;
     const int k0 = ks * (K / KS);  // this work-group's K slice: K / KS, a multiple of 32
-    const f16 *w = W + static_cast<int64_t>(min(n0 + c, N - 1)) * K + k0 + 8 * g;  // rows past N repeat the last
+    // Row-major W: this lane's row (rows past N repeat the last), k step s at
+    // +32 s. Packed W: the tile's k steps are 1 KiB blocks in lane order.
+    const f16 *w = PACKED ? W + (static_cast<int64_t>(fb) * (K / 32) + k0 / 32) * kPackBlock + 8 * lane
+                          : W + static_cast<int64_t>(min(n0 + c, N - 1)) * K + k0 + 8 * g;
+    constexpr int wstep = PACKED ? kPackBlock : 32;  // halves per k step
     const f16 *x[MT];
     bool xok[MT];
 #pragma unroll
@@ -93,7 +102,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
         constexpr int U = decltype(unroll)::value;
         f16x8 wv[U], xv[U][MT];
 #pragma unroll
-        for (int u = 0; u < U; u++) wv[u] = load_w(w + 32 * (s0 + u * stride));
+        for (int u = 0; u < U; u++) wv[u] = load_w(w + wstep * (s0 + u * stride));
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
@@ -234,7 +243,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
 constexpr int kWideTiles = 4;
 constexpr int kWideMinTiles = 4096;  // 16-feature tiles at which a launch goes wide
 
-template <int EP>
+template <int EP, bool PACKED>
 __global__ void __launch_bounds__(kGemvThreads) gemv_wide_kernel(const f16 *__restrict__ A, int lda,
                                                                  const f16 *__restrict__ W, int M, int N, int K,
                                                                  void *__restrict__ C, int ldc) {
@@ -245,7 +254,10 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_wide_kernel(const f16 *__re
     const int n0 = static_cast<int>(blockIdx.x) * 16 * kWideTiles;
     const f16 *w[kWideTiles];
 #pragma unroll
-    for (int f = 0; f < kWideTiles; f++) w[f] = W + static_cast<int64_t>(min(n0 + 16 * f + c, N - 1)) * K + 8 * g;
+    for (int f = 0; f < kWideTiles; f++)
+        w[f] = PACKED ? W + static_cast<int64_t>(min(n0 / 16 + f, (N + 15) / 16 - 1)) * (K / 32) * kPackBlock + 8 * lane
+                      : W + static_cast<int64_t>(min(n0 + 16 * f + c, N - 1)) * K + 8 * g;
+    constexpr int wstep = PACKED ? kPackBlock : 32;
     const bool xok = c < M;
     const f16 *x = A + static_cast<int64_t>(min(c, M - 1)) * lda + 8 * g;
     f32x4 acc[kWideTiles];
@@ -259,7 +271,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_wide_kernel(const f16 *__re
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
-            for (int f = 0; f < kWideTiles; f++) wv[u][f] = load_w(w[f] + 32 * (s0 + u * kGemvWaves));
+            for (int f = 0; f < kWideTiles; f++) wv[u][f] = load_w(w[f] + wstep * (s0 + u * kGemvWaves));
 #pragma unroll
         for (int u = 0; u < U; u++)
             xv[u] = xok ? *reinterpret_cast<const f16x8 *>(x + 32 * (s0 + u * kGemvWaves)) : f16x8{};
@@ -352,21 +364,47 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     };
     if (!split && a.M <= 16 && nfb >= kWideMinTiles) {
         const dim3 wide(static_cast<unsigned>((nfb + kWideTiles - 1) / kWideTiles));
-        hipLaunchKernelGGL(gemv_wide_kernel<EP>, wide, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C,
-                           a.ldc);
+        if (a.w_packed)
+            hipLaunchKernelGGL((gemv_wide_kernel<EP, true>), wide, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N,
+                               a.K, a.C, a.ldc);
+        else
+            hipLaunchKernelGGL((gemv_wide_kernel<EP, false>), wide, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N,
+                               a.K, a.C, a.ldc);
         return hipGetLastError();
     }
-    switch ((a.M + 15) / 16 + (split ? 4 : 0)) {
-        case 1: return go(gemv_kernel<1, EP, false>);
-        case 2: return go(gemv_kernel<2, EP, false>);
-        case 3: return go(gemv_kernel<3, EP, false>);
-        case 4: return go(gemv_kernel<4, EP, false>);
-        case 5: return go(gemv_kernel<1, EP, true>);
-        case 6: return go(gemv_kernel<2, EP, true>);
-        case 7: return go(gemv_kernel<3, EP, true>);
-        case 8: return go(gemv_kernel<4, EP, true>);
+    switch ((a.M + 15) / 16 + (split ? 4 : 0) + (a.w_packed ? 8 : 0)) {
+        case 1: return go(gemv_kernel<1, EP, false, false>);
+        case 2: return go(gemv_kernel<2, EP, false, false>);
+        case 3: return go(gemv_kernel<3, EP, false, false>);
+        case 4: return go(gemv_kernel<4, EP, false, false>);
+        case 5: return go(gemv_kernel<1, EP, true, false>);
+        case 6: return go(gemv_kernel<2, EP, true, false>);
+        case 7: return go(gemv_kernel<3, EP, true, false>);
+        case 8: return go(gemv_kernel<4, EP, true, false>);
+        case 9: return go(gemv_kernel<1, EP, false, true>);
+        case 10: return go(gemv_kernel<2, EP, false, true>);
+        case 11: return go(gemv_kernel<3, EP, false, true>);
+        case 12: return go(gemv_kernel<4, EP, false, true>);
+        case 13: return go(gemv_kernel<1, EP, true, true>);
+        case 14: return go(gemv_kernel<2, EP, true, true>);
+        case 15: return go(gemv_kernel<3, EP, true, true>);
+        case 16: return go(gemv_kernel<4, EP, true, true>);
         default: return hipErrorInvalidValue;
     }
+}
+
+// One thread per 16-byte piece of packed W: piece q is lane q % 64 of k step
+// (q / 64) % (K / 32) of tile q / (64 K / 32).
+__global__ void __launch_bounds__(256) gemv_pack_kernel(const f16 *__restrict__ W, int N, int K, int64_t pieces,
+                                                        f16 *__restrict__ out) {
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (q >= pieces) return;
+    const int lane = static_cast<int>(q % 64);
+    const int64_t ks = K / 32, step = (q / 64) % ks, tile = q / (64 * ks);
+    const int64_t row = 16 * tile + lane % 16;
+    f16x8 v = {};
+    if (row < N) v = *reinterpret_cast<const f16x8 *>(W + row * K + 32 * step + 8 * (lane / 16));
+    *reinterpret_cast<f16x8 *>(out + 8 * q) = v;
 }
 
 constexpr int kNormThreads = 256;
@@ -420,6 +458,15 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float 
 }  // namespace
 
 int64_t gemv_workspace_bytes(int M, int N, int K) { return gemv_workspace(M, N, K); }
+
+int64_t gemv_packed_bytes(int N, int K) { return static_cast<int64_t>((N + 15) / 16) * 16 * K * 2; }
+
+hipError_t launch_gemv_pack(const void *W, int N, int K, void *out, hipStream_t stream) {
+    const int64_t pieces = static_cast<int64_t>((N + 15) / 16) * (K / 32) * 64;
+    hipLaunchKernelGGL(gemv_pack_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0, stream,
+                       static_cast<const f16 *>(W), N, K, pieces, static_cast<f16 *>(out));
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream) {
     switch (a.epilogue) {

@@ -356,13 +356,27 @@ def gemv_workspace(M: int, N: int, K: int, device="cuda"):
     return torch.zeros(n, dtype=torch.uint8, device=device) if n > 0 else None
 
 
-def gemv(a, w, c, epilogue: int, stream=None, workspace=None):
+def gemv_pack(w, stream=None):
+    """W (f16 [N, K]) laid out for gemv(..., packed=True): a flat f16 device tensor (N rounded up to 16 rows)."""
+    if w.dtype != torch.float16 or w.dim() != 2:
+        raise EmberError("gemv_pack: w must be f16 [N, K]")
+    N, K = w.shape
+    n = int(_lib.lib().ember_hip_gemv_packed_bytes(N, K))
+    if n <= 0:
+        raise EmberError(f"gemv_pack: K must be a positive multiple of 32 (got {K})")
+    out = torch.empty(n // 2, dtype=torch.float16, device=w.device)
+    check(_lib.lib().ember_hip_gemv_pack(_dev(w, "w"), N, K, out.data_ptr(), _stream_handle(stream)), "gemv_pack")
+    return out
+
+
+def gemv(a, w, c, epilogue: int, stream=None, workspace=None, packed=None):
     """C = A . W^T for decode-sized batches (≙ cuda::gemm with GemmKernel::gemv_tc, k_gemm.cu:302-425).
 
     a: f16 [M, K] (M <= 64, K a multiple of 32); w: f16 [N, K]; c: per epilogue, f16 [M, N] (store_f16),
     f32 [M, N] (store_f32; add_f32 adds into it) or f16 [M, N / 2] (silu_mul, W rows interleaving gate and up).
     workspace: None, or a zeroed device tensor of at least gemv_workspace's size, which lets a shape with few
     output features split K over more work-groups (not shared by launches that overlap in time).
+    packed: None, or gemv_pack(w): the kernel then reads W from that layout (the same bits); w still gives N, K.
     """
     if a.dtype != torch.float16 or w.dtype != torch.float16 or a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
         raise EmberError("gemv: a [M, K] and w [N, K] must be f16 with the same K")
@@ -377,6 +391,8 @@ def gemv(a, w, c, epilogue: int, stream=None, workspace=None):
     g.C, g.ldc, g.epilogue = _dev(c, "c"), cols, epilogue
     if workspace is not None:
         g.workspace, g.workspace_bytes = _dev(workspace, "workspace"), workspace.numel() * workspace.element_size()
+    if packed is not None:
+        g.W, g.w_packed = _dev(packed, "packed w"), 1
     check(_lib.lib().ember_hip_gemv(g, _stream_handle(stream)), "gemv")
 
 

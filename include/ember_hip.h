@@ -238,6 +238,10 @@ typedef struct EmberGemvArgs {
      * not share one. */
     void *workspace;
     int64_t workspace_bytes;
+    /* 0: W is row-major [N, K]. 1: W was laid out by ember_hip_gemv_pack
+     * (no counterpart in the reference): the same product, the same bits, with
+     * every load of W one contiguous KiB. */
+    int32_t w_packed;
 } EmberGemvArgs;
 
 /* C[M, N] = A[M, K] . W[N, K]^T, f16 in, f32 accumulation, then the epilogue
@@ -253,6 +257,17 @@ int ember_hip_gemv(const EmberGemvArgs *args, void *stream);
 /* Bytes of workspace ember_hip_gemv uses for this shape (0: it would not
  * split). No counterpart in the reference. */
 int64_t ember_hip_gemv_workspace_bytes(int32_t M, int32_t N, int32_t K);
+
+/* Bytes of a packed copy of an f16 [N, K] weight (N rounded up to 16 rows). No
+ * counterpart in the reference. */
+int64_t ember_hip_gemv_packed_bytes(int32_t N, int32_t K);
+
+/* Lays out W (f16 [N, K], K a multiple of 32, 16-byte aligned) for
+ * ember_hip_gemv with w_packed = 1: for each 16-row tile and 32-wide k step, the
+ * 64 lanes' 16-byte operand pieces in lane order (lane 16 g + c: row 16 t + c,
+ * columns 32 s + 8 g ..); rows past N are zero. out holds
+ * ember_hip_gemv_packed_bytes(N, K). A backend packs once, at weight load. */
+int ember_hip_gemv_pack(const void *W, int32_t N, int32_t K, void *out, void *stream);
 
 /* The arguments of cuda::rmsnorm_rows (kernels.cuh:70-72). */
 typedef struct EmberNormArgs {

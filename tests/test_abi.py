@@ -103,3 +103,18 @@ def test_gemv_workspace_sizes():
     assert size(1, 256, 512) == 256 + 2 * 16 * 1 * 1024  # 512 / 4 = 128 would leave a wave without a k step
     assert size(3, 130, 256) == 0  # K too short to split
     assert size(65, 2048, 2048) == 0 and size(32, 2048, 40) == 0  # invalid shapes: no workspace
+
+
+def test_gemv_pack_sizes_and_errors():
+    lib = _lib.lib()
+    assert lib.ember_hip_gemv_packed_bytes(4096, 1024) == 4096 * 1024 * 2
+    assert lib.ember_hip_gemv_packed_bytes(37, 64) == 48 * 64 * 2  # rows rounded up to 16
+    assert lib.ember_hip_gemv_packed_bytes(37, 40) == 0
+    assert lib.ember_hip_gemv_pack(None, 16, 64, None, None) == _lib.ERR_INVALID
+    assert lib.ember_hip_gemv_pack(16, 16, 40, 16, None) == _lib.ERR_INVALID
+    assert "multiple of 32" in _lib.last_error()
+    g = _lib.GemvArgs()
+    g.M, g.N, g.K, g.lda, g.ldc, g.epilogue, g.w_packed = 1, 16, 64, 64, 16, 0, 2
+    g.A, g.W, g.C = 16, 16, 16
+    assert lib.ember_hip_gemv(g, None) == _lib.ERR_INVALID
+    assert "w_packed" in _lib.last_error()

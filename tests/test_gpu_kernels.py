@@ -553,6 +553,49 @@ def test_gemv_split_is_deterministic_and_leaves_counters_zero(device):
     assert not ws[: (N // 16) * 4].any()
 
 
+def _pack_reference(w):
+    """The packed layout by its definition: tile t, k step s, lane l = 16 g + c holds w[16 t + c, 32 s + 8 g: +8]."""
+    N, K = w.shape
+    T = (N + 15) // 16
+    wp = np.zeros((T * 16, K), w.dtype)
+    wp[:N] = w
+    return wp.reshape(T, 16, K // 32, 4, 8).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+def test_gemv_pack_layout(device):
+    rng = np.random.default_rng(8)
+    for N, KD in [(16, 32), (37, 64), (4096, 1024)]:
+        w = (rng.standard_normal((N, KD))).astype(np.float16)
+        got = K.gemv_pack(torch.from_numpy(w).to(device)).cpu().numpy()
+        np.testing.assert_array_equal(got.view(np.uint16), _pack_reference(w).view(np.uint16))
+
+
+@pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (16, 1024, 2048), (32, 4096, 2048),
+                                   (8, 1024, 3072), (64, 256, 1024), (3, 70000, 256), (17, 48, 32)])
+@pytest.mark.parametrize("ep", [0, 1, 2, 3])
+def test_gemv_packed_equals_row_major(device, M, N, KD, ep):
+    """A packed W changes only where each lane's 16 bytes come from: the product is the same bits, with and without
+    the K split, in the wide form, and with a ragged last tile (rows past N are zero in the packed copy)."""
+    from ember_amd import _lib
+    rng = np.random.default_rng(M * 17 + N + KD + ep)
+    a = torch.from_numpy(rng.standard_normal((M, KD)).astype(np.float16)).to(device)
+    w = torch.from_numpy((rng.standard_normal((N, KD)) * 0.05).astype(np.float16)).to(device)
+    wp = K.gemv_pack(w)
+    cols = N // 2 if ep == _lib.EPILOGUE_SILU_MUL else N
+    f32 = ep in (_lib.EPILOGUE_STORE_F32, _lib.EPILOGUE_ADD_F32)
+    start = torch.from_numpy(rng.standard_normal((M, cols)).astype(np.float32)).to(device)
+    for split in (False, True):
+        ws = K.gemv_workspace(M, N, KD, device) if split else None
+        outs = []
+        for packed in (None, wp):
+            c = start.clone() if f32 else torch.full((M, cols), float("nan"), dtype=torch.float16, device=device)
+            K.gemv(a, w, c, ep, workspace=ws, packed=packed)
+            outs.append(c)
+        torch.cuda.synchronize()
+        view = torch.int32 if f32 else torch.int16
+        assert torch.equal(outs[0].view(view), outs[1].view(view)), f"split={split}"
+
+
 def test_gemv_saturates_f16_outputs(device):
     """store_f16 clamps to the finite f16 range instead of overflowing to inf (k_gemm.cu's to_half_sat)."""
     a = np.full((2, 64), 100.0, np.float16)
