@@ -123,6 +123,11 @@ class Workload:
             self.h = torch.randn((BATCH, HID), generator=g, device="cuda")
             self.xn = torch.empty((BATCH, HID), device="cuda", dtype=torch.float16)
             self.qkv_buf = torch.empty((BATCH, NQKV), device="cuda", dtype=torch.float16)
+        from ember_amd import kernels as K
+
+        with torch.cuda.stream(self.stream):
+            self.p_qkv = [K.gemv_pack(w, stream=self.stream) for w in self.w_qkv]
+            self.p_o = [K.gemv_pack(w, stream=self.stream) for w in self.w_o]
         ws_bytes = max(int(_lib.lib().ember_hip_gemv_workspace_bytes(BATCH, n, HID)) for n in (NQKV, HID))
         self.gemv_ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")  # both GEMVs, one stream
         torch.cuda.synchronize()  # the zero fill ran on torch's stream
@@ -132,13 +137,14 @@ class Workload:
             n.x, n.w, n.out, n.R, n.hidden, n.eps = (self.h.data_ptr(), self.in_norm[layer].data_ptr(),
                                                      self.xn.data_ptr(), BATCH, HID, 1e-6)
             gq = _lib.GemvArgs()
-            gq.A, gq.lda, gq.W, gq.M, gq.N, gq.K = self.xn.data_ptr(), HID, self.w_qkv[layer].data_ptr(), BATCH, NQKV, HID
+            gq.A, gq.lda, gq.W, gq.M, gq.N, gq.K = self.xn.data_ptr(), HID, self.p_qkv[layer].data_ptr(), BATCH, NQKV, HID
             gq.C, gq.ldc, gq.epilogue = self.qkv_buf.data_ptr(), NQKV, _lib.EPILOGUE_STORE_F16
             go = _lib.GemvArgs()
-            go.A, go.lda, go.W, go.M, go.N, go.K = self.out.data_ptr(), HID, self.w_o[layer].data_ptr(), BATCH, HID, HID
+            go.A, go.lda, go.W, go.M, go.N, go.K = self.out.data_ptr(), HID, self.p_o[layer].data_ptr(), BATCH, HID, HID
             go.C, go.ldc, go.epilogue = self.h.data_ptr(), HID, _lib.EPILOGUE_ADD_F32
             for ga in (gq, go):
                 ga.workspace, ga.workspace_bytes = self.gemv_ws.data_ptr(), ws_bytes
+                ga.w_packed = 1  # the weights as a backend keeps them, in the GEMV's packed layout
             self.block_args.append((ctypes.byref(n), ctypes.byref(gq), ctypes.byref(go), n, gq, go,
                                     self.qn[layer].data_ptr(), self.kn[layer].data_ptr()))
         self.block_weight_bytes = N_LAYERS * (NQKV * HID * 2 + HID * HID * 2)
@@ -458,6 +464,8 @@ def run_linear(args) -> dict:
     # One zeroed workspace for both projections (they never overlap): the o projection's 2048 features split K.
     ws = max((K.gemv_workspace(M, n, HID, dev) for n in (NQKV, HID)),
              key=lambda t: 0 if t is None else t.numel(), default=None)
+    p_qkv = [K.gemv_pack(w) for w in w_qkv]  # W as a backend keeps it: the GEMV's packed layout
+    p_o = [K.gemv_pack(w) for w in w_o]
     torch.cuda.synchronize()
     names = ["rmsnorm_rows", "gemv qkv (store_f16)", "gemv o (add_f32)"]
     ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in names]
@@ -465,8 +473,8 @@ def run_linear(args) -> dict:
 
     def layer(l, timed):
         ops = [lambda: K.rmsnorm_rows(h, norm_w[l], xn, 1e-6),
-               lambda: K.gemv(xn, w_qkv[l], qkv, 0, workspace=ws),
-               lambda: K.gemv(att, w_o[l], h, 2, workspace=ws)]
+               lambda: K.gemv(xn, w_qkv[l], qkv, 0, workspace=ws, packed=p_qkv[l]),
+               lambda: K.gemv(att, w_o[l], h, 2, workspace=ws, packed=p_o[l])]
         for i, op in enumerate(ops):
             if timed:
                 ev[l][i][0].record()

@@ -149,7 +149,8 @@ private:
 
 struct Linear {
     int N = 0, K = 0;
-    const void *w = nullptr;  // f16 [N, K]
+    const void *w = nullptr;  // f16 [N, K], or packed for the GEMV (ember_hip_gemv_pack's layout)
+    bool packed = false;
 };
 
 struct LayerWeights {
@@ -383,6 +384,7 @@ private:
             g.epilogue = ep;
             g.workspace = gemv_ws_.get();
             g.workspace_bytes = static_cast<int64_t>(gemv_ws_.bytes());
+            g.w_packed = W.packed ? 1 : 0;
             check_abi(ember_hip_gemv(&g, stream_), "gemv");
         }
     }
@@ -425,9 +427,11 @@ private:
                       V = c.vocab_size;
         const bool tied = c.tie_embeddings || !st.has("lm_head.weight");
         auto al = [](int64_t bytes) { return static_cast<size_t>((bytes + 255) & ~int64_t(255)); };
-        const size_t per_layer = al(2 * (Q + 2 * KV) * H) + al(2 * H * Q) + al(2 * 2 * I * H) + al(2 * H * I) +
-                                 2 * al(4 * H) + 2 * al(4 * D) + al(4 * (Q + 2 * KV));
-        const size_t bytes = al(2 * V * H) * (tied ? 1 : 2) + al(4 * H) + per_layer * static_cast<size_t>(c.n_layers);
+        auto prow = [](int64_t rows) { return (rows + 15) / 16 * 16; };  // a packed matrix's rows
+        const size_t per_layer = al(2 * prow(Q + 2 * KV) * H) + al(2 * prow(H) * Q) + al(2 * prow(2 * I) * H) +
+                                 al(2 * prow(H) * I) + 2 * al(4 * H) + 2 * al(4 * D) + al(4 * (Q + 2 * KV));
+        const size_t bytes = al(2 * V * H) + (tied ? 0 : al(2 * prow(V) * H)) + al(4 * H) +
+                             per_layer * static_cast<size_t>(c.n_layers);
         size_t free = 0, total = 0;
         HIPB_CHECK(hipMemGetInfo(&free, &total));
         EMBER_CHECK(bytes + (256u << 20) < free, "the model needs {} MiB of GPU memory, {} MiB are free",
@@ -442,9 +446,13 @@ private:
         };
         // A device matrix is assembled on the host as f16 rows and uploaded with one copy: `parts` are
         // (tensor, first destination row, destination row stride) for tensors of `cols` columns.
-        std::vector<uint16_t> staging;
+        // With `packed`, the matrix goes up in ember_hip_gemv_pack's layout instead (its rows rounded up to 16,
+        // the extra rows zero): for 16-row tile t and 32-wide k step s, lane l = 16 g + c's 8 halves are row
+        // 16 t + c, columns 32 s + 8 g ..., the 64 lanes in order.
+        std::vector<uint16_t> staging, packed;
         auto upload_matrix = [&](void *dst, int64_t rows, int64_t cols,
-                                 std::initializer_list<std::tuple<const TensorView *, int64_t, int64_t>> parts) {
+                                 std::initializer_list<std::tuple<const TensorView *, int64_t, int64_t>> parts,
+                                 bool pack = false) {
             staging.assign(static_cast<size_t>(rows * cols), 0);
             for (const auto &[t, first, stride] : parts) {
                 const int64_t n = t->shape.size() == 1 ? 1 : t->shape[0];
@@ -453,7 +461,22 @@ private:
                     for (int64_t k = 0; k < cols; k++)
                         staging[static_cast<size_t>((first + r * stride) * cols + k)] = half_bits(element(*t, r * cols + k));
             }
-            HIPB_CHECK(hipMemcpy(dst, staging.data(), staging.size() * 2, hipMemcpyHostToDevice));
+            if (!pack) {
+                HIPB_CHECK(hipMemcpy(dst, staging.data(), staging.size() * 2, hipMemcpyHostToDevice));
+                return;
+            }
+            EMBER_CHECK(cols % 32 == 0, "a packed matrix needs a multiple of 32 columns (got {})", cols);
+            const int64_t steps = cols / 32;
+            packed.assign(static_cast<size_t>(prow(rows) * cols), 0);
+            size_t q = 0;
+            for (int64_t tile = 0; tile < prow(rows) / 16; tile++)
+                for (int64_t s = 0; s < steps; s++)
+                    for (int lane = 0; lane < 64; lane++, q += 8) {
+                        const int64_t row = 16 * tile + lane % 16;
+                        if (row < rows)
+                            std::copy_n(&staging[static_cast<size_t>(row * cols + 32 * s + 8 * (lane / 16))], 8, &packed[q]);
+                    }
+            HIPB_CHECK(hipMemcpy(dst, packed.data(), packed.size() * 2, hipMemcpyHostToDevice));
         };
         auto upload_vector = [&](const TensorView &t) {
             std::vector<float> v(static_cast<size_t>(t.numel()));
@@ -469,32 +492,33 @@ private:
         if (tied) {
             lm_head_.w = embed_;
         } else {
-            void *w = take(2 * V * H);
-            upload_matrix(w, V, H, {{&st.get("lm_head.weight", {V, H}), 0, 1}});
+            void *w = take(2 * prow(V) * H);
+            upload_matrix(w, V, H, {{&st.get("lm_head.weight", {V, H}), 0, 1}}, true);
             lm_head_.w = w;
+            lm_head_.packed = true;
         }
         final_norm_ = upload_vector(st.get("model.norm.weight", {H}));
         layers_.resize(static_cast<size_t>(c.n_layers));
         for (int l = 0; l < c.n_layers; l++) {
             const std::string p = "model.layers." + std::to_string(l) + ".";
             LayerWeights &L = layers_[static_cast<size_t>(l)];
-            void *qkv = take(2 * (Q + 2 * KV) * H);
+            void *qkv = take(2 * prow(Q + 2 * KV) * H);
             upload_matrix(qkv, Q + 2 * KV, H,
                           {{&st.get(p + "self_attn.q_proj.weight", {Q, H}), 0, 1},
                            {&st.get(p + "self_attn.k_proj.weight", {KV, H}), Q, 1},
-                           {&st.get(p + "self_attn.v_proj.weight", {KV, H}), Q + KV, 1}});
-            L.qkv = {static_cast<int>(Q + 2 * KV), static_cast<int>(H), qkv};
-            void *o = take(2 * H * Q);
-            upload_matrix(o, H, Q, {{&st.get(p + "self_attn.o_proj.weight", {H, Q}), 0, 1}});
-            L.o = {static_cast<int>(H), static_cast<int>(Q), o};
-            void *gu = take(2 * 2 * I * H);
+                           {&st.get(p + "self_attn.v_proj.weight", {KV, H}), Q + KV, 1}}, true);
+            L.qkv = {static_cast<int>(Q + 2 * KV), static_cast<int>(H), qkv, true};
+            void *o = take(2 * prow(H) * Q);
+            upload_matrix(o, H, Q, {{&st.get(p + "self_attn.o_proj.weight", {H, Q}), 0, 1}}, true);
+            L.o = {static_cast<int>(H), static_cast<int>(Q), o, true};
+            void *gu = take(2 * prow(2 * I) * H);
             upload_matrix(gu, 2 * I, H,
                           {{&st.get(p + "mlp.gate_proj.weight", {I, H}), 0, 2},    // even rows
-                           {&st.get(p + "mlp.up_proj.weight", {I, H}), 1, 2}});    // odd rows
-            L.gate_up = {static_cast<int>(2 * I), static_cast<int>(H), gu};
-            void *down = take(2 * H * I);
-            upload_matrix(down, H, I, {{&st.get(p + "mlp.down_proj.weight", {H, I}), 0, 1}});
-            L.down = {static_cast<int>(H), static_cast<int>(I), down};
+                           {&st.get(p + "mlp.up_proj.weight", {I, H}), 1, 2}}, true);    // odd rows
+            L.gate_up = {static_cast<int>(2 * I), static_cast<int>(H), gu, true};
+            void *down = take(2 * prow(H) * I);
+            upload_matrix(down, H, I, {{&st.get(p + "mlp.down_proj.weight", {H, I}), 0, 1}}, true);
+            L.down = {static_cast<int>(H), static_cast<int>(I), down, true};
             L.in_norm = upload_vector(st.get(p + "input_layernorm.weight", {H}));
             L.post_norm = upload_vector(st.get(p + "post_attention_layernorm.weight", {H}));
             if (c.qk_norm) {
