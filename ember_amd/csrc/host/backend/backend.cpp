@@ -34,7 +34,8 @@ int64_t estimate_weight_bytes(const std::string &dir, const BackendOptions &opt)
     const int64_t H = c.hidden, I = c.intermediate;
     const int64_t per_layer = (c.q_dim() + 2LL * c.kv_dim()) * H + H * c.q_dim() + 2 * I * H + H * I;
     const int64_t head = static_cast<int64_t>(c.vocab_size) * H;
-    return 2 * (c.n_layers * per_layer + head * (c.tie_embeddings ? 1 : 2));
+    // The hip backend keeps the embedding table and a packed LM head, tied or not.
+    return 2 * (c.n_layers * per_layer + head * 2);
 }
 
 int64_t gpu_free_memory() {
