@@ -15,7 +15,7 @@
 // 5, ..., and in each group wave w owns tokens 16 (w % 4) .. + 15 of the tile
 // for head w / 4 - four waves per SIMD, so one wave's LDS and MFMA latency
 // hides behind the others'. Keys go in blocks of 32 (two pages): each group
-// stages its block's K rows and V transposed (dims x keys) in its own
+// stages its block's K and V rows (one key each) in its own
 // double-buffered LDS, fetching its next block from HBM while the current one
 // computes; both groups pass one barrier per step. At the end group 1 hands
 // its partial (reference max, row sums, O) through LDS to the group 0 wave
@@ -29,8 +29,9 @@
 //                 when a row's max passes its reference by more than 2^8;
 //   O += P V      P is the A operand as the S^T lanes hold it: lane l's eight
 //                 k-slots are keys {4g..4g+3, 16+4g..16+4g+3} (g = l / 16),
-//                 and V^T in LDS serves exactly those keys per dim, so the
-//                 products pair up (k order inside one MFMA is free).
+//                 and the transposing LDS read (ds_read_b64_tr_b16) of
+//                 the V rows gives lane l exactly those keys of dim l % 16,
+//                 so the products pair up (k order inside one MFMA is free).
 // P is rounded to f16 for the MFMA and the row sums are one more MFMA of the
 // same P against ones, so numerator and denominator agree.
 #include <hip/hip_ext.h>
@@ -47,10 +48,14 @@ template <int HG>
 constexpr int kThreadsFor = 512 * HG;  // two key groups of 4 waves per query head
 constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's partial: O (8), l, m
 constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
-constexpr int kVRow = kKeyBlock + 4;              // LDS row of V^T (one dim), halves: 18 dwords, rows 2 apart 4 banks apart
-constexpr int kVAhead = 2;                        // V^T operand reads in flight ahead of their MFMAs
+constexpr int kVRow = kHeadDim + 16;              // LDS row of V (one key), halves: 72 dwords, rows 8 banks apart
+constexpr int kVAhead = 2;                        // V operand reads in flight ahead of their MFMAs
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+// The transposing LDS read's operand type. Its v4i16 form, with each element
+// bit-cast to f16 after the read, came out of hipcc keeping only the first
+// dword of each read; this form goes straight into the MFMA operand.
+typedef __fp16 tr16x4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 
 // How far a block's max may pass the running reference max (base 2) before
 // the reference moves: P stays below 2^8.
@@ -65,7 +70,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     constexpr int kGroupThreads = kPThreads / 2;       // one key group
     constexpr int kGroupWaves = kGroupThreads / kWave; // 4 x HG: wave w takes tokens 16 (w % 4).. and head w / 4
     constexpr int kWavesP = 2 * kGroupWaves;
-    constexpr int kKBytes = kKeyBlock * kKRow * 2, kVBytes = kHeadDim * kVRow * 2;
+    constexpr int kKBytes = kKeyBlock * kKRow * 2, kVBytes = kKeyBlock * kVRow * 2;
     constexpr int kStageBytes = 2 * 2 * (kKBytes + kVBytes);           // [group][buffer] K and V
     constexpr int kMergeBytes = kGroupWaves * kMergeSlots * kWave * 16;  // group 1's partials, one float4 per slot
     __shared__ __align__(16) unsigned char lds[kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes];
@@ -132,28 +137,22 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     for (int i = 0; i < 8; i++) ones[i] = static_cast<f16>(1.0f);
 
     // A key block's K and V, fetched by its group into registers and later
-    // stored to the group's LDS buffer. K: 512 chunks of 8 dims of one key
-    // (one or two per thread), stored as rows. V: 512 pieces of 4 keys x 2 dims
-    // (dims 2 dp, 2 dp + 1 of keys 4 kq .. 4 kq + 3), each one 4-byte load per
-    // key - a wave's load reads one 256-byte key row - regrouped into two
-    // 8-byte rows of V^T (dims x keys), so V is transposed without sub-dword
-    // LDS stores. A chunk's page (the block's first or second) is the same for
-    // a whole wave, so the block ids are scalar loads and each thread's
-    // offsets inside a page are fixed. Pages past the tile's last position or
-    // outside the pool give zeros, and so do V slots past the last position
-    // (an unwritten slot may hold anything, and P = 0 must not meet a NaN).
+    // stored to the group's LDS buffer. K and V alike: 512 chunks of 8 dims of
+    // one key (one or two per thread, 16-byte loads), stored as rows; the PV
+    // product transposes V as it reads it from LDS. A chunk's page (the
+    // block's first or second) is the same for a whole wave, so the block ids
+    // are scalar loads and each thread's offsets inside a page are fixed.
+    // Pages past the tile's last position or outside the pool give zeros, and
+    // so do V slots past the last position (an unwritten slot may hold
+    // anything, and P = 0 must not meet a NaN).
     constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kGroupThreads;
     const int wl_u = __builtin_amdgcn_readfirstlane(wl);
     const int64_t page_elems = static_cast<int64_t>(a.n_kv) * kPage * kHeadDim;
-    uint32_t koff[kChunks], voff[kChunks];
-    int vkey[kChunks];
+    uint32_t koff[kChunks];
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
         const int chunk = tg + j * kGroupThreads;
         koff[j] = static_cast<uint32_t>((kvh * kPage + (chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8);
-        const int kq = chunk / 64, dp = chunk % 64;
-        voff[j] = static_cast<uint32_t>((kvh * kPage + (4 * kq) % kPage) * kHeadDim + 2 * dp);
-        vkey[j] = 4 * kq;
     }
     auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
         const bool whole = kb * kKeyBlock + kKeyBlock - 1 <= max_pos;  // no slot past the last position
@@ -167,15 +166,8 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
                 if (blk >= 0 && blk < a.num_blocks) {
                     const f16 *kp = kc + blk * page_elems, *vp = vc + blk * page_elems;
                     kv4[j] = *reinterpret_cast<const uint4 *>(kp + koff[j]);
-                    uint32_t w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) w[e] = *reinterpret_cast<const uint32_t *>(vp + voff[j] + e * kHeadDim);
-                    if (!whole) {
-#pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            if (kb * kKeyBlock + vkey[j] + e > max_pos) w[e] = 0;
-                    }
-                    vq[j] = make_uint4(w[0], w[1], w[2], w[3]);
+                    vq[j] = *reinterpret_cast<const uint4 *>(vp + koff[j]);
+                    if (!whole && kb * kKeyBlock + (tg + j * kGroupThreads) / 16 > max_pos) vq[j] = make_uint4(0, 0, 0, 0);
                 }
             }
         }
@@ -187,17 +179,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
             const int chunk = tg + j * kGroupThreads;
             const int key = chunk / 16, d8 = (chunk % 16) * 8;
             *reinterpret_cast<uint4 *>(&kl[key * kKRow + d8]) = kv4[j];
-            // vq = (key e: dim 2dp | dim 2dp+1 << 16), e = 0..3; v_perm picks halves.
-            const int kq = chunk / 64, dp = chunk % 64;
-            const uint2 lo = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x05040100u),
-                                        __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x05040100u));
-            const uint2 hi = make_uint2(__builtin_amdgcn_perm(vq[j].y, vq[j].x, 0x07060302u),
-                                        __builtin_amdgcn_perm(vq[j].w, vq[j].z, 0x07060302u));
-            // The 4-key unit is XOR-swizzled by bit 4 of the dim, so lanes dp and
-            // dp + 8 (rows 36 dwords apart) land on different banks.
-            const int unit = kq ^ ((dp >> 3) & 1);
-            *reinterpret_cast<uint2 *>(&vl[(2 * dp) * kVRow + 4 * unit]) = lo;
-            *reinterpret_cast<uint2 *>(&vl[(2 * dp + 1) * kVRow + 4 * unit]) = hi;
+            *reinterpret_cast<uint4 *>(&vl[key * kVRow + d8]) = vq[j];
         }
     };
 
@@ -265,15 +247,21 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 #pragma unroll
             for (int i = 0; i < 8; i++) pa[i] = static_cast<f16>(exp2_fast(fmaf(sv[i], scale_log2, neg_ref)));
             l_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, ones, l_acc, 0, 0, 0);
-            // The V^T operand of dim tile dt; reads run kVAhead tiles ahead of
+            // The V operand of dim tile dt; reads run kVAhead tiles ahead of
             // their MFMAs. Left to itself the scheduler issues each read next to
             // its MFMA, one LDS round trip per tile; the scheduling barriers keep
             // the reads ahead (3-4% of the launch at configs 3 and 4).
+            // ds_read_b64_tr_b16: in each 16-lane block, lane r reads 4 halves
+            // (row r of a 16 x 4 matrix M) and lane i receives M[4 m + i / 4][i % 4],
+            // m = 0..3. Lane r reading key 4 g + r / 4, dims 16 dt + 4 (r % 4) + 0..3
+            // so hands lane i dim 16 dt + i of keys 4 g + 0..3; the second read
+            // is the same 16 keys on. A half-wave's 8 key rows sit 8 banks apart.
             auto vread = [&](int dt) {
-                const f16 *vrow = &vl[(16 * dt + ql) * kVRow];
-                const int gs = g ^ (dt & 1);  // the staging swizzle: bit 4 of the dim is dt's low bit
-                const f16x4 lo = *reinterpret_cast<const f16x4 *>(vrow + 4 * gs);
-                const f16x4 hi = *reinterpret_cast<const f16x4 *>(vrow + 16 + 4 * gs);
+                const f16 *p = &vl[(4 * g + ql / 4) * kVRow + 16 * dt + 4 * (ql % 4)];
+                typedef __attribute__((address_space(3))) tr16x4 lds_tr16x4;
+                const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr16x4 *)(p)));
+                const f16x4 hi =
+                    __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_tr16x4 *)(p + 16 * kVRow)));
                 return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
             };
             f16x8 vb[kVAhead];
