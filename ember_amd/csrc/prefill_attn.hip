@@ -47,7 +47,10 @@ constexpr int kKeyBlock = 32;                     // keys per LDS block: two pag
 template <int HG>
 constexpr int kThreadsFor = 512 * HG;  // two key groups of 4 waves per query head
 constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's partial: O (8), l, m
-constexpr int kKRow = kHeadDim + 8;               // LDS row of K, halves (272 B: rows land on distinct banks)
+// LDS row of K, halves. 288 B: the score operand's 16-byte reads (rows 16 h + ql,
+// chunk 4 c + g) measured free of bank conflicts, where 272 B rows cost 2.7
+// conflict cycles per read.
+constexpr int kKRow = kHeadDim + 16;
 constexpr int kVRow = kHeadDim + 16;              // LDS row of V (one key), halves: 72 dwords, rows 8 banks apart
 constexpr int kVAhead = 2;                        // V operand reads in flight ahead of their MFMAs
 
