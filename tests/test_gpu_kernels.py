@@ -97,6 +97,46 @@ def test_append_matches_oracle(rng, device, dtype, bias, norm):
         np.testing.assert_allclose(q_out.cpu().numpy(), q_ref, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("heads", [(12, 4), (4, 2)], ids=["12q4kv", "4q2kv"])
+def test_append_waves_mixing_query_and_kv_heads(rng, device, dtype, heads):
+    """A wave holds 8 heads: with 12 / 4 heads its second wave holds 4 query and 4 K heads and its third 4 V heads
+    and 4 dead lanes; with 4 / 2 one wave holds query, K and V heads. Write set, V bits and K against the oracle."""
+    h, kvh = heads
+    NB, w = 48, (h + 2 * kvh) * D
+    step = make_step(rng, [1, 40, 200], [1, 3, 17], NB)
+    qkv = rng.standard_normal((step.T, w)).astype(np.float32)
+    f16 = dtype == torch.float16
+    qkv_in = qkv.astype(np.float16) if f16 else qkv
+    qn = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    inv = oracle.inv_freq(THETA, D)
+    kp = torch.full((NB, kvh, PAGE, D), float("nan"), dtype=torch.float32, device=device).to(dtype)
+    vp = kp.clone()
+    q_out = torch.empty((step.T, h, D), dtype=dtype, device=device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    dv = lambda a: torch.from_numpy(a).to(device)  # noqa: E731
+    K.qk_norm_rope_store(dv(qkv_in), q_out, kp, vp, ints, n_heads=h, n_kv=kvh, inv_freq_dev=dv(inv), q_norm=dv(qn),
+                         k_norm=dv(kn))
+    torch.cuda.synchronize()
+    # The oracle's f16 pools are f16 bits, NaN-filled as the device pools are.
+    ko = np.full((NB, kvh, PAGE, D), np.nan, np.float16).view(np.uint16) if f16 else \
+        np.full((NB, kvh, PAGE, D), np.nan, np.float32)
+    vo = ko.copy()
+    q_ref = oracle.append_layer(qkv_in.astype(np.float32), step.positions, step.query_start, step.tables, ko, vo,
+                                n_heads=h, n_kv=kvh, inv_freq_=inv, q_norm=qn, k_norm=kn, num_blocks=NB, kv_f16=f16)
+    kg, vg = kp.float().cpu().numpy(), vp.float().cpu().numpy()
+    if f16:
+        ko, vo = ko.view(np.float16).astype(np.float32), vo.view(np.float16).astype(np.float32)
+    written = ~np.isnan(ko)
+    assert written.sum() == step.T * kvh * D
+    assert np.array_equal(~np.isnan(kg), written) and np.array_equal(~np.isnan(vg), ~np.isnan(vo))
+    assert np.array_equal(vg[written], vo[written])
+    tol = 2e-3 if f16 else 1e-5  # f16: K within one f16 ulp of the oracle's rounding
+    np.testing.assert_allclose(kg[written], ko[written], rtol=tol, atol=tol)
+    np.testing.assert_allclose(q_out.float().cpu().numpy(), q_ref, rtol=tol, atol=tol)
+
+
 def test_append_far_positions_and_clamp(rng, device):
     """Positions up to 40959 (Qwen3 max), and V beyond the f16 range is clamped to +-65504."""
     NB = 2700  # 2560 + 63 pages for the two contexts
