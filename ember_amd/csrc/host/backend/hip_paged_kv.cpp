@@ -92,8 +92,8 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
         dev_ints_[i] = device_alloc<int32_t>(ints_capacity_);
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming));
-        EMBER_HIP_CHECK(hipEventCreateWithFlags(&consumed_[i], hipEventDisableTiming));
     }
+    for (int i = 0; i < kMarks; i++) EMBER_HIP_CHECK(hipEventCreateWithFlags(&consumed_[i], hipEventDisableTiming));
     EMBER_HIP_CHECK(hipStreamCreateWithFlags(&upload_stream_, hipStreamNonBlocking));  // default priority
     for (int i = 0; i < 2; i++) {  // copy-on-write pair lists: kCowPairs (src, dst) pairs per buffer
         cow_dev_[i] = device_alloc<int32_t>(2 * static_cast<size_t>(kCowPairs));
@@ -101,10 +101,8 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&cow_done_[i], hipEventDisableTiming));
     }
     // every event starts out recorded, so the first plans wait on nothing pending
-    for (int i = 0; i < kStages; i++) {
-        EMBER_HIP_CHECK(hipEventRecord(staged_[i], stream_));
-        EMBER_HIP_CHECK(hipEventRecord(consumed_[i], stream_));
-    }
+    for (int i = 0; i < kStages; i++) EMBER_HIP_CHECK(hipEventRecord(staged_[i], stream_));
+    for (int i = 0; i < kMarks; i++) EMBER_HIP_CHECK(hipEventRecord(consumed_[i], stream_));
     for (int i = 0; i < 2; i++) EMBER_HIP_CHECK(hipEventRecord(cow_done_[i], stream_));
     EMBER_HIP_CHECK(hipStreamSynchronize(stream_));
 }
@@ -121,7 +119,7 @@ HipPagedKv::~HipPagedKv() {
         for (hipEvent_t e : t->events) (void)hipEventDestroy(e);
     for (int i = 0; i < kStages; i++) {
         if (staged_[i]) (void)hipEventDestroy(staged_[i]);
-        if (consumed_[i]) (void)hipEventDestroy(consumed_[i]);
+        if (i < kMarks && consumed_[i]) (void)hipEventDestroy(consumed_[i]);
         if (host_ints_[i]) (void)hipHostFree(host_ints_[i]);
         if (dev_ints_[i]) (void)hipFree(dev_ints_[i]);
     }
@@ -278,10 +276,12 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     }
 
     // Pack into the staging buffer (wait until its previous upload has run), then one copy.
-    // Everything enqueued on stream_ so far reads the previous plan's buffer;
-    // that buffer is reused kStages plans from now, after this event.
-    EMBER_HIP_CHECK(hipEventRecord(consumed_[stage_], stream_));
-    stage_ = (stage_ + 1) % kStages;
+    // Everything enqueued on stream_ so far reads earlier plans' buffers. A mark
+    // on stream_ every kMarkEvery plans records that point: a mark between two
+    // steps idles the GPU for about 5 us, so there is not one per plan.
+    const int64_t n = plans_++;
+    if (n % kMarkEvery == 0) EMBER_HIP_CHECK(hipEventRecord(consumed_[(n / kMarkEvery) % kMarks], stream_));
+    stage_ = static_cast<int>(n % kStages);
     EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));  // its staging buffer is free again
     int32_t *hp = host_ints_[stage_];
     int32_t *dp = dev_ints_[stage_];
@@ -313,7 +313,14 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     // ago), then runs beside stream_'s work. The host, not stream_, waits for
     // it: the host is normally steps ahead, so the wait costs it little, while a
     // cross-stream wait on stream_ idles the GPU for about 10 us per step.
-    EMBER_HIP_CHECK(hipStreamWaitEvent(upload_stream_, consumed_[stage_], 0));
+    if (n >= kStages) {
+        // This buffer's previous plan, n - kStages, had its kernels enqueued
+        // before plan n - kStages + 1; the first mark after it, at plan m
+        // (at most n - kMarkEvery), covers them, and its ring slot is not
+        // recorded again before plan m + kMarks * kMarkEvery > n.
+        const int64_t m = ((n - kStages) / kMarkEvery + 1) * kMarkEvery;
+        EMBER_HIP_CHECK(hipStreamWaitEvent(upload_stream_, consumed_[(m / kMarkEvery) % kMarks], 0));
+    }
     EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, upload_stream_));
     EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], upload_stream_));
     EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));

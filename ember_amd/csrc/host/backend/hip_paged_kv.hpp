@@ -137,14 +137,18 @@ private:
     // pinned staging and copies them up on upload_stream_, so the copy overlaps
     // earlier steps' kernels instead of sitting between the steps on stream_. A
     // buffer is reused kStages plans later, so the host can run kStages - 1
-    // steps ahead of the GPU.
-    static constexpr int kStages = 3;
+    // steps ahead of the GPU. Every kMarkEvery-th plan records a mark on
+    // stream_ (all kernels of the earlier plans); an upload waits for the first
+    // mark recorded after its buffer's previous plan.
+    static constexpr int kStages = 8, kMarkEvery = 4, kMarks = 4;
+    static_assert(kStages >= kMarkEvery && kMarks * kMarkEvery > kStages, "a mark must cover each reuse");
     int32_t *dev_ints_[kStages] = {};
     int32_t *host_ints_[kStages] = {};  // pinned staging, one per dev_ints_ buffer
     hipEvent_t staged_[kStages] = {};   // the upload into each buffer has run
-    hipEvent_t consumed_[kStages] = {}; // the kernels that read each buffer have run
+    hipEvent_t consumed_[kMarks] = {};  // the marks, a ring: plan m's mark in (m / kMarkEvery) % kMarks
     hipStream_t upload_stream_ = nullptr;
     int stage_ = 0;
+    int64_t plans_ = 0;
     int graph_tb_ = 0, graph_wb_ = 0;  // the last plan_graph's buckets
     // copy_blocks' pair lists, double-buffered: pinned staging, the device list
     // the copy kernel reads, and an event recorded after that kernel.
