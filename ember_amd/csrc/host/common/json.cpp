@@ -1,8 +1,10 @@
-// JSON parsing and serialization for the declarations in json.hpp: a
-// recursive-descent parser over the text (RFC 8259: objects, arrays, strings
-// with escapes and surrogate pairs, numbers, literals), and a writer.
+// JSON for the declarations in json.hpp: a recursive-descent parser over the
+// text (RFC 8259: objects, arrays, strings with escapes and surrogate pairs,
+// numbers, literals), the typed accessors over Value's flat record, and a
+// compact writer.
 #include "common/json.hpp"
 
+#include <algorithm>
 #include <charconv>
 #include <cmath>
 #include <cstdio>
@@ -13,18 +15,6 @@
 namespace ember::json {
 
 namespace {
-
-const char *type_name(Value::Type t) {
-    switch (t) {
-        case Value::Type::null: return "null";
-        case Value::Type::boolean: return "a boolean";
-        case Value::Type::number: return "a number";
-        case Value::Type::string: return "a string";
-        case Value::Type::array: return "an array";
-        case Value::Type::object: return "an object";
-    }
-    return "?";
-}
 
 class Parser {
 public:
@@ -228,178 +218,199 @@ private:
     size_t at_ = 0;
 };
 
+// How messages name each kind, indexed by Value::Type.
+constexpr const char *kKindNames[] = {"null", "a boolean", "a number", "a string", "an array", "an object"};
+
+const char *kind_name(Value::Type t) { return kKindNames[static_cast<size_t>(t)]; }
+
+// An optional member: absent or null gives the fallback; otherwise `read` converts it (and checks its kind).
+template <class T, class Read>
+T member_or(const Value &object, std::string_view key, T fallback, Read read) {
+    const Value *member = object.find(key);
+    return member == nullptr || member->is_null() ? fallback : read(*member);
+}
+
+// Integers print exactly; other numbers with 17 significant digits, which round-trip a double. JSON has no
+// infinities or NaNs, so those print as null.
+void append_number(std::string &out, bool exact, int64_t whole, double real) {
+    char buf[32];
+    if (exact) {
+        const auto res = std::to_chars(buf, buf + sizeof buf, whole);
+        out.append(buf, res.ptr);
+    } else if (std::isfinite(real)) {
+        out.append(buf, static_cast<size_t>(std::snprintf(buf, sizeof buf, "%.17g", real)));
+    } else {
+        out += "null";
+    }
+}
+
 }  // namespace
 
 Value Value::parse(std::string_view text) { return Parser(text).document(); }
 
+Value::Value(uint64_t i) : kind_(Type::number), real_(static_cast<double>(i)) {
+    if (i <= static_cast<uint64_t>(INT64_MAX)) {
+        exact_ = true;
+        whole_ = static_cast<int64_t>(i);
+    }
+}
+
+void Value::require(Type want, const char *what) const {
+    if (kind_ != want) fail("JSON: {} needs {}, but the value is {}", what, kind_name(want), kind_name(kind_));
+}
+
 bool Value::as_bool() const {
-    if (!is_bool()) fail("JSON: expected a boolean, found {}", type_name(type()));
-    return std::get<bool>(v_);
+    require(Type::boolean, "as_bool");
+    return truth_;
 }
 
 double Value::as_number() const {
-    if (!is_number()) fail("JSON: expected a number, found {}", type_name(type()));
-    return std::get<Number>(v_).d;
+    require(Type::number, "as_number");
+    return real_;
 }
 
 int64_t Value::as_int() const {
-    if (!is_number()) fail("JSON: expected an integer, found {}", type_name(type()));
-    const Number &n = std::get<Number>(v_);
-    if (n.is_int) return n.i;
-    if (std::trunc(n.d) != n.d || std::fabs(n.d) > 9.2e18) fail("JSON: expected an integer, found {}", n.d);
-    return static_cast<int64_t>(n.d);
+    require(Type::number, "as_int");
+    if (exact_) return whole_;
+    // Written with a fraction or an exponent ("2.0", "1e3"): still an integer if the value is whole and in range.
+    constexpr double kTwo63 = 9223372036854775808.0;
+    if (std::nearbyint(real_) == real_ && real_ >= -kTwo63 && real_ < kTwo63) return static_cast<int64_t>(real_);
+    fail("JSON: as_int needs a whole number, but the value is {}", real_);
 }
 
 const std::string &Value::as_string() const {
-    if (!is_string()) fail("JSON: expected a string, found {}", type_name(type()));
-    return std::get<std::string>(v_);
+    require(Type::string, "as_string");
+    return text_;
 }
 
 const Array &Value::as_array() const {
-    if (!is_array()) fail("JSON: expected an array, found {}", type_name(type()));
-    return std::get<Array>(v_);
+    require(Type::array, "as_array");
+    return items_;
 }
 
 const Object &Value::as_object() const {
-    if (!is_object()) fail("JSON: expected an object, found {}", type_name(type()));
-    return std::get<Object>(v_);
+    require(Type::object, "as_object");
+    return members_;
 }
 
 Array &Value::as_array() {
-    if (!is_array()) fail("JSON: expected an array, found {}", type_name(type()));
-    return std::get<Array>(v_);
+    require(Type::array, "as_array");
+    return items_;
 }
 
 Object &Value::as_object() {
-    if (!is_object()) fail("JSON: expected an object, found {}", type_name(type()));
-    return std::get<Object>(v_);
+    require(Type::object, "as_object");
+    return members_;
 }
 
 const Value *Value::find(std::string_view key) const {
-    if (!is_object()) return nullptr;
-    for (const auto &[k, v] : std::get<Object>(v_))
-        if (k == key) return &v;
-    return nullptr;
+    if (kind_ != Type::object) return nullptr;
+    const auto hit = std::find_if(members_.begin(), members_.end(), [key](const auto &m) { return m.first == key; });
+    return hit == members_.end() ? nullptr : &hit->second;
 }
 
 const Value &Value::operator[](std::string_view key) const {
-    const Value *v = find(key);
-    if (!v) fail("JSON: missing member \"{}\"", std::string(key));
-    return *v;
+    if (const Value *member = find(key)) return *member;
+    fail("JSON: no member named \"{}\"", key);
 }
 
 Value &Value::set(std::string_view key, Value value) {
-    if (is_null()) v_ = Object{};
-    Object &o = as_object();
-    for (auto &[k, v] : o)
-        if (k == key) return v = std::move(value);
-    o.emplace_back(std::string(key), std::move(value));
-    return o.back().second;
+    if (kind_ == Type::null) kind_ = Type::object;
+    require(Type::object, "set");
+    auto slot = std::find_if(members_.begin(), members_.end(), [key](const auto &m) { return m.first == key; });
+    if (slot == members_.end()) slot = members_.insert(members_.end(), {std::string(key), Value()});
+    slot->second = std::move(value);
+    return slot->second;
 }
 
 double Value::get_number(std::string_view key, double def) const {
-    const Value *v = find(key);
-    return v && !v->is_null() ? v->as_number() : def;
+    return member_or(*this, key, def, [](const Value &v) { return v.as_number(); });
 }
 
 int64_t Value::get_int(std::string_view key, int64_t def) const {
-    const Value *v = find(key);
-    return v && !v->is_null() ? v->as_int() : def;
+    return member_or(*this, key, def, [](const Value &v) { return v.as_int(); });
 }
 
 bool Value::get_bool(std::string_view key, bool def) const {
-    const Value *v = find(key);
-    return v && !v->is_null() ? v->as_bool() : def;
+    return member_or(*this, key, def, [](const Value &v) { return v.as_bool(); });
 }
 
 std::string Value::get_string(std::string_view key, std::string_view def) const {
-    const Value *v = find(key);
-    return v && !v->is_null() ? v->as_string() : std::string(def);
+    return member_or(*this, key, std::string(def), [](const Value &v) { return v.as_string(); });
 }
 
 size_t Value::size() const {
-    if (is_array()) return std::get<Array>(v_).size();
-    if (is_object()) return std::get<Object>(v_).size();
-    fail("JSON: size() of {}", type_name(type()));
+    if (kind_ == Type::array) return items_.size();
+    if (kind_ == Type::object) return members_.size();
+    fail("JSON: size needs an array or an object, but the value is {}", kind_name(kind_));
 }
 
 const Value &Value::operator[](size_t i) const {
-    const Array &a = as_array();
-    if (i >= a.size()) fail("JSON: index {} past an array of {}", i, a.size());
-    return a[i];
+    require(Type::array, "operator[](index)");
+    if (i < items_.size()) return items_[i];
+    fail("JSON: index {} is past the end of an array of {} elements", i, items_.size());
 }
 
 void Value::push(Value value) {
-    if (is_null()) v_ = Array{};
-    as_array().push_back(std::move(value));
+    if (kind_ == Type::null) kind_ = Type::array;
+    require(Type::array, "push");
+    items_.push_back(std::move(value));
 }
 
 void write_string(std::string &out, std::string_view s) {
-    out += '"';
-    for (const char c : s) {
-        switch (c) {
-            case '"': out += "\\\""; break;
-            case '\\': out += "\\\\"; break;
-            case '\n': out += "\\n"; break;
-            case '\r': out += "\\r"; break;
-            case '\t': out += "\\t"; break;
-            case '\b': out += "\\b"; break;
-            case '\f': out += "\\f"; break;
-            default:
-                if (static_cast<unsigned char>(c) < 0x20) {
-                    char buf[8];
-                    std::snprintf(buf, sizeof buf, "\\u%04x", static_cast<unsigned>(static_cast<unsigned char>(c)));
-                    out += buf;
-                } else {
-                    out += c;
-                }
+    // Short escapes of the control characters 0x08..0x0D (0x0B has none).
+    constexpr char kShort[] = {'b', 't', 'n', 0, 'f', 'r'};
+    out.push_back('"');
+    for (const char ch : s) {
+        const auto c = static_cast<unsigned char>(ch);
+        if (c == '"' || c == '\\') {
+            out.push_back('\\');
+            out.push_back(ch);
+        } else if (c >= 0x20) {
+            out.push_back(ch);
+        } else if (c >= 0x08 && c <= 0x0D && kShort[c - 0x08] != 0) {
+            out.push_back('\\');
+            out.push_back(kShort[c - 0x08]);
+        } else {
+            char buf[8];
+            out.append(buf, static_cast<size_t>(std::snprintf(buf, sizeof buf, "\\u%04x", static_cast<unsigned>(c))));
         }
     }
-    out += '"';
+    out.push_back('"');
 }
 
 void Value::dump_to(std::string &out) const {
-    switch (type()) {
-        case Type::null: out += "null"; break;
-        case Type::boolean: out += std::get<bool>(v_) ? "true" : "false"; break;
-        case Type::number: {
-            const Number &n = std::get<Number>(v_);
-            char buf[32];
-            if (n.is_int) {
-                std::snprintf(buf, sizeof buf, "%lld", static_cast<long long>(n.i));
-            } else if (!std::isfinite(n.d)) {
-                std::snprintf(buf, sizeof buf, "null");  // JSON has no inf / nan
-            } else {
-                std::snprintf(buf, sizeof buf, "%.17g", n.d);
+    switch (kind_) {
+        case Type::null:
+            out += "null";
+            return;
+        case Type::boolean:
+            out += truth_ ? "true" : "false";
+            return;
+        case Type::number:
+            append_number(out, exact_, whole_, real_);
+            return;
+        case Type::string:
+            write_string(out, text_);
+            return;
+        case Type::array:
+            out.push_back('[');
+            for (size_t i = 0; i < items_.size(); ++i) {
+                if (i > 0) out.push_back(',');
+                items_[i].dump_to(out);
             }
-            out += buf;
-            break;
-        }
-        case Type::string: write_string(out, std::get<std::string>(v_)); break;
-        case Type::array: {
-            out += '[';
-            bool first = true;
-            for (const Value &v : std::get<Array>(v_)) {
-                if (!first) out += ',';
-                first = false;
-                v.dump_to(out);
+            out.push_back(']');
+            return;
+        case Type::object:
+            out.push_back('{');
+            for (size_t i = 0; i < members_.size(); ++i) {
+                if (i > 0) out.push_back(',');
+                write_string(out, members_[i].first);
+                out.push_back(':');
+                members_[i].second.dump_to(out);
             }
-            out += ']';
-            break;
-        }
-        case Type::object: {
-            out += '{';
-            bool first = true;
-            for (const auto &[k, v] : std::get<Object>(v_)) {
-                if (!first) out += ',';
-                first = false;
-                write_string(out, k);
-                out += ':';
-                v.dump_to(out);
-            }
-            out += '}';
-            break;
-        }
+            out.push_back('}');
+            return;
     }
 }
 

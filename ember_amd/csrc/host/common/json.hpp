@@ -1,17 +1,17 @@
-// A JSON value and parser: config.json, generation_config.json and the
-// safetensors header. The declarations are the reference's
-// (src/common/json.hpp:15-92), so ModelConfig::from_json keeps its signature;
-// the implementation (json.cpp) is this build's.
+// A JSON document model for the three files the backend reads: config.json,
+// generation_config.json and a safetensors header. The public declarations are
+// the reference's (src/common/json.hpp:15-92), so ModelConfig::from_json and
+// its callers keep their signatures; the representation below and every
+// definition (json.cpp) are this build's.
 //
-// Objects keep their members in document order and look keys up linearly:
-// the documents read here are small.
+// An object keeps its members in document order and finds a key by a linear
+// scan: these documents hold at most a few thousand members.
 #pragma once
 
 #include <cstdint>
 #include <string>
 #include <string_view>
 #include <utility>
-#include <variant>
 #include <vector>
 
 namespace ember::json {
@@ -26,21 +26,21 @@ public:
 
     Value() = default;
     Value(std::nullptr_t) {}
-    Value(bool b) : v_(b) {}
-    Value(double d) : v_(Number{d, false, 0}) {}
-    Value(int i) : v_(Number{static_cast<double>(i), true, i}) {}
-    Value(int64_t i) : v_(Number{static_cast<double>(i), true, i}) {}
-    Value(uint64_t i) : v_(Number{static_cast<double>(i), true, static_cast<int64_t>(i)}) {}
-    Value(const char *s) : v_(std::string(s)) {}
-    Value(std::string s) : v_(std::move(s)) {}
-    Value(std::string_view s) : v_(std::string(s)) {}
-    Value(Array a) : v_(std::move(a)) {}
-    Value(Object o) : v_(std::move(o)) {}
+    Value(bool b) : kind_(Type::boolean), truth_(b) {}
+    Value(double d) : kind_(Type::number), real_(d) {}
+    Value(int i) : Value(static_cast<int64_t>(i)) {}
+    Value(int64_t i) : kind_(Type::number), exact_(true), real_(static_cast<double>(i)), whole_(i) {}
+    Value(uint64_t i);  // exact when it fits int64_t, else held as a double
+    Value(const char *s) : kind_(Type::string), text_(s) {}
+    Value(std::string s) : kind_(Type::string), text_(std::move(s)) {}
+    Value(std::string_view s) : kind_(Type::string), text_(s) {}
+    Value(Array a) : kind_(Type::array), items_(std::move(a)) {}
+    Value(Object o) : kind_(Type::object), members_(std::move(o)) {}
 
     // Throws ember::Error naming the line and column of the first problem.
     static Value parse(std::string_view text);
 
-    Type type() const { return static_cast<Type>(v_.index()); }
+    Type type() const { return kind_; }
     bool is_null() const { return type() == Type::null; }
     bool is_bool() const { return type() == Type::boolean; }
     bool is_number() const { return type() == Type::number; }
@@ -79,12 +79,18 @@ public:
     void dump_to(std::string &out) const;
 
 private:
-    struct Number {
-        double d;
-        bool is_int;
-        int64_t i;
-    };
-    std::variant<std::monostate, bool, Number, std::string, Array, Object> v_;
+    // Throws unless this value is of kind `want`; `what` names the access.
+    void require(Type want, const char *what) const;
+
+    // One flat record: `kind_` says which of the fields after it holds the value.
+    Type kind_ = Type::null;
+    bool truth_ = false;   // boolean
+    bool exact_ = false;   // number: the text was an integer that fits int64_t, kept in whole_
+    double real_ = 0.0;    // number, as a double (always set)
+    int64_t whole_ = 0;    // number, exactly, when exact_
+    std::string text_;     // string
+    Array items_;          // array
+    Object members_;       // object members, in document order
 };
 
 // Appends s as a JSON string literal.

@@ -1,5 +1,8 @@
-// ModelConfig from a Hugging Face config.json: the fields and checks the
-// reference reads (src/model/config.cpp:10-67), for the Qwen3 / Qwen2 families.
+// ModelConfig from a Hugging Face config.json (and generation_config.json).
+// Behaviour follows the reference's loader (src/model/config.cpp:10-67): the
+// Qwen3 and Qwen2 families, the same keys with the same defaults, the same
+// refusals (rope_scaling, dimensions that cannot form the attention layout) and
+// eos ids taken from generation_config.json first.
 #include "model/config.hpp"
 
 #include <cstdio>
@@ -8,6 +11,60 @@
 #include "common/mmap_file.hpp"
 
 namespace ember {
+
+namespace {
+
+// What the architecture name fixes about the attention layer.
+struct Family {
+    const char *model_type;
+    bool qk_norm;   // RMSNorm on every q / k head vector before RoPE
+    bool qkv_bias;  // biases on the q / k / v projections
+};
+
+constexpr Family kFamilies[] = {
+    {"qwen3", true, false},
+    {"qwen2", false, true},
+};
+
+const Family &family_of(const std::string &model_type) {
+    for (const Family &f : kFamilies)
+        if (model_type == f.model_type) return f;
+    fail("config.json: model_type \"{}\" is not one this backend runs (it runs qwen3 and qwen2)", model_type);
+}
+
+// An integer member that must be present.
+int need_int(const json::Value &doc, const char *key) {
+    const json::Value *v = doc.find(key);
+    if (v == nullptr || v->is_null()) fail("config.json: \"{}\" is missing", key);
+    return static_cast<int>(v->as_int());
+}
+
+int int_or(const json::Value &doc, const char *key, int64_t fallback) {
+    return static_cast<int>(doc.get_int(key, fallback));
+}
+
+// eos_token_id is either one id or a list of ids.
+void append_ids(const json::Value *field, std::vector<int> &ids) {
+    if (field == nullptr || field->is_null()) return;
+    if (!field->is_array()) {
+        ids.push_back(static_cast<int>(field->as_int()));
+        return;
+    }
+    for (size_t i = 0; i < field->size(); ++i) ids.push_back(static_cast<int>((*field)[i].as_int()));
+}
+
+// The shape checks the attention path needs: positive sizes, whole GQA groups, and a RoPE split into two halves.
+void validate(const ModelConfig &m) {
+    const int sizes[] = {m.vocab_size, m.hidden, m.intermediate, m.n_layers, m.n_heads, m.n_kv_heads, m.head_dim};
+    for (const int v : sizes)
+        if (v <= 0) fail("config.json: every model dimension must be positive ({})", m.describe());
+    if (m.n_heads % m.n_kv_heads != 0)
+        fail("config.json: {} query heads do not divide into groups of {} kv heads", m.n_heads, m.n_kv_heads);
+    if (m.head_dim % 2 != 0 || m.head_dim > 256)
+        fail("config.json: head_dim {} is not supported (it must be even and no larger than 256)", m.head_dim);
+}
+
+}  // namespace
 
 int64_t ModelConfig::parameters() const {
     const int64_t H = hidden, I = intermediate, Q = q_dim(), KV = kv_dim();
@@ -19,50 +76,43 @@ int64_t ModelConfig::parameters() const {
     return n_layers * per_layer + embedding * (tie_embeddings ? 1 : 2) + H;  // + the final norm
 }
 
-ModelConfig ModelConfig::from_json(const json::Value &c, const json::Value *gen) {
+ModelConfig ModelConfig::from_json(const json::Value &doc, const json::Value *generation) {
     ModelConfig m;
-    m.arch = c.get_string("model_type", "");
-    EMBER_CHECK(m.arch == "qwen3" || m.arch == "qwen2", "unsupported model_type \"{}\" (supported: qwen3, qwen2)", m.arch);
-    m.vocab_size = static_cast<int>(c["vocab_size"].as_int());
-    m.hidden = static_cast<int>(c["hidden_size"].as_int());
-    m.intermediate = static_cast<int>(c["intermediate_size"].as_int());
-    m.n_layers = static_cast<int>(c["num_hidden_layers"].as_int());
-    m.n_heads = static_cast<int>(c["num_attention_heads"].as_int());
-    m.n_kv_heads = static_cast<int>(c.get_int("num_key_value_heads", m.n_heads));
-    m.head_dim = static_cast<int>(c.get_int("head_dim", m.n_heads > 0 ? m.hidden / m.n_heads : 0));
-    m.rms_eps = static_cast<float>(c.get_number("rms_norm_eps", 1e-6));
-    m.rope_theta = c.get_number("rope_theta", 10000.0);
-    m.max_position = static_cast<int>(c.get_int("max_position_embeddings", 4096));
-    m.tie_embeddings = c.get_bool("tie_word_embeddings", false);
-    m.qk_norm = m.arch == "qwen3";
-    m.qkv_bias = m.arch == "qwen2" || c.get_bool("attention_bias", false);
-    if (const json::Value *rs = c.find("rope_scaling"); rs && !rs->is_null()) fail("rope_scaling is not supported");
-    EMBER_CHECK(m.hidden > 0 && m.n_layers > 0 && m.n_heads > 0 && m.n_kv_heads > 0 && m.head_dim > 0 &&
-                    m.vocab_size > 0 && m.intermediate > 0,
-                "config.json has non-positive dimensions");
-    EMBER_CHECK(m.n_heads % m.n_kv_heads == 0, "num_attention_heads must be a multiple of num_key_value_heads");
-    EMBER_CHECK(m.head_dim % 2 == 0 && m.head_dim <= 256, "head_dim must be even and at most 256");
+    m.arch = doc.get_string("model_type", "");
+    const Family &family = family_of(m.arch);
+    if (const json::Value *scaling = doc.find("rope_scaling"); scaling != nullptr && !scaling->is_null())
+        fail("config.json: rope_scaling is set, and scaled RoPE is not implemented");
 
-    // eos: generation_config.json's eos_token_id wins over config.json's; either may be one id or a list.
-    auto eos_from = [&m](const json::Value *v) {
-        if (!v || v->is_null()) return;
-        if (v->is_array()) {
-            for (const json::Value &e : v->as_array()) m.eos_ids.push_back(static_cast<int>(e.as_int()));
-        } else {
-            m.eos_ids.push_back(static_cast<int>(v->as_int()));
-        }
-    };
-    eos_from(gen ? gen->find("eos_token_id") : nullptr);
-    if (m.eos_ids.empty()) eos_from(c.find("eos_token_id"));
+    // Sizes.
+    m.vocab_size = need_int(doc, "vocab_size");
+    m.hidden = need_int(doc, "hidden_size");
+    m.intermediate = need_int(doc, "intermediate_size");
+    m.n_layers = need_int(doc, "num_hidden_layers");
+    m.n_heads = need_int(doc, "num_attention_heads");
+    m.n_kv_heads = int_or(doc, "num_key_value_heads", m.n_heads);  // absent: plain multi-head attention
+    m.head_dim = int_or(doc, "head_dim", m.n_heads > 0 ? m.hidden / m.n_heads : 0);
+    m.max_position = int_or(doc, "max_position_embeddings", 4096);
+
+    // Numerics and layout switches.
+    m.rms_eps = static_cast<float>(doc.get_number("rms_norm_eps", 1e-6));
+    m.rope_theta = doc.get_number("rope_theta", 10000.0);
+    m.tie_embeddings = doc.get_bool("tie_word_embeddings", false);
+    m.qk_norm = family.qk_norm;
+    m.qkv_bias = family.qkv_bias || doc.get_bool("attention_bias", false);
+    validate(m);
+
+    // Stop tokens: generation_config.json, when it names any, overrides config.json.
+    append_ids(generation != nullptr ? generation->find("eos_token_id") : nullptr, m.eos_ids);
+    if (m.eos_ids.empty()) append_ids(doc.find("eos_token_id"), m.eos_ids);
     return m;
 }
 
 ModelConfig ModelConfig::load(const std::string &dir) {
-    const json::Value config = json::Value::parse(read_file(dir + "/config.json"));
-    const std::string gen_path = dir + "/generation_config.json";
-    if (!file_exists(gen_path)) return from_json(config, nullptr);
-    const json::Value gen = json::Value::parse(read_file(gen_path));
-    return from_json(config, &gen);
+    const json::Value doc = json::Value::parse(read_file(dir + "/config.json"));
+    const std::string generation_path = dir + "/generation_config.json";
+    if (!file_exists(generation_path)) return from_json(doc, nullptr);
+    const json::Value generation = json::Value::parse(read_file(generation_path));
+    return from_json(doc, &generation);
 }
 
 std::string ModelConfig::describe() const {

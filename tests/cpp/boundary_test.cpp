@@ -137,6 +137,20 @@ void json_parser() {
     EXPECT(throws([&] { (void)v["d"].as_int(); }));                      // 0.5 is not an integer
     EXPECT(throws([&] { (void)v["a"].as_string(); }));
     EXPECT(json::Value::parse(v.dump()).dump() == v.dump());             // round trip
+    EXPECT(json::Value::parse("[2.0, 1e3, -4E0]").dump() == "[2,1000,-4]");  // doubles print with %.17g
+    EXPECT(json::Value::parse("1e3").as_int() == 1000 && json::Value::parse("-4E0").as_int() == -4);
+    EXPECT(json::Value(uint64_t{18446744073709551615ULL}).as_number() == 18446744073709551616.0);
+    EXPECT(throws([&] { (void)json::Value(uint64_t{18446744073709551615ULL}).as_int(); }));  // past int64
+    EXPECT(json::Value(std::string("a\x0b\x01\"\\\t")).dump() == "\"a\\u000b\\u0001\\\"\\\\\\t\"");
+    json::Value obj;
+    obj.set("k", 1);
+    obj.set("j", "x");
+    obj.set("k", 2);  // replaces in place, keeps document order
+    EXPECT(obj.dump() == "{\"k\":2,\"j\":\"x\"}" && obj.size() == 2);
+    json::Value list;
+    list.push(true);
+    list.push(json::Value());
+    EXPECT(list.dump() == "[true,null]" && throws([&] { (void)list[2]; }) && throws([&] { (void)json::Value(1).size(); }));
     for (const char *bad : {"{", "[1,]", "{\"a\" 1}", "\"\\ud800\"", "01x", "nul", "\"a\tb\"", "[1] 2"})
         EXPECT(throws([&] { json::Value::parse(bad); }));
     try {
