@@ -529,6 +529,7 @@ def run_backend(args) -> dict:
     Bytes per step: every weight once plus the K/V of every context token."""
     import tempfile
 
+    from ember_amd import _lib
     from ember_amd.backend import BackendOptions, SampleRequest, SamplingParams, create_backend
     from ember_amd.paged_kv import StepBatch
 
@@ -559,6 +560,8 @@ def run_backend(args) -> dict:
     with tempfile.TemporaryDirectory() as td:
         log(f"[bench] writing a synthetic {LAYERS}-layer Qwen3-0.6B-shaped model ({weight_bytes / 1e9:.2f} GB f16)")
         write_model(Path(td), layers=LAYERS, vocab=VOCAB)
+        captures = _lib.lib().ember_backend_graph_captures
+        timed_captures = 0
         for graphs in (True, False):
             be = create_backend(td, BackendOptions(max_batch_tokens=B * PROMPT, max_seqs=B, kv_cache_tokens=B * width * PAGE,
                                                    cuda_graphs=graphs))
@@ -567,12 +570,14 @@ def run_backend(args) -> dict:
             ctx_sum = 0
             for step in range(n_steps):
                 if step == args.warmup:
-                    t0, ctx_sum = time.perf_counter(), 0
+                    t0, ctx_sum, c0 = time.perf_counter(), 0, captures()
                 be.forward(batch([[t] for t in nxt], lens, range(B)))
                 nxt = be.sample(greedy)  # waits for the step's logits
                 lens = [n + 1 for n in lens]
                 ctx_sum += sum(lens)
             wall = time.perf_counter() - t0
+            if graphs:
+                timed_captures = captures() - c0
             be.close()
             results[graphs] = (wall / args.steps, ctx_sum / args.steps)
             log(f"[bench] backend decode, graphs {'on' if graphs else 'off'}: {wall / args.steps * 1e3:.3f} ms/step")
@@ -583,6 +588,7 @@ def run_backend(args) -> dict:
         "value": round(B / step_s, 1), "unit": "tokens/s", "ms_per_step": round(step_s * 1e3, 4),
         "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(step_bytes / step_s / 1e9 / HBM_PEAK_GBS, 4),
         "eager_ms_per_step": round(results[False][0] * 1e3, 4),
+        "graph_captures_timed": timed_captures,
         "config": {"workload": "synthetic Qwen3-0.6B-shaped model (28 layers, tied 151,936 vocabulary), 8 sequences, "
                                "128-token prompts, greedy decode steps (forward + sample) as one replayed graph each; "
                                "eager_ms_per_step: the same steps launched one by one"},
@@ -880,6 +886,7 @@ def main() -> int:
     w.stream.synchronize()
     w.alloc_s = 0.0
     sum_ctx = 0
+    captures0 = w.kv.graph_captures()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -887,6 +894,8 @@ def main() -> int:
     w.stream.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    # graphs captured inside the timed window (a new bucket layout); 0 means every timed step relaunched a kept graph
+    timed_captures = w.kv.graph_captures() - captures0
     alloc_us = w.alloc_s / args.steps * 1e6
 
     w.graph = False  # events cannot sit inside a graph: the timing pass launches layer by layer
@@ -950,6 +959,7 @@ def main() -> int:
             "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
             "split_len": args.split_len,
             "graph": args.graph,
+            "graph_captures": {"total": w.kv.graph_captures(), "timed": timed_captures} if args.graph else None,
             "host_blockmanager_us_per_step": round(alloc_us, 2),
         },
         "roofline": {

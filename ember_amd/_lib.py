@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 5
+ABI_VERSION = 6
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
@@ -186,6 +186,7 @@ PROTOTYPES = {
     "ember_kv_plan": (c_int32, [c_void_p, POINTER(StepBatchC)]),
     "ember_kv_layer": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ember_kv_decode_graph": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(LayerIo), c_int32]),
+    "ember_kv_graph_captures": (c_int64, [c_void_p]),
     "ember_kv_copy_blocks": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), c_int32]),
     "ember_kv_k_pool": (c_void_p, [c_void_p, c_int32]),
     "ember_kv_v_pool": (c_void_p, [c_void_p, c_int32]),
@@ -198,6 +199,7 @@ PROTOTYPES = {
     "ember_backend_create": (c_void_p, [c_char_p, POINTER(BackendOptions)]),
     "ember_backend_destroy": (None, [c_void_p]),
     "ember_backend_graph_replays": (c_int64, []),
+    "ember_backend_graph_captures": (c_int64, []),
     "ember_backend_info": (c_int32, [c_void_p, POINTER(ModelInfo)]),
     "ember_backend_forward": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(c_int32), c_int32]),
     "ember_backend_sample": (c_int32, [c_void_p, POINTER(SampleParams), c_int32, POINTER(c_int32)]),

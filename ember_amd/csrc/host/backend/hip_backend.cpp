@@ -46,7 +46,8 @@ namespace ember {
 
 namespace {
 
-std::atomic<int64_t> g_graph_replays{0};  // whole-step graphs launched, every backend of the process
+std::atomic<int64_t> g_graph_replays{0};   // whole-step graphs launched, every backend of the process
+std::atomic<int64_t> g_graph_captures{0};  // whole-step graphs captured and instantiated
 
 void check_abi(int code, const char *what) {
     if (code != EMBER_OK) fail("{}: {}", what, ember_hip_last_error());
@@ -211,6 +212,8 @@ public:
                     "batch of {} sequences / {} logit rows exceeds the limits", S, R);
         EMBER_CHECK(static_cast<int>(b.positions.size()) == T, "malformed batch: {} positions for {} tokens",
                     b.positions.size(), T);
+        EMBER_CHECK(static_cast<int>(b.tokens.size()) == T, "malformed batch: {} token ids for {} tokens",
+                    b.tokens.size(), T);
         for (int32_t t : b.tokens) EMBER_CHECK(t >= 0 && t < c.vocab_size, "token id {} outside the vocabulary", t);
         for (int32_t r : b.logit_rows) EMBER_CHECK(r >= 0 && r < T, "logit row {} outside the batch", r);
         rows_ = 0;  // until this step's logits exist
@@ -363,6 +366,7 @@ private:
             (void)hipGraphDestroy(graph);
             HIPB_CHECK(inst);
             it = graphs_.emplace(key, exec).first;
+            g_graph_captures.fetch_add(1, std::memory_order_relaxed);
         }
         HIPB_CHECK(hipGraphLaunch(it->second, stream_));
         g_graph_replays.fetch_add(1, std::memory_order_relaxed);
@@ -620,6 +624,7 @@ private:
 }  // namespace
 
 int64_t hip_backend_graph_replays() { return g_graph_replays.load(std::memory_order_relaxed); }
+int64_t hip_backend_graph_captures() { return g_graph_captures.load(std::memory_order_relaxed); }
 
 std::unique_ptr<Backend> create_hip_backend(const std::string &dir, const BackendOptions &opt) {
     return std::make_unique<HipBackend>(dir, opt);

@@ -93,6 +93,7 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
         EMBER_HIP_CHECK(hipHostMalloc(reinterpret_cast<void **>(&host_ints_[i]), ints_capacity_ * sizeof(int32_t), 0));
         EMBER_HIP_CHECK(hipEventCreateWithFlags(&staged_[i], hipEventDisableTiming));
     }
+    graph_ints_ = device_alloc<int32_t>(ints_capacity_);
     for (int i = 0; i < kMarks; i++) EMBER_HIP_CHECK(hipEventCreateWithFlags(&consumed_[i], hipEventDisableTiming));
     EMBER_HIP_CHECK(hipStreamCreateWithFlags(&upload_stream_, hipStreamNonBlocking));  // default priority
     for (int i = 0; i < 2; i++) {  // copy-on-write pair lists: kCowPairs (src, dst) pairs per buffer
@@ -128,7 +129,7 @@ HipPagedKv::~HipPagedKv() {
         if (cow_host_[i]) (void)hipHostFree(cow_host_[i]);
         if (cow_dev_[i]) (void)hipFree(cow_dev_[i]);
     }
-    for (void *p : {k_, v_, q_, static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
+    for (void *p : {k_, v_, q_, static_cast<void *>(graph_ints_), static_cast<void *>(inv_freq_), static_cast<void *>(part_acc_),
                     static_cast<void *>(part_ml_), static_cast<void *>(merge_counters_)})
         if (p) (void)hipFree(p);
 }
@@ -324,6 +325,12 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     EMBER_HIP_CHECK(hipMemcpyAsync(dp, hp, off * sizeof(int32_t), hipMemcpyHostToDevice, upload_stream_));
     EMBER_HIP_CHECK(hipEventRecord(staged_[stage_], upload_stream_));
     EMBER_HIP_CHECK(hipEventSynchronize(staged_[stage_]));
+    if (graph_splits > 0) {
+        // A graph plan: the kernels read the fixed graph block, refreshed on stream_ behind the launches of
+        // earlier plans (the upload it copies has completed: the host waited for it above).
+        EMBER_HIP_CHECK(hipMemcpyAsync(graph_ints_, dp, off * sizeof(int32_t), hipMemcpyDeviceToDevice, stream_));
+        dp = graph_ints_;
+    }
     d_positions_ = dp + at[0];
     d_token_seq_ = dp + at[1];
     d_tables_ = dp + at[2];
@@ -513,6 +520,7 @@ bool HipPagedKv::decode_graph(const StepBatch &b, std::span<const LayerIo> io) {
         (void)hipGraphDestroy(graph);
         EMBER_HIP_CHECK(inst);
         it = graphs_.emplace(key, std::move(e)).first;
+        graph_captures_++;
     }
     EMBER_HIP_CHECK(hipGraphLaunch(it->second.exec, stream_));
     return true;
@@ -529,8 +537,8 @@ int HipPagedKv::graph_bucket(const StepBatch &b) const {
 }
 
 uint64_t HipPagedKv::graph_key() const {
-    return (static_cast<uint64_t>(graph_tb_) << 34) | (static_cast<uint64_t>(graph_wb_) << 2) |
-           static_cast<uint64_t>(stage_);
+    // Within a bucket pair every array of the plan has the same length, so the same offsets in the graph block.
+    return (static_cast<uint64_t>(graph_tb_) << 32) | static_cast<uint64_t>(graph_wb_);
 }
 
 int HipPagedKv::plan_graph(const StepBatch &b) {

@@ -65,9 +65,9 @@ public:
     // tokens are sequences of length 1 at position 0 on the spare block, and the
     // splits follow the width bucket, so a replay always matches its capture.
     // qkv and out of every layer must hold token_bucket(T) rows (64 suffice);
-    // rows past T are padding. Graphs are kept per (bucket pair, staging buffer)
-    // and captured again when the layer buffers change. Returns false, with
-    // nothing enqueued, when the step is not a pure decode step of <= 64 tokens.
+    // rows past T are padding. Graphs are kept per bucket pair and captured
+    // again when the layer buffers change. Returns false, with nothing
+    // enqueued, when the step is not a pure decode step of <= 64 tokens.
     bool decode_graph(const StepBatch &b, std::span<const LayerIo> io);
     // The planning half of decode_graph, for a caller that captures more than
     // the attention layers (a backend's whole model step): the token bucket
@@ -80,6 +80,9 @@ public:
     // captured graph replays either.
     int plan_graph(const StepBatch &b);
     uint64_t graph_key() const;
+    // Graphs decode_graph has captured (and instantiated) so far; a launch of a
+    // kept graph does not count.
+    int64_t graph_captures() const { return graph_captures_; }
     static int token_bucket(int T);
     int width_bucket(int w) const;
 
@@ -150,6 +153,12 @@ private:
     int stage_ = 0;
     int64_t plans_ = 0;
     int graph_tb_ = 0, graph_wb_ = 0;  // the last plan_graph's buckets
+    // A graph plan's kernels read their integers from this one block, not from
+    // the staging ring: the plan copies its stage here on stream_ (so after
+    // every earlier graph launch has read it), and one graph per bucket pair
+    // replays whatever stage the ring gave the step.
+    int32_t *graph_ints_ = nullptr;
+    int64_t graph_captures_ = 0;
     // copy_blocks' pair lists, double-buffered: pinned staging, the device list
     // the copy kernel reads, and an event recorded after that kernel.
     static constexpr int kCowPairs = 4096;

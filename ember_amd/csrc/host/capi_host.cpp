@@ -15,6 +15,7 @@
 
 namespace ember {
 int64_t hip_backend_graph_replays();  // hip_backend.cpp
+int64_t hip_backend_graph_captures();  // hip_backend.cpp
 }
 #include "common/error.hpp"
 #include "ember_hip.h"
@@ -213,6 +214,8 @@ int32_t ember_kv_decode_graph(EmberPagedKv *h, const EmberStepBatch *b, const Em
     });
 }
 
+int64_t ember_kv_graph_captures(const EmberPagedKv *h) { return h ? h->kv.graph_captures() : -1; }
+
 int32_t ember_kv_layer(EmberPagedKv *h, int32_t layer, const void *qkv, const float *q_norm, const float *k_norm,
                        const float *bias, void *out) {
     return guarded("kv_layer", [&] {
@@ -305,6 +308,7 @@ EmberBackend *ember_backend_create(const char *model_dir, const EmberBackendOpti
 void ember_backend_destroy(EmberBackend *h) { delete h; }
 
 int64_t ember_backend_graph_replays(void) { return ember::hip_backend_graph_replays(); }
+int64_t ember_backend_graph_captures(void) { return ember::hip_backend_graph_captures(); }
 
 int32_t ember_backend_info(const EmberBackend *h, EmberModelInfo *out) {
     return guarded("backend_info", [&] {

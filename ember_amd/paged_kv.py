@@ -94,6 +94,10 @@ class PagedKv:
         check(code, "kv_decode_graph")
         return True
 
+    def graph_captures(self) -> int:
+        """Graphs decode_graph has captured on this path so far (a launch of a kept graph does not count)."""
+        return int(_lib.lib().ember_kv_graph_captures(self._h))
+
     def layer(self, layer: int, qkv: torch.Tensor, out: torch.Tensor, q_norm=None, k_norm=None, bias=None) -> None:
         for t in (qkv, out):
             if not t.is_cuda or not t.is_contiguous() or t.dtype != self.dtype:

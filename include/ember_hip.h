@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 5
+#define EMBER_ABI_VERSION 6
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
@@ -458,6 +458,10 @@ typedef struct EmberLayerIo {
  * enqueued: use ember_kv_plan + ember_kv_layer), or an error. */
 int32_t ember_kv_decode_graph(EmberPagedKv *kv, const EmberStepBatch *batch, const EmberLayerIo *layers,
                               int32_t n_layers);
+/* Graphs ember_kv_decode_graph has captured so far on this path (launches of a
+ * kept graph do not count); -1 for a NULL handle. No counterpart in the
+ * reference: a diagnostic for tests and benchmarks. */
+int64_t ember_kv_graph_captures(const EmberPagedKv *kv);
 /* Device copies of whole pages, src[i] -> dst[i] (host arrays of n blocks), all layers. */
 int32_t ember_kv_copy_blocks(EmberPagedKv *kv, const int32_t *src, const int32_t *dst, int32_t n);
 void *ember_kv_k_pool(EmberPagedKv *kv, int32_t layer);
@@ -514,6 +518,9 @@ int32_t ember_backend_info(const EmberBackend *backend, EmberModelInfo *out);
 /* Whole-step decode graphs replayed so far by every backend of the process
  * (no counterpart in the reference; a diagnostic for tests and benchmarks). */
 int64_t ember_backend_graph_replays(void);
+/* Whole-step decode graphs captured and instantiated so far by every backend
+ * of the process: one per planned layout (token bucket, table-width bucket). */
+int64_t ember_backend_graph_captures(void);
 /* Backend::forward (backend.hpp:104-106): appends every token's K/V and keeps
  * the logits of the n_rows tokens logit_rows[] on the device. */
 int32_t ember_backend_forward(EmberBackend *backend, const EmberStepBatch *batch, const int32_t *logit_rows,

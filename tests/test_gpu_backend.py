@@ -185,8 +185,10 @@ def test_decode_steps_replay_one_graph_and_equal_eager(model):
     """A pure decode step (one token per sequence, every token a logit row in order) replays one hipGraph of the whole
     model step, as the reference's forward does (cuda_backend.cu:145-149, :402-454): padded to the token bucket with
     spare-block rows. Its real rows' logits equal the eager step's bit for bit (graphs off, same model, same steps):
-    five sequences (bucket 6, one padding row), then four (bucket 4). A step whose logit rows are not every token in
-    order runs eagerly, and so does every step with graphs off (the replay counter shows which)."""
+    five sequences (bucket 6, one padding row) for 12 steps, then four (bucket 4) for 4. A step whose logit rows are not
+    every token in order runs eagerly, and so does every step with graphs off (the replay counter shows which). Each
+    layout is captured once and its graph relaunched after: the first bucket runs for more steps than the planner's
+    staging ring has buffers, so the kept graph reads step integers staged through every buffer."""
     from ember_amd import _lib
 
     d, _ = model
@@ -194,6 +196,8 @@ def test_decode_steps_replay_one_graph_and_equal_eager(model):
     bg = create_backend(str(d), BackendOptions(**opts))  # graphs on: the reference's default
     be = create_backend(str(d), BackendOptions(cuda_graphs=False, **opts))
     replays = _lib.lib().ember_backend_graph_replays
+    captures = _lib.lib().ember_backend_graph_captures
+    captured0 = captures()
     rng = np.random.default_rng(11)
     lens = [40, 70, 17, 33, 5]
     width = 8  # pages per table row: room for every prompt plus the decodes
@@ -207,8 +211,8 @@ def test_decode_steps_replay_one_graph_and_equal_eager(model):
     assert nxt == [int(np.argmax(bg.logits(r))) for r in range(5)]
     cur = list(lens)
     graphs_run = 0
-    for step in range(9):
-        S = 5 if step < 6 else 4
+    for step in range(16):
+        S = 5 if step < 12 else 4
         logit_rows = [0, 2] if step == 3 else list(range(S))
         b = _multi_batch([[t] for t in nxt[:S]], cur[:S], firsts[:S], width, logit_rows)
         before = replays()
@@ -218,11 +222,12 @@ def test_decode_steps_replay_one_graph_and_equal_eager(model):
         graph_step = step != 3
         assert replays() == before + (1 if graph_step else 0)
         graphs_run += graph_step
+        assert captures() - captured0 == (1 if step < 12 else 2), f"step {step}: one capture per layout"
         for i in range(len(logit_rows)):
             np.testing.assert_array_equal(bg.logits(i), be.logits(i), err_msg=f"step {step} row {i}")
         got = {r: int(np.argmax(be.logits(i))) for i, r in enumerate(logit_rows)}
         nxt = [got.get(r, 7) for r in range(S)] + nxt[S:]
         cur = [c + 1 for c in cur[:S]] + cur[S:]
-    assert graphs_run == 8
+    assert graphs_run == 15
     bg.close()
     be.close()

@@ -333,7 +333,9 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
     same graph replayed step after step with eager work in between, and new graphs when the batch moves
     to another bucket. Only the spare block differs (the padding writes there and nowhere else). Every
     replay's outputs are also checked against the oracle (2e-3 f16, 1e-5 f32) on a snapshot of the pages
-    the step reads."""
+    the step reads. A graph is captured once per (token bucket, width bucket) and then relaunched: the
+    first bucket runs for more steps than the planner's staging ring has buffers, so its kept graph is
+    launched with step integers staged through every buffer of the ring."""
     L, NB, maxpos = 2, 700, 2048
     mk = lambda: PagedKv(n_layers=L, n_heads=H, n_kv_heads=KVH, rms_eps=EPS, rope_theta=THETA,  # noqa: E731
                          max_position=maxpos, num_blocks=NB, max_batch_tokens=64, max_seqs=64, dtype=dtype)
@@ -347,12 +349,21 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
     ctx = [int(c) for c in rng.integers(1, 240, 9)]  # tokens cached per sequence
     blocks = [[] for _ in ctx]
     free = list(rng.permutation(NB))
-    # active sequences per step: same bucket (replays), then 7 -> bucket 8, 3 -> bucket 3; contexts grow past
-    # 256 tokens (width bucket 16 -> 64 blocks) on the way
-    active_per_step = [5, 5, 5, 7, 7, 3, 3, 9]
+    # active sequences per step: same bucket (replays) for 11 steps, then 7 -> bucket 8, 3 -> bucket 3; contexts
+    # grow past 256 tokens (width bucket 16 -> 64 blocks) on the way
+    active_per_step = [5] * 11 + [7, 7, 3, 3, 9]
+    buckets = (1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 40, 48, 56, 64)
+
+    def width_bucket(w):  # HipPagedKv::width_bucket: 16 * 4^k blocks, at most the table's width
+        b = 16
+        while b < w:
+            b *= 4
+        return min(b, maxpos // PAGE)
+
+    keys = set()
     for step, n_act in enumerate(active_per_step):
         seqs = list(range(n_act))
-        if step == 4:
+        if step == 12:
             for s in seqs:
                 ctx[s] += 200  # jump: as if many steps had passed
         for s in seqs:
@@ -370,7 +381,9 @@ def test_decode_graph_equals_plan_and_layer(rng, device, dtype):
             qkv[l][:n_act] = torch.from_numpy(acts[l]).to(device, dtype)
         # the oracle's view of the pages this step reads, before the step (both worlds hold the same pages)
         snaps = [snapshot(eb, l, tables, (pos + PAGE) // PAGE) for l in range(L)]
+        keys.add((next(b for b in buckets if b >= n_act), width_bucket(mb)))
         assert ga.decode_graph(batch, io)
+        assert ga.graph_captures() == len(keys), f"step {step}: one capture per bucket pair, relaunched after"
         eb.plan(batch)
         for l in range(L):
             eb.layer(l, qkv[l][:n_act], out_e[l][:n_act], q_norm=qn[l], k_norm=kn[l])
