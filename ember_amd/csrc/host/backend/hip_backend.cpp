@@ -212,8 +212,6 @@ public:
                     "batch of {} sequences / {} logit rows exceeds the limits", S, R);
         EMBER_CHECK(static_cast<int>(b.positions.size()) == T, "malformed batch: {} positions for {} tokens",
                     b.positions.size(), T);
-        EMBER_CHECK(static_cast<int>(b.tokens.size()) == T, "malformed batch: {} token ids for {} tokens",
-                    b.tokens.size(), T);
         for (int32_t t : b.tokens) EMBER_CHECK(t >= 0 && t < c.vocab_size, "token id {} outside the vocabulary", t);
         for (int32_t r : b.logit_rows) EMBER_CHECK(r >= 0 && r < T, "logit row {} outside the batch", r);
         rows_ = 0;  // until this step's logits exist
