@@ -187,8 +187,6 @@ PROTOTYPES = {
     "ember_kv_layer": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ember_kv_decode_graph": (c_int32, [c_void_p, POINTER(StepBatchC), POINTER(LayerIo), c_int32]),
     "ember_kv_graph_captures": (c_int64, [c_void_p]),
-    "ember_kv_dispatch_order": (c_int32, [POINTER(c_int32), c_int32, c_int32, c_int32, c_int32, POINTER(c_int32), c_int32,
-                                         POINTER(c_int32)]),
     "ember_kv_copy_blocks": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32), c_int32]),
     "ember_kv_k_pool": (c_void_p, [c_void_p, c_int32]),
     "ember_kv_v_pool": (c_void_p, [c_void_p, c_int32]),

@@ -6,9 +6,6 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
-#include <functional>
-#include <numeric>
-#include <queue>
 
 #include "common/error.hpp"
 #include "kernels.hpp"
@@ -38,49 +35,6 @@ size_t pad32(size_t n) { return (n + 31) & ~size_t(31); }
 
 }  // namespace
 
-std::vector<int> decode_dispatch_order(std::span<const int> pages, int n_kv, int n_cu, int slots_per_cu) {
-    const int n = static_cast<int>(pages.size());
-    std::vector<int> order(static_cast<size_t>(n));
-    std::iota(order.begin(), order.end(), 0);
-    auto larger = [&](int a, int b) { return pages[static_cast<size_t>(a)] > pages[static_cast<size_t>(b)]; };
-    auto smaller = [&](int a, int b) { return pages[static_cast<size_t>(a)] < pages[static_cast<size_t>(b)]; };
-    std::stable_sort(order.begin(), order.end(), larger);
-    if (n_kv <= 0 || n_cu <= 0 || n_cu % n_kv != 0 || slots_per_cu <= 0) return order;
-    const int cols = n_cu / n_kv, rounds = slots_per_cu, first_round = cols * rounds;
-    if (n <= cols || n > 2 * first_round) return order;
-    // Largest first onto the least loaded column (lowest index on ties); within one round a column holds at most
-    // `rounds` items.
-    const bool capped = n <= first_round;
-    std::vector<std::vector<int>> col(static_cast<size_t>(cols));
-    using Entry = std::pair<int64_t, int>;  // (load, column)
-    std::priority_queue<Entry, std::vector<Entry>, std::greater<Entry>> open;
-    for (int c = 0; c < cols; c++) open.push({0, c});
-    for (const int i : order) {
-        const auto [load, c] = open.top();
-        open.pop();
-        std::vector<int> &items = col[static_cast<size_t>(c)];
-        items.push_back(i);
-        if (!capped || static_cast<int>(items.size()) < rounds) open.push({load + pages[static_cast<size_t>(i)], c});
-    }
-    // Each column smallest first: its first slots free early, where the extra items land.
-    for (std::vector<int> &items : col) std::stable_sort(items.begin(), items.end(), smaller);
-    std::vector<int> out;
-    out.reserve(static_cast<size_t>(first_round + n));
-    for (int k = 0; k < rounds; k++)
-        for (int c = 0; c < cols; c++) {
-            const std::vector<int> &items = col[static_cast<size_t>(c)];
-            out.push_back(k < static_cast<int>(items.size()) ? items[static_cast<size_t>(k)] : -1);
-        }
-    std::vector<int> extra;
-    for (const std::vector<int> &items : col)
-        extra.insert(extra.end(), items.begin() + std::min<ptrdiff_t>(rounds, static_cast<ptrdiff_t>(items.size())),
-                     items.end());
-    std::stable_sort(extra.begin(), extra.end(), larger);
-    out.insert(out.end(), extra.begin(), extra.end());
-    while (!out.empty() && out.back() < 0) out.pop_back();
-    return out;
-}
-
 HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStream_t stream)
     : cfg_(cfg), opt_(opt), stream_(stream) {
     EMBER_CHECK(cfg_.head_dim == 128, "the paged-KV path needs head_dim 128 (got {})", cfg_.head_dim);
@@ -95,9 +49,6 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_CHECK(opt_.max_batch_tokens > 0 && opt_.max_seqs > 0, "bad batch limits");
     EMBER_CHECK(cfg_.max_position > 0, "max_position must be set");
     elem_ = opt_.dtype == EMBER_DTYPE_F16 ? 2 : 4;
-    int device = 0;
-    EMBER_HIP_CHECK(hipGetDevice(&device));
-    EMBER_HIP_CHECK(hipDeviceGetAttribute(&n_cu_, hipDeviceAttributeMultiprocessorCount, device));
 
     const int64_t block_elems = static_cast<int64_t>(cfg_.n_kv_heads) * kBlockSize * cfg_.head_dim;
     layer_elems_ = block_elems * (opt_.num_blocks + 1);  // + the spare block
@@ -266,25 +217,24 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     fused_ = fused_ && tiles_ == 0 && decode_count_ == T;
     splits_ = graph_splits > 0 ? graph_splits : std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
 
-    // Decode work items (run, split) and the pages each reads, launched in the
-    // order decode_dispatch_order gives for this kernel instance's occupancy
-    // (a graph's list keeps the plain largest-first order: its length is fixed).
+    // Decode work items (run, split), dispatched in list order: every full
+    // split first, then the partial last splits, longest first, so the short
+    // ones fill the tail of the launch.
     work_.clear();
-    std::vector<std::pair<int, int>> items;  // (run, split)
-    std::vector<int> pages;
+    std::vector<std::pair<int, int>> partial;  // (keys, run)
     for (int r = 0; r < decode_runs_; r++) {
         const int ctx = run_ctx_[static_cast<size_t>(r)];
-        for (int s = 0; s * opt_.split_len < ctx; s++) {
-            items.emplace_back(r, s);
-            pages.push_back((std::min(opt_.split_len, ctx - s * opt_.split_len) + kBlockSize - 1) / kBlockSize);
+        const int full = ctx / opt_.split_len;
+        for (int s = 0; s < full; s++) {
+            work_.push_back(r);
+            work_.push_back(s);
         }
+        if (ctx % opt_.split_len) partial.emplace_back(ctx % opt_.split_len, r);
     }
-    const int rows = hip::decode_rows(cfg_.group(), max_run_);
-    const std::vector<int> order = decode_dispatch_order(
-        pages, cfg_.n_kv_heads, n_cu_, graph_splits > 0 || items.empty() ? 0 : decode_slots(rows, fused_));
-    for (const int i : order) {
-        work_.push_back(i < 0 ? -1 : items[static_cast<size_t>(i)].first);
-        work_.push_back(i < 0 ? -1 : items[static_cast<size_t>(i)].second);
+    std::stable_sort(partial.begin(), partial.end(), [](const auto &a, const auto &b) { return a.first > b.first; });
+    for (const auto &[keys, r] : partial) {
+        work_.push_back(r);
+        work_.push_back(run_ctx_[static_cast<size_t>(r)] / opt_.split_len);
     }
     if (graph_splits > 0) {  // the graph's fixed-length list: padding items name no run
         EMBER_CHECK(static_cast<int>(work_.size() / 2) <= decode_runs_ * graph_splits, "internal: graph work list");
@@ -394,13 +344,6 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     d_work_desc_ = dp + at[10];
     d_tokens_ = b.tokens.size() == static_cast<size_t>(T) ? dp + at[11] : nullptr;
     d_logit_rows_ = dp + at[12];
-}
-
-int HipPagedKv::decode_slots(int rows, bool fused) {
-    const int key = (opt_.dtype * 64 + rows) * 2 + (fused ? 1 : 0);
-    auto it = decode_slots_.find(key);
-    if (it == decode_slots_.end()) it = decode_slots_.emplace(key, hip::decode_slots_per_cu(opt_.dtype, rows, fused)).first;
-    return it->second;
 }
 
 void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float *k_norm, const float *bias, void *out) {

@@ -36,22 +36,6 @@ struct PagedKvOptions {
     bool use_prefill_kernel = true;   // route runs of >= 16 tokens to MFMA tiles (f16 pools; f32 always decodes)
 };
 
-// The order in which the decode kernel's work-groups are launched, for a
-// dispatcher that places work-group b on the CU of b mod n_cu while every CU
-// still has a free slot, and later work-groups on whichever slot frees first.
-// pages[i]: the pages item i reads (its cost); each item is n_kv work-groups
-// (one per kv head), consecutive in the grid, so item position q lands in CU
-// column q mod (n_cu / n_kv) in round q / (n_cu / n_kv). Returns item indices in
-// launch order; -1 marks an empty item (its work-groups exit at once) that
-// keeps a column's later items in place. Within one round or less of work the
-// items are packed onto the columns largest first, each onto the least loaded;
-// with an overflow of up to one more round, columns keep their extra items for
-// last and run their smallest items first, so the slots that free first (and
-// take the extra items) are on the light columns. Otherwise (more rounds, or a
-// layout the column model does not cover): largest first. Only the order
-// changes, never an item's arithmetic.
-std::vector<int> decode_dispatch_order(std::span<const int> pages, int n_kv, int n_cu, int slots_per_cu);
-
 class HipPagedKv {
 public:
     static constexpr int kFlashMinTokens = 16;  // a run this long uses prefill tiles (cuda_backend.cu:257)
@@ -183,10 +167,6 @@ private:
     hipEvent_t cow_done_[2] = {nullptr, nullptr};
     int cow_stage_ = 0;
     size_t ints_capacity_ = 0;
-
-    int n_cu_ = 0;                   // compute units of the device (the dispatch model's columns)
-    std::map<int, int> decode_slots_;  // work-groups per CU by decode instance (dtype, rows, fused)
-    int decode_slots(int rows, bool fused);
 
     // The current plan (device addresses into dev_ints_[stage_]).
     int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;

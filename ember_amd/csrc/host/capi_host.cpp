@@ -216,20 +216,6 @@ int32_t ember_kv_decode_graph(EmberPagedKv *h, const EmberStepBatch *b, const Em
 
 int64_t ember_kv_graph_captures(const EmberPagedKv *h) { return h ? h->kv.graph_captures() : -1; }
 
-int32_t ember_kv_dispatch_order(const int32_t *pages, int32_t n, int32_t n_kv, int32_t n_cu, int32_t slots_per_cu,
-                                int32_t *order, int32_t capacity, int32_t *count) {
-    return guarded("kv_dispatch_order", [&] {
-        EMBER_CHECK(n >= 0 && (n == 0 || pages) && order && count && capacity >= 0, "null or negative arguments");
-        for (int32_t i = 0; i < n; i++) EMBER_CHECK(pages[i] >= 0, "item {} has {} pages", i, pages[i]);
-        const std::vector<int> out = ember::decode_dispatch_order(std::span<const int>(pages, static_cast<size_t>(n)),
-                                                                  n_kv, n_cu, slots_per_cu);
-        EMBER_CHECK(out.size() <= static_cast<size_t>(capacity), "{} entries do not fit {}", out.size(), capacity);
-        std::copy(out.begin(), out.end(), order);
-        *count = static_cast<int32_t>(out.size());
-        return EMBER_OK;
-    });
-}
-
 int32_t ember_kv_layer(EmberPagedKv *h, int32_t layer, const void *qkv, const float *q_norm, const float *k_norm,
                        const float *bias, void *out) {
     return guarded("kv_layer", [&] {

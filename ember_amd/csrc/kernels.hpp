@@ -56,8 +56,4 @@ constexpr int kDecodeRowInstances[] = {1, 2, 4, 8, 10, 16};
 // to max_run tokens; 0 if none does.
 int decode_rows(int G, int max_run);
 
-// Work-groups of the decode kernel instance (dtype, rows, fused) that one CU
-// holds at once on the current device (its occupancy); 0 if unknown.
-int decode_slots_per_cu(int dtype, int rows, bool fused);
-
 }  // namespace ember::hip

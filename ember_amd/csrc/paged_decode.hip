@@ -1134,29 +1134,7 @@ hipError_t launch(const DecodeParams &p, const EmberAttnArgs &a, int rows, bool 
     return hipGetLastError();
 }
 
-template <typename T, bool FUSED>
-int slots_typed(int rows) {
-    int n = 0;
-    hipError_t e = hipErrorInvalidValue;
-    switch (rows) {
-        case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 1, FUSED>, kThreads, 0); break;
-        case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 2, FUSED>, kThreads, 0); break;
-        case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 4, FUSED>, kThreads, 0); break;
-        case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 8, FUSED>, kThreads, 0); break;
-        case 10: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 10, FUSED>, kThreads, 0); break;
-        case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_kernel<T, 16, FUSED>, kThreads, 0); break;
-        default: break;
-    }
-    return e == hipSuccess ? n : 0;
-}
-
 }  // namespace
-
-int decode_slots_per_cu(int dtype, int rows, bool fused) {
-    if (dtype == EMBER_DTYPE_F16) return fused ? slots_typed<f16, true>(rows) : slots_typed<f16, false>(rows);
-    if (dtype == EMBER_DTYPE_F32) return fused ? slots_typed<float, true>(rows) : slots_typed<float, false>(rows);
-    return 0;
-}
 
 hipError_t launch_paged_decode(const EmberAttnArgs &a, int rows, hipStream_t stream, hipEvent_t start,
                                hipEvent_t stop) {

@@ -179,18 +179,6 @@ class PagedKv:
         return self.plan_info()[3]
 
 
-def dispatch_order(pages, n_kv: int, n_cu: int, slots_per_cu: int) -> list[int]:
-    """The decode work list's launch order for items of the given page counts (ember_kv_dispatch_order; host only):
-    item indices in launch order, -1 for an empty item."""
-    pg = np.ascontiguousarray(np.asarray(pages, np.int32).reshape(-1))
-    cap = 2 * pg.size + (n_cu // max(n_kv, 1)) * max(slots_per_cu, 0) + 1
-    out, count = np.zeros(cap, np.int32), ctypes.c_int32()
-    i32p = ctypes.POINTER(ctypes.c_int32)
-    check(_lib.lib().ember_kv_dispatch_order(pg.ctypes.data_as(i32p), pg.size, n_kv, n_cu, slots_per_cu,
-                                             out.ctypes.data_as(i32p), cap, ctypes.byref(count)), "kv_dispatch_order")
-    return out[:count.value].tolist()
-
-
 def _wrap_device(addr: int, numel: int, dtype: torch.dtype) -> torch.Tensor:
     """A non-owning torch tensor over device memory the C++ side owns (DLPack-free, via __cuda_array_interface__)."""
     typestr = {torch.float16: "<f2", torch.float32: "<f4"}[dtype]

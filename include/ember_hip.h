@@ -462,17 +462,6 @@ int32_t ember_kv_decode_graph(EmberPagedKv *kv, const EmberStepBatch *batch, con
  * kept graph do not count); -1 for a NULL handle. No counterpart in the
  * reference: a diagnostic for tests and benchmarks. */
 int64_t ember_kv_graph_captures(const EmberPagedKv *kv);
-/* The launch order of a decode work list, as ember_kv_plan orders it: pages[i]
- * is the page count of item i (an item is one (run, split), launched as n_kv
- * consecutive work-groups); order receives item indices in launch order, -1
- * for an empty item whose work-groups exit at once, *count their number (at
- * most capacity; 2 * n + n_cu / n_kv * slots_per_cu always suffices). The
- * model: work-group b runs on the CU of b mod n_cu while every CU has a free
- * slot (slots_per_cu work-groups each), later ones on whichever slot frees
- * first. Host only: touches no device. No counterpart in the reference, whose
- * decode grid is a dense (token, kv head, split) box (k_attention.cu:372-386). */
-int32_t ember_kv_dispatch_order(const int32_t *pages, int32_t n, int32_t n_kv, int32_t n_cu, int32_t slots_per_cu,
-                                int32_t *order, int32_t capacity, int32_t *count);
 /* Device copies of whole pages, src[i] -> dst[i] (host arrays of n blocks), all layers. */
 int32_t ember_kv_copy_blocks(EmberPagedKv *kv, const int32_t *src, const int32_t *dst, int32_t n);
 void *ember_kv_k_pool(EmberPagedKv *kv, int32_t layer);
