@@ -84,10 +84,15 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     const int grp = __builtin_amdgcn_readfirstlane(wave / kGroupWaves);  // key blocks grp, grp + 2, ...
     const int wl = wave % kGroupWaves, tg = tid % kGroupThreads;
     const int ql = lane % 16, g = lane / 16;
-    const int tile = static_cast<int>(blockIdx.x);
-    const int head = static_cast<int>(blockIdx.y) * HG + wl / 4;
+    // Work-group id -> (tile, head pair), head pairs fastest: ids that differ by
+    // a multiple of 8 run on one XCD, so with 8 head pairs every tile of one
+    // (sequence, kv head) shares that XCD's L2 for the keys they all read.
+    const int n_pairs = a.n_heads / HG;
+    const int tile = static_cast<int>(blockIdx.x) / n_pairs;
+    const int pair = static_cast<int>(blockIdx.x) % n_pairs;
+    const int head = pair * HG + wl / 4;
     const int G = a.n_heads / a.n_kv;
-    const int kvh = static_cast<int>(blockIdx.y) * HG / G;
+    const int kvh = pair * HG / G;
     const int t0 = a.tile_start[tile];
     const int nt = min(a.tile_end[tile] - t0, kTileTokens);
     const int32_t *table = a.block_tables + static_cast<int64_t>(a.tile_seq[tile]) * a.max_blocks;
@@ -336,7 +341,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const int G = a.n_heads / a.n_kv;
     const int hg = G % 2 == 0 ? 2 : 1;
-    const dim3 grid(static_cast<unsigned>(a.num_tiles), static_cast<unsigned>(a.n_heads / hg));
+    const dim3 grid(static_cast<unsigned>(a.num_tiles * (a.n_heads / hg)));
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)
         hipExtLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, start, stop, 0, a, scale_log2);
