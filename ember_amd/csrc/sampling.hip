@@ -4,9 +4,12 @@
 // (src/backend/cuda/k_sampling.cu:149-198) with the distribution its host
 // sampler defines (src/backend/sampling_host.cpp:20-66), in that order:
 // temperature, top-k, top-p over the top-k set's mass, then min-p relative to
-// the most likely token. The kept set is a threshold on the scaled logit
-// v = x / temperature (kept iff v >= theta, and exp(v - max) >= min_p), and the
-// token is argmax over the kept set of v + Gumbel noise (the Gumbel-max trick,
+// the most likely token. Each cut keeps a prefix of the order the host sorts
+// by (scaled logit v = x / temperature descending, token id ascending): a
+// threshold theta and the last id kept at it (kept iff v > theta, or v ==
+// theta and id <= id_cut), so tokens tied at a boundary are kept lowest id
+// first, as many as the count or mass asks for. Min-p keeps exp(v - max) >=
+// min_p. The token is argmax over the kept set of v + Gumbel noise (the Gumbel-max trick,
 // sampling_rng.hpp:20-33: the noise depends only on (seed, counter, token id),
 // so a row draws the same token in any batch). Greedy rows (temperature <=
 // 1e-5) take the first largest logit.
@@ -57,7 +60,14 @@ struct SampleLds {
     float wmax[kSampleWaves];
     int widx[kSampleWaves];
     uint32_t prefix, mask;
-    unsigned long long above;
+    unsigned long long above, at;  // after a selection: the weight above the found key, and at it
+};
+
+// A prefix of the (v descending, id ascending) order.
+struct Cut {
+    float theta = -INFINITY;
+    int id_cut = 0x7fffffff;
+    __device__ bool keeps(float v, int i) const { return v > theta || (v == theta && i <= id_cut); }
 };
 
 __device__ __forceinline__ float scaled(const float *x, int i, float t) { return x[i] / t; }
@@ -143,9 +153,10 @@ __device__ int block_argmax(const float *x, int V, F score, SampleLds &sh) {
 }
 
 // The largest key K such that the weight of the elements with key >= K (among
-// those with v >= floor) reaches `target`; weight 1 (prob = false) or
-// exp(v - mx) in fixed point (prob = true). Returns the value of K.
-__device__ float radix_threshold(const float *x, int V, float t, float floor, float mx, bool prob,
+// those `within` keeps) reaches `target`; weight 1 (prob = false) or
+// exp(v - mx) in fixed point (prob = true). Returns the value of K; sh.above
+// and sh.at then hold the weight above K and at K.
+__device__ float radix_threshold(const float *x, int V, float t, const Cut &within, float mx, bool prob,
                                  unsigned long long target, SampleLds &sh) {
     const int tid = static_cast<int>(threadIdx.x);
     if (tid == 0) {
@@ -157,9 +168,9 @@ __device__ float radix_threshold(const float *x, int V, float t, float floor, fl
         for (int i = tid; i < 256; i += kSampleThreads) sh.hist[i] = 0;
         __syncthreads();
         const uint32_t prefix = sh.prefix, mask = sh.mask;
-        for_row(x, V, [&](int, float xi) {
+        for_row(x, V, [&](int i, float xi) {
             const float v = xi / t;
-            if (v < floor) return;
+            if (!within.keeps(v, i)) return;
             const uint32_t k = order_key(v);
             if ((k & mask) != prefix) return;
             const unsigned long long w =
@@ -191,6 +202,7 @@ __device__ float radix_threshold(const float *x, int V, float t, float floor, fl
                     cum += sh.hist[d];
                 }
                 sh.above = cum;
+                sh.at = sh.hist[d];
                 sh.prefix = prefix | (static_cast<uint32_t>(d) << shift);
                 sh.mask = mask | (255u << shift);
             }
@@ -200,11 +212,83 @@ __device__ float radix_threshold(const float *x, int V, float t, float floor, fl
     return key_value(sh.prefix);
 }
 
+// The r-th lowest id (r >= 1) among the elements `within` keeps whose v equals
+// theta: a radix selection over the ids, 8 bits per pass from the top, counting
+// from the lowest bin up.
+__device__ int kth_tied_id(const float *x, int V, float t, const Cut &within, float theta, unsigned long long r,
+                           SampleLds &sh) {
+    const int tid = static_cast<int>(threadIdx.x);
+    if (tid == 0) {
+        sh.prefix = 0;
+        sh.mask = 0;
+        sh.above = 0;  // here: the count below the bins looked at so far
+    }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        for (int i = tid; i < 256; i += kSampleThreads) sh.hist[i] = 0;
+        __syncthreads();
+        const uint32_t prefix = sh.prefix, mask = sh.mask;
+        for_row(x, V, [&](int i, float xi) {
+            const float v = xi / t;
+            if (v != theta || !within.keeps(v, i) || (static_cast<uint32_t>(i) & mask) != prefix) return;
+            atomicAdd(&sh.hist[(static_cast<uint32_t>(i) >> shift) & 255u], 1ull);
+        });
+        __syncthreads();
+        if (tid < kWave) {  // wave 0 finds the digit: lane l holds bins 4l .. 4l + 3
+            unsigned long long mine = 0;
+            for (int j = 0; j < 4; j++) mine += sh.hist[4 * tid + j];
+            unsigned long long incl = mine;
+#pragma unroll
+            for (int o = 1; o < kWave; o <<= 1) {
+                const unsigned long long up = __shfl_up(incl, o, kWave);
+                if (tid >= o) incl += up;
+            }
+            const unsigned long long below = sh.above;
+            const bool hit = below + incl >= r;
+            const unsigned long long ballot = __ballot(hit);
+            const int first = ballot ? __ffsll(static_cast<long long>(ballot)) - 1 : kWave - 1;
+            if (tid == first) {
+                unsigned long long cum = below + (incl - mine);
+                int d = 4 * tid;
+                for (int j = 0; j < 3; j++, d++) {
+                    if (cum + sh.hist[d] >= r) break;
+                    cum += sh.hist[d];
+                }
+                sh.above = cum;
+                sh.prefix = prefix | (static_cast<uint32_t>(d) << shift);
+                sh.mask = mask | (255u << shift);
+            }
+        }
+        __syncthreads();
+    }
+    return static_cast<int>(sh.prefix);
+}
+
+// The cut at the key radix_threshold just found (in sh): when the weight at
+// that key holds more tied tokens than the target still needs, only the lowest
+// ids that reach it are kept. w_each: the weight of one token at the key.
+__device__ Cut cut_at(const float *x, int V, float t, const Cut &within, float theta, unsigned long long target,
+                      unsigned long long w_each, SampleLds &sh) {
+    Cut c;
+    c.theta = theta;
+    const unsigned long long above = sh.above, at = sh.at;
+    __syncthreads();  // every thread has read sh before it is reused
+    if (w_each == 0 || target <= above) return c;
+    const unsigned long long need = (target - above + w_each - 1) / w_each, ties = at / w_each;
+    if (need < ties) c.id_cut = kth_tied_id(x, V, t, within, theta, need, sh);
+    return c;
+}
+
 struct Dist {
     bool greedy;
-    float t, mx, theta, min_w;
+    float t, mx, min_w;
+    Cut k, p;              // the top-k and top-p cuts (the top-p one lies inside the top-k one)
     unsigned long long z;  // fixed-point mass of the kept set
+    __device__ bool keeps(float v, int i) const { return k.keeps(v, i) && p.keeps(v, i) && expf(v - mx) >= min_w; }
 };
+
+__device__ __forceinline__ unsigned long long fixed_weight(float v, float mx) {
+    return static_cast<unsigned long long>(static_cast<double>(expf(v - mx)) * kFix);
+}
 
 // The kept set of one row, in the host sampler's order.
 __device__ Dist distribution(const float *x, int V, const EmberSampleParams &p, SampleLds &sh) {
@@ -215,30 +299,32 @@ __device__ Dist distribution(const float *x, int V, const EmberSampleParams &p, 
     float m = -INFINITY;
     for_row(x, V, [&](int, float xi) { m = fmaxf(m, xi / d.t); });
     d.mx = block_max(m, sh);
-    d.theta = -INFINITY;
-    if (p.top_k > 0 && p.top_k < V)
-        d.theta = radix_threshold(x, V, d.t, -INFINITY, d.mx, false, static_cast<unsigned long long>(p.top_k), sh);
-    auto mass = [&](float theta) {
-        unsigned long long s = 0;
-        for_row(x, V, [&](int, float xi) {
-            const float v = xi / d.t;
-            if (v >= theta) s += static_cast<unsigned long long>(static_cast<double>(expf(v - d.mx)) * kFix);
-        });
-        return block_sum_u64(s, sh);
-    };
+    const Cut all;
+    d.k = all;
+    d.p = all;
+    if (p.top_k > 0 && p.top_k < V) {
+        const auto target = static_cast<unsigned long long>(p.top_k);
+        const float theta = radix_threshold(x, V, d.t, all, d.mx, false, target, sh);
+        d.k = cut_at(x, V, d.t, all, theta, target, 1ull, sh);
+    }
     if (p.top_p < 1.0f) {
-        const unsigned long long zk = mass(d.theta);
+        unsigned long long s = 0;
+        for_row(x, V, [&](int i, float xi) {
+            const float v = xi / d.t;
+            if (d.k.keeps(v, i)) s += fixed_weight(v, d.mx);
+        });
+        const unsigned long long zk = block_sum_u64(s, sh);
         const double want = ceil(static_cast<double>(p.top_p) * static_cast<double>(zk));
         const unsigned long long target = want < 1.0 ? 1ull : static_cast<unsigned long long>(want);
-        d.theta = fmaxf(d.theta, radix_threshold(x, V, d.t, d.theta, d.mx, true, target, sh));
+        const float theta = radix_threshold(x, V, d.t, d.k, d.mx, true, target, sh);
+        d.p = cut_at(x, V, d.t, d.k, theta, target, fixed_weight(theta, d.mx), sh);
     }
     d.min_w = p.min_p > 0.0f ? p.min_p : 0.0f;
     // the kept set's mass (min-p applied), for token probabilities
     unsigned long long s = 0;
-    for_row(x, V, [&](int, float xi) {
+    for_row(x, V, [&](int i, float xi) {
         const float v = xi / d.t;
-        const float w = expf(v - d.mx);
-        if (v >= d.theta && w >= d.min_w) s += static_cast<unsigned long long>(static_cast<double>(w) * kFix);
+        if (d.keeps(v, i)) s += fixed_weight(v, d.mx);
     });
     d.z = block_sum_u64(s, sh);
     return d;
@@ -258,8 +344,7 @@ __global__ void __launch_bounds__(kSampleThreads) sample_kernel(const float *__r
     } else {
         tok = block_argmax(x, V, [&](int i, float xi) {
             const float v = xi / d.t;
-            const bool kept = v >= d.theta && expf(v - d.mx) >= d.min_w;
-            return kept ? v + gumbel_noise(p.seed, p.counter, static_cast<uint32_t>(i)) : -INFINITY;
+            return d.keeps(v, i) ? v + gumbel_noise(p.seed, p.counter, static_cast<uint32_t>(i)) : -INFINITY;
         }, sh);
     }
     if (threadIdx.x == 0) out[r] = tok;
@@ -285,8 +370,7 @@ __global__ void __launch_bounds__(kSampleThreads) prob_kernel(const float *__res
     } else {
         const float v = scaled(x, tok, d.t);
         const float w = expf(v - d.mx);
-        const bool kept = v >= d.theta && w >= d.min_w;
-        prob = kept && d.z ? static_cast<float>(static_cast<double>(w) * kFix / static_cast<double>(d.z)) : 0.0f;
+        prob = d.keeps(v, tok) && d.z ? static_cast<float>(static_cast<double>(w) * kFix / static_cast<double>(d.z)) : 0.0f;
     }
     if (threadIdx.x == 0) out[q] = prob;
 }

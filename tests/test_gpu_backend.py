@@ -42,8 +42,8 @@ class OracleModel:
 
     def __init__(self, w, num_blocks=64):
         self.w, self.NB = w, num_blocks
-        self.k = [np.zeros((num_blocks, NKV, PAGE, D), np.uint16) for _ in range(L)]
-        self.v = [np.zeros_like(self.k[0]) for _ in range(L)]
+        self.k = [np.zeros((num_blocks, NKV, PAGE, D), np.uint16) for _ in w["layers"]]
+        self.v = [np.zeros_like(self.k[0]) for _ in w["layers"]]
         self.inv = oracle.inv_freq(1e6, D)
 
     def _norm(self, h, wt):
@@ -231,3 +231,45 @@ def test_decode_steps_replay_one_graph_and_equal_eager(model):
     assert graphs_run == 15
     bg.close()
     be.close()
+
+
+def test_full_shape_28_layers_full_vocabulary(tmp_path_factory):
+    """The model bench.py --backend times: 28 layers and the tied 151,936-token vocabulary (1.19 GB of f16 weights).
+    Two sequences prefill 24- and 40-token prompts in one batch, then run 3 greedy decode steps together (pure decode
+    steps of every token a logit row: the whole-step graph replays). Every logit row is within 2e-2 of the oracle's
+    composition run on that sequence alone; both follow the oracle's greedy tokens."""
+    from ember_amd import _lib
+
+    d = tmp_path_factory.mktemp("qwen3_full_shape")
+    layers, vocab = 28, 151936
+    w = write_model(d, layers=layers, vocab=vocab)
+    assert len(w["layers"]) == layers and w["embed"].shape == (vocab, H)
+    width = 8  # pages per sequence: 40 + 3 tokens fit in 3
+    be = create_backend(str(d), BackendOptions(max_batch_tokens=128, max_seqs=2, kv_cache_tokens=2 * width * PAGE))
+    assert be.vocab_size == vocab
+    rng = np.random.default_rng(17)
+    lens = [24, 40]
+    prompts = [rng.integers(3, vocab, n).tolist() for n in lens]
+    oms = [OracleModel(w, num_blocks=width) for _ in lens]
+    otab = np.arange(width, dtype=np.int32)[None, :]
+    replays = _lib.lib().ember_backend_graph_replays
+    worst, nxt, cur = 0.0, [], [0, 0]
+    for step in range(4):
+        seqs = prompts if step == 0 else [[t] for t in nxt]
+        rows = np.cumsum([len(t) for t in seqs]) - 1
+        b = _multi_batch(seqs, cur, [0, width], width, rows)
+        before = replays()
+        be.forward(b)
+        assert replays() == before + (0 if step == 0 else 1), "pure decode steps replay the whole-step graph"
+        nxt = []
+        for i, toks in enumerate(seqs):
+            want = oms[i].forward(toks, np.arange(cur[i], cur[i] + len(toks), dtype=np.int32), otab, [len(toks) - 1])[0]
+            got = be.logits(i)
+            err = _rel(got, want)
+            assert err < 2e-2, f"step {step} sequence {i}: logits differ from the oracle by {err:.2e}"
+            worst = max(worst, err)
+            nxt.append(int(np.argmax(want)))
+        cur = [c + len(t) for c, t in zip(cur, seqs)]
+    print(f"28 layers, vocabulary {vocab}: worst logit error {worst:.2e}")
+    be.close()
+

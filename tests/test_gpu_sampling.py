@@ -97,3 +97,39 @@ def test_full_vocabulary_rows_and_batch_invariance():
     alone = [gpu_sample(x[i:i + 1], rows[i:i + 1])[0] for i in range(6)]
     assert together == alone
     assert together == [oracle.sample(x[i], 0.9, 0.9, 0, 0.0, seed=7, counter=i) for i in range(6)]
+
+
+def _tied_rows():
+    """Rows whose top-k or top-p cut falls inside a run of exactly equal logits (sampling_host.cpp:31-58 keeps the
+    lower ids first)."""
+    rng = np.random.default_rng(23)
+    base = rng.normal(0.0, 1.0, 3000).astype(np.float32)
+    k_tie = base.copy()
+    k_tie[np.argsort(base)[-5:]] += 8.0                  # 5 clear leaders
+    ties_k = np.array([17, 400, 401, 1999, 2500, 2999])
+    k_tie[ties_k] = np.float32(6.5)                      # 6 tokens tied just below them; top-k 8 keeps 3 of them
+    p_tie = np.full(3000, -10.0, np.float32)
+    ties_p = np.array([5, 77, 78, 900, 1500, 2100, 2200, 2901])
+    p_tie[ties_p] = np.float32(4.0)                      # 8 equal leaders: top-p 0.3 keeps the 3 lowest ids
+    return [(k_tie, (1.0, 1.0, 8, 0.0), ties_k), (p_tie, (1.0, 0.3, 0, 0.0), ties_p),
+            (p_tie, (0.9, 0.55, 6, 0.0), ties_p), (k_tie, (1.3, 0.999, 7, 0.0), ties_k)]
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_ties_at_the_top_k_and_top_p_cuts(case):
+    """Tokens tied at a top-k or top-p boundary: the GPU keeps the same tokens as the host sampler (the lowest ids of
+    the tie, as many as the count or mass asks for), gives the same probabilities, and draws the same tokens."""
+    x, (t, top_p, top_k, min_p), ties = _tied_rows()[case]
+    kept, probs = oracle.sampling_distribution(x, t, top_p, top_k, min_p)
+    in_tie = np.intersect1d(kept, ties)
+    assert 0 < in_tie.size < ties.size, "the case must cut inside the tie"
+    assert np.array_equal(in_tie, np.sort(ties)[:in_tie.size]), "the host keeps the lowest ids of a tie"
+    rows = [(t, top_p, top_k, min_p, 31, 0)]
+    q = [(0, int(i)) for i in ties] + [(0, int(kept[0]))]
+    got = gpu_probs(x[None, :], rows, q)
+    want = np.array([probs[list(kept).index(i)] if i in kept else 0.0 for i in ties] + [probs[0]], np.float32)
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=0.0)
+    R = 400
+    toks = gpu_sample(np.tile(x, (R, 1)), [(t, top_p, top_k, min_p, 31, c) for c in range(R)])
+    assert set(toks) <= set(kept.tolist()), "a draw outside the host's kept set"
+    assert toks[:100] == [oracle.sample(x, t, top_p, top_k, min_p, seed=31, counter=c) for c in range(100)]
