@@ -17,6 +17,8 @@ Prints one JSON line (the driver's contract); a human summary goes to stderr.
 from __future__ import annotations
 
 import argparse
+import contextlib
+import gc
 import json
 import os
 import platform
@@ -42,6 +44,23 @@ KV_BYTES_PER_TOKEN = 2 * KVH * D * 2  # f16 K + V of one token, one layer: 4096 
 TOKEN_BYTES = 8192 + 4096 + 4096 + 4096 + 4096
 FUSED_TOKEN_BYTES = 8192 + 4096 + 4096
 METRIC = "paged decode-attn+append tokens/s and % HBM peak (Qwen3-1.7B shape, batch 32)"
+
+
+@contextlib.contextmanager
+def collector_paused():
+    """Python's cyclic garbage collector off inside a timed region, after one full collection (as timeit does).
+    The step loop here stands in for an engine's C++ loop, which has no collector. A collection of an older
+    generation that lands inside a timed region stalls this host thread for tens of milliseconds, long enough for
+    the GPU to run out of queued steps: at BASELINE config 3 plain runs read 3.78-4.20 ms/step depending on where
+    it landed (one ~45 ms idle window in the GPU trace), and 3.772-3.776 ms/step with the collector off."""
+    gc.collect()
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 def log(msg: str) -> None:
@@ -382,18 +401,20 @@ def _timed(path, step, steps, warmup):
     path.stream.synchronize()
     path.alloc_s = 0.0
     bytes_ = 0
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        bytes_ += step()
-    path.stream.synchronize()
-    wall = time.perf_counter() - t0
+    with collector_paused():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            bytes_ += step()
+        path.stream.synchronize()
+        wall = time.perf_counter() - t0
     alloc_us = path.alloc_s / steps * 1e6
     path.kv.set_timing(True)
     path.kv.timing()
     path.kv.prefill_timing()
-    for _ in range(steps):
-        step()
-    path.stream.synchronize()
+    with collector_paused():
+        for _ in range(steps):
+            step()
+        path.stream.synchronize()
     launches, kernel_ms = path.kv.timing()
     path.prefill_timed = path.kv.prefill_timing()  # (launches, total ms) of the prefill tiles in the same pass
     path.kv.set_timing(False)
@@ -486,12 +507,13 @@ def run_linear(args) -> dict:
         for l in range(N_LAYERS):
             layer(l, False)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        for l in range(N_LAYERS):
-            layer(l, False)
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
+    with collector_paused():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            for l in range(N_LAYERS):
+                layer(l, False)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
     tot = [0.0] * len(names)
     for _ in range(args.steps):
         for l in range(N_LAYERS):
@@ -568,14 +590,15 @@ def run_backend(args) -> dict:
             be.forward(batch(prompts, [0] * B, [PROMPT * (i + 1) - 1 for i in range(B)]))
             nxt, lens = be.sample(greedy), [PROMPT] * B
             ctx_sum = 0
-            for step in range(n_steps):
-                if step == args.warmup:
-                    t0, ctx_sum, c0 = time.perf_counter(), 0, captures()
-                be.forward(batch([[t] for t in nxt], lens, range(B)))
-                nxt = be.sample(greedy)  # waits for the step's logits
-                lens = [n + 1 for n in lens]
-                ctx_sum += sum(lens)
-            wall = time.perf_counter() - t0
+            with collector_paused():
+                for step in range(n_steps):
+                    if step == args.warmup:
+                        t0, ctx_sum, c0 = time.perf_counter(), 0, captures()
+                    be.forward(batch([[t] for t in nxt], lens, range(B)))
+                    nxt = be.sample(greedy)  # waits for the step's logits
+                    lens = [n + 1 for n in lens]
+                    ctx_sum += sum(lens)
+                wall = time.perf_counter() - t0
             if graphs:
                 timed_captures = captures() - c0
             be.close()
@@ -606,12 +629,13 @@ def run_block(args) -> dict:
         w.step()
     w.stream.synchronize()
     sum_ctx = 0
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        sum_ctx += w.step()
-    w.stream.synchronize()
-    torch.cuda.synchronize()
-    step_s = (time.perf_counter() - t0) / args.steps
+    with collector_paused():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            sum_ctx += w.step()
+        w.stream.synchronize()
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
     kv_bytes = N_LAYERS * (KV_BYTES_PER_TOKEN * sum_ctx / args.steps + TOKEN_BYTES * BATCH)
     step_bytes = kv_bytes + w.block_weight_bytes
     gbs = step_bytes / step_s / 1e9
@@ -888,12 +912,13 @@ def main() -> int:
     sum_ctx = 0
     captures0 = w.kv.graph_captures()
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        sum_ctx += w.step()
-    w.stream.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with collector_paused():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            sum_ctx += w.step()
+        w.stream.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
     # graphs captured inside the timed window (a new bucket layout); 0 means every timed step relaunched a kept graph
     timed_captures = w.kv.graph_captures() - captures0
     alloc_us = w.alloc_s / args.steps * 1e6
@@ -902,11 +927,12 @@ def main() -> int:
     w.kv.set_timing(True)
     w.kv.timing()  # start from zero
     sum_ctx_inst = 0
-    t1 = time.perf_counter()
-    for _ in range(args.steps):
-        sum_ctx_inst += w.step()
-    w.stream.synchronize()
-    wall_inst = time.perf_counter() - t1
+    with collector_paused():
+        t1 = time.perf_counter()
+        for _ in range(args.steps):
+            sum_ctx_inst += w.step()
+        w.stream.synchronize()
+        wall_inst = time.perf_counter() - t1
     launches, kernel_ms = w.kv.timing()
     w.kv.set_timing(False)
 
