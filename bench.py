@@ -411,10 +411,12 @@ def _timed(path, step, steps, warmup):
     path.kv.set_timing(True)
     path.kv.timing()
     path.kv.prefill_timing()
+    timed_bytes = 0
     with collector_paused():
         for _ in range(steps):
-            step()
+            timed_bytes += step()
         path.stream.synchronize()
+    path.timed_bytes = timed_bytes / steps  # the step bytes of the pass the events timed
     launches, kernel_ms = path.kv.timing()
     path.prefill_timed = path.kv.prefill_timing()  # (launches, total ms) of the prefill tiles in the same pass
     path.kv.set_timing(False)
@@ -450,11 +452,14 @@ def run_config5(args) -> dict:
 
     step_s, step_bytes, alloc_us, launches, kernel_ms = _timed(path, step, args.steps, args.warmup)
     gbs = step_bytes / step_s / 1e9
+    kernel_us = kernel_ms / max(launches, 1) * 1e3
+    kernel_gbs = path.timed_bytes / N_LAYERS / (kernel_us * 1e-6) / 1e9
     return {
         "metric": "speculative verify rows/s and % HBM peak (Qwen3-1.7B shape, batch 64, q_len 5)",
         "value": round(B5 * Q / step_s, 1), "unit": "query rows/s", "ms_per_step": round(step_s * 1e3, 4),
         "step_gb": round(step_bytes / 1e9, 4), "step_hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-        "decode_kernel_avg_us": round(kernel_ms / max(launches, 1) * 1e3, 2),
+        "decode_kernel_avg_us": round(kernel_us, 2),
+        "decode_kernel_hbm_frac": round(kernel_gbs / HBM_PEAK_GBS, 4),
         "host_blockmanager_us_per_step": round(alloc_us, 2),
         "config": {"workload": "BASELINE configs[4]: 64 sequences, context U[512,4096], 4 drafts + 1 per sequence "
                                "verified in one fused launch per layer, rollback to accepted U{0..4}, 28 layers",

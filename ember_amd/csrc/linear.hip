@@ -24,7 +24,10 @@
 // 2 or 4 work-groups share each 16 features, each taking a K slice (grid y).
 // Each stores its slice sum; the last to count in adds the KS sums in slice
 // order and applies the epilogue. KS depends on N and K only.
+#include <algorithm>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 #include "device.hpp"
 #include "kernels.hpp"
@@ -62,15 +65,33 @@ __device__ __forceinline__ f16x8 load_w(const f16 *p) {
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
+// Activations staged in LDS (when the launcher passes staged): the
+// work-group's rows of A over its K slice, copied by buffer_load_dwordx4 ...
+// lds, each load writing 1 KiB of LDS (lane l's 16 bytes at 16 l). Slot t
+// (16 bytes) holds piece (t % P) ^ (r & 15) of row r = t / P, P = 16-byte
+// pieces per row (a multiple of 16). Every global load then reads whole
+// 128-byte lines of consecutive pieces; read straight from A, a wave's
+// operand load reads 64 bytes from each of 16 rows, 4 KiB apart at K = 2048,
+// and the qkv projection at 32 tokens took 9.4 instead of 7.1 us. The operand
+// read of step s (row 16 mt + c, piece 4 s + g) is one ds_read_b128 whose 16
+// lanes of a given g hit 16 different slots modulo 16: no bank conflicts.
+// Rows past M read as zeros (offsets past the descriptor's records).
+constexpr int kGemvMaxStage = 128 * 1024;  // bytes of staged activations a work-group may hold
+constexpr int kGemvRedBytes = kGemvWaves * kWave * 16;  // one f32x4 per lane and wave, per 16-token tile
+constexpr int kDescWord3 = 0x00020000;  // gfx9 raw buffer: 32-bit data format, no swizzle
+
 // MT tiles of 16 tokens (M <= 16 MT); EP an EMBER_EPILOGUE_*; SPLIT: K split
 // over gridDim.y work-groups (a separate instance, so the unsplit one keeps
-// its constant-stride loads and no merge code).
-template <int MT, int EP, bool SPLIT, bool PACKED>
+// its constant-stride loads and no merge code). Dynamic LDS: the staged
+// activations (staged) or nothing, and afterwards the waves' partial sums.
+template <int MT, int EP, bool SPLIT, bool PACKED, bool STAGED>
 __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restrict__ A, int lda,
                                                             const f16 *__restrict__ W, int M, int N, int K,
                                                             void *__restrict__ C, int ldc,
-                                                            float *__restrict__ slices, uint32_t *__restrict__ counters) {
-    __shared__ f32x4 red[kGemvWaves - 1][MT][kWave];
+                                                            uint32_t piece_magic, float *__restrict__ slices,
+                                                            uint32_t *__restrict__ counters) {
+    extern __shared__ __align__(16) unsigned char gemv_lds[];
+    constexpr bool staged = STAGED;
     __shared__ int merge_here;
     const int tid = static_cast<int>(threadIdx.x);
     const int lane = tid % kWave, wave = tid / kWave;
@@ -78,7 +99,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     const int fb = static_cast<int>(blockIdx.x), nfb = static_cast<int>(gridDim.x);
     const int ks = SPLIT ? static_cast<int>(blockIdx.y) : 0, KS = SPLIT ? static_cast<int>(gridDim.y) : 1;
     const int n0 = fb * 16;
-    const int k0 = ks * (K / KS);  // this work-group's K slice: K / KS, a multiple of 32
+    const int kw = K / KS, k0 = ks * kw;  // this work-group's K slice, a multiple of 32 wide
     // Row-major W: this lane's row (rows past N repeat the last), k step s at
     // +32 s. Packed W: the tile's k steps are 1 KiB blocks in lane order.
     const f16 *w = PACKED ? W + (static_cast<int64_t>(fb) * (K / 32) + k0 / 32) * kPackBlock + 8 * lane
@@ -92,30 +113,60 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
         xok[mt] = tok < M;
         x[mt] = A + static_cast<int64_t>(min(tok, M - 1)) * lda + k0 + 8 * g;
     }
+    const uint32_t pieces = kw / 8;  // 16-byte pieces per staged row
+    // The f32 residual this work-group's epilogue adds to, read now so that
+    // its latency hides behind the W loads (wave mt ends with token tile mt).
+    float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (EP == EMBER_EPILOGUE_ADD_F32) {
+        const int tok = 16 * wave + c;
+        if (wave < MT && tok < M) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int n = n0 + 4 * g + i;
+                if (n < N) prev[i] = static_cast<const float *>(C)[static_cast<int64_t>(tok) * ldc + n];
+            }
+        }
+    }
     f32x4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) acc[mt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // Up to kGemvUnroll k steps per round, every W load of the round issued
-    // before its MFMAs.
-    auto round = [&](auto unroll, int s0, int stride) {
+    // The MFMAs of U k steps s0, s0 + stride, ... whose W operands are in wv,
+    // with the activations from LDS (staged) or from A.
+    auto compute = [&](auto unroll, const f16x8 *wv, int s0, int stride) {
         constexpr int U = decltype(unroll)::value;
-        f16x8 wv[U], xv[U][MT];
+        f16x8 xv[U][MT];
+        if constexpr (staged) {
 #pragma unroll
-        for (int u = 0; u < U; u++) wv[u] = load_w(w + wstep * (s0 + u * stride));
+            for (int u = 0; u < U; u++)
 #pragma unroll
-        for (int u = 0; u < U; u++)
+                for (int mt = 0; mt < MT; mt++) {
+                    const uint32_t r = 16 * mt + c, q = 4 * (s0 + u * stride) + g;
+                    xv[u][mt] = *reinterpret_cast<const f16x8 *>(gemv_lds + 16 * (r * pieces + (q ^ (r & 15u))));
+                }
+        } else {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-                xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s0 + u * stride)) : f16x8{};
+            for (int u = 0; u < U; u++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+                    xv[u][mt] = xok[mt] ? *reinterpret_cast<const f16x8 *>(x[mt] + 32 * (s0 + u * stride)) : f16x8{};
+        }
 #pragma unroll
         for (int u = 0; u < U; u++)
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(wv[u], xv[u][mt], acc[mt], 0, 0, 0);
     };
+    // One round: U k steps, every W load issued before the MFMAs.
+    auto round = [&](auto unroll, int s0, int stride) {
+        constexpr int U = decltype(unroll)::value;
+        f16x8 wv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) wv[u] = load_w(w + wstep * (s0 + u * stride));
+        compute(unroll, wv, s0, stride);
+    };
     using Full = std::integral_constant<int, kGemvUnroll>;
     using Half = std::integral_constant<int, kGemvUnroll / 2>;
-    // A tail of n = 1..4 steps (wave-uniform) as one round of exactly n: the
+    // A round of n = 1..4 steps (wave-uniform) as one round of exactly n: the
     // same steps in the same order, their loads issued together. (A form with
     // every step of the round guarded by u < n, its unused operands left
     // unset, gave wrong sums in one accumulator element of some lanes at 4-way
@@ -128,49 +179,103 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
             default: round(Half{}, s0, stride); break;
         }
     };
-    const int steps = K / KS / 32;
-    if constexpr (SPLIT) {
-        // A slice has few steps per wave: each wave takes a contiguous run, so
-        // its consecutive loads read whole 128-byte lines of W.
-        int s = wave * steps / kGemvWaves;
-        const int end = (wave + 1) * steps / kGemvWaves;
-        for (; s + kGemvUnroll <= end; s += kGemvUnroll) round(Full{}, s, 1);
-        if (s + kGemvUnroll / 2 <= end) {
-            round(Half{}, s, 1);
-            s += kGemvUnroll / 2;
+    // This wave's k steps (local to the slice): unsplit, w, w + 8, ...; split,
+    // a contiguous run, so its consecutive loads read whole 128-byte lines of
+    // a row-major W. A wave accumulates its steps in that order whatever the
+    // rounds they are issued in, so the rounds do not change the sums.
+    const int steps = kw / 32;
+    const int stride = SPLIT ? 1 : kGemvWaves;
+    int s = SPLIT ? wave * steps / kGemvWaves : wave;
+    int left = SPLIT ? (wave + 1) * steps / kGemvWaves - s : (steps - wave + kGemvWaves - 1) / kGemvWaves;
+    // The first round has the same size in every wave (8 when every wave has
+    // 8 steps, else up to 4 and at most the fewest any wave has: steps / 8 in
+    // both schemes), so it and the staging barrier inside it are uniform
+    // across the work-group. The copies into LDS go out first, then the
+    // round's W loads; the wave then waits for its copies only (vector memory
+    // operations complete in issue order), so the W loads stay in flight
+    // across the barrier. The barrier orders LDS alone (the copies are
+    // already complete), so it does not wait for them either.
+    auto issue_stage = [&]() {
+        const uint32_t records = static_cast<uint32_t>((static_cast<int64_t>(M - 1) * lda + K) * 2);
+        const __amdgpu_buffer_rsrc_t d = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16 *>(A), 0, records, kDescWord3);
+        const int blocks = 16 * MT * pieces / 64;
+        for (int b = wave; b < blocks; b += kGemvWaves) {
+            // slot t = r * pieces + q': r = t / pieces by one multiply-high
+            // (exact here: t * pieces < 2^32)
+            const uint32_t t = 64u * b + lane, r = __umulhi(t, piece_magic);
+            const uint32_t q = (t - r * pieces) ^ (r & 15u);
+            const uint32_t off = static_cast<int>(r) < M ? (r * lda + k0 + 8 * q) * 2 : records;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(d, (__attribute__((address_space(3))) void *)(gemv_lds + 1024 * b), 16,
+                                                     off, 0, 0, 0);
         }
-        if (s < end) tail(s, 1, end - s);
-    } else {
-        // Wave w takes k steps w, w + 8, ...
-        int s = wave;
-        for (; s + (kGemvUnroll - 1) * kGemvWaves < steps; s += kGemvUnroll * kGemvWaves) round(Full{}, s, kGemvWaves);
-        for (int left = (steps - s + kGemvWaves - 1) / kGemvWaves; left > 0;) {
-            const int n = min(left, kGemvUnroll / 2);
-            tail(s, kGemvWaves, n);
-            s += n * kGemvWaves;
-            left -= n;
+    };
+    auto stage_barrier = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    };
+    auto first_round = [&](auto unroll) {
+        constexpr int U = decltype(unroll)::value;
+        if constexpr (staged) issue_stage();
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 wv[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) wv[u] = load_w(w + wstep * (s + u * stride));
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (staged) {
+            // s_waitcnt vmcnt(U), expcnt and lgkmcnt left alone: every copy
+            // (issued before the U W loads) has landed
+            __builtin_amdgcn_s_waitcnt(0x0F70 | U);
+            stage_barrier();
         }
+        compute(unroll, wv, s, stride);
+    };
+    const int least = steps / kGemvWaves;
+    const int first = least >= kGemvUnroll ? kGemvUnroll : min(least, kGemvUnroll / 2);
+    switch (first) {
+        case kGemvUnroll: first_round(Full{}); break;
+        case 4: first_round(Half{}); break;
+        case 3: first_round(std::integral_constant<int, 3>{}); break;
+        case 2: first_round(std::integral_constant<int, 2>{}); break;
+        case 1: first_round(std::integral_constant<int, 1>{}); break;
+        default:
+            if constexpr (staged) {
+                issue_stage();
+                __builtin_amdgcn_s_waitcnt(0);
+                stage_barrier();
+            }
+            break;
+    }
+    s += first * stride;
+    left -= first;
+    for (; left >= kGemvUnroll; left -= kGemvUnroll, s += kGemvUnroll * stride) round(Full{}, s, stride);
+    while (left > 0) {
+        const int n = min(left, kGemvUnroll / 2);
+        tail(s, stride, n);
+        s += n * stride;
+        left -= n;
     }
 
-    if (wave > 0) {
+    // The waves' partial sums meet in LDS (over the staged activations, once
+    // every wave is done with them); wave mt adds token tile mt's in wave order.
+    f32x4 *red = reinterpret_cast<f32x4 *>(gemv_lds);  // [wave][mt][lane]
+    if constexpr (staged) __syncthreads();
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) red[wave - 1][mt][lane] = acc[mt];
-    }
+    for (int mt = 0; mt < MT; mt++) red[(wave * MT + mt) * kWave + lane] = acc[mt];
     __syncthreads();
-    if (wave == 0) {
+    const int mt = wave;
+    f32x4 sum = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    if (mt < MT) {
+        sum = red[mt * kWave + lane];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int v = 0; v < kGemvWaves - 1; v++) acc[mt] = acc[mt] + red[v][mt][lane];
+        for (int v = 1; v < kGemvWaves; v++) sum = sum + red[(v * MT + mt) * kWave + lane];
     }
     if constexpr (SPLIT) {
         // Slice sums: [ks][fb][mt][element i][lane], one 256-byte row per store.
-        auto slice = [&](int q, int mt) { return slices + ((static_cast<int64_t>(q) * nfb + fb) * MT + mt) * 256 + lane; };
-        if (wave == 0) {
+        auto slice = [&](int q) { return slices + ((static_cast<int64_t>(q) * nfb + fb) * MT + mt) * 256 + lane; };
+        if (mt < MT) {
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                for (int i = 0; i < 4; i++) put_slice(slice(ks, mt) + 64 * i, acc[mt][i]);
+            for (int i = 0; i < 4; i++) put_slice(slice(ks) + 64 * i, sum[i]);
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -180,56 +285,50 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
             if (merge_here) __hip_atomic_store(counters + fb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         __syncthreads();
-        if (!merge_here || wave != 0) return;
+        if (!merge_here || mt >= MT) return;
         // The slices in slice order, this work-group's own included, so the sum
         // does not depend on which work-group merges.
+        float part[kGemvMaxSplit][4];
 #pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            float part[kGemvMaxSplit][4];
+        for (int q = 0; q < kGemvMaxSplit; q++)
 #pragma unroll
-            for (int q = 0; q < kGemvMaxSplit; q++)
+            for (int i = 0; i < 4; i++) part[q][i] = q < KS ? get_slice(slice(q) + 64 * i) : 0.0f;
 #pragma unroll
-                for (int i = 0; i < 4; i++) part[q][i] = q < KS ? get_slice(slice(q, mt) + 64 * i) : 0.0f;
+        for (int i = 0; i < 4; i++) {
+            float t = part[0][i];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                float t = part[0][i];
-#pragma unroll
-                for (int q = 1; q < kGemvMaxSplit; q++)
-                    if (q < KS) t += part[q][i];
-                acc[mt][i] = t;
-            }
+            for (int q = 1; q < kGemvMaxSplit; q++)
+                if (q < KS) t += part[q][i];
+            sum[i] = t;
         }
-    } else if (wave != 0) {
+    } else if (mt >= MT) {
         return;
     }
 
-    // acc[mt][i] = C[token 16 mt + c][feature n0 + 4 g + i].
+    // sum[i] = C[token 16 mt + c][feature n0 + 4 g + i].
+    const int tok = 16 * mt + c;
+    if (tok >= M) return;
+    if constexpr (EP == EMBER_EPILOGUE_SILU_MUL) {
+        // gate rows even, up rows odd: this lane holds the pairs (4g, 4g+1), (4g+2, 4g+3)
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        const int tok = 16 * mt + c;
-        if (tok >= M) continue;
-        if constexpr (EP == EMBER_EPILOGUE_SILU_MUL) {
-            // gate rows even, up rows odd: this lane holds the pairs (4g, 4g+1), (4g+2, 4g+3)
+        for (int i = 0; i < 4; i += 2) {
+            const int n = n0 + 4 * g + i;
+            if (n + 1 < N)
+                static_cast<f16 *>(C)[static_cast<int64_t>(tok) * ldc + n / 2] =
+                    static_cast<f16>(clamp_half(silu(sum[i]) * sum[i + 1]));
+        }
+    } else {
 #pragma unroll
-            for (int i = 0; i < 4; i += 2) {
-                const int n = n0 + 4 * g + i;
-                if (n + 1 < N)
-                    static_cast<f16 *>(C)[static_cast<int64_t>(tok) * ldc + n / 2] =
-                        static_cast<f16>(clamp_half(silu(acc[mt][i]) * acc[mt][i + 1]));
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int n = n0 + 4 * g + i;
-                if (n >= N) continue;
-                const int64_t at = static_cast<int64_t>(tok) * ldc + n;
-                if constexpr (EP == EMBER_EPILOGUE_STORE_F16)
-                    static_cast<f16 *>(C)[at] = static_cast<f16>(clamp_half(acc[mt][i]));
-                else if constexpr (EP == EMBER_EPILOGUE_STORE_F32)
-                    static_cast<float *>(C)[at] = acc[mt][i];
-                else
-                    static_cast<float *>(C)[at] += acc[mt][i];
-            }
+        for (int i = 0; i < 4; i++) {
+            const int n = n0 + 4 * g + i;
+            if (n >= N) continue;
+            const int64_t at = static_cast<int64_t>(tok) * ldc + n;
+            if constexpr (EP == EMBER_EPILOGUE_STORE_F16)
+                static_cast<f16 *>(C)[at] = static_cast<f16>(clamp_half(sum[i]));
+            else if constexpr (EP == EMBER_EPILOGUE_STORE_F32)
+                static_cast<float *>(C)[at] = sum[i];
+            else
+                static_cast<float *>(C)[at] = prev[i] + sum[i];
         }
     }
 }
@@ -346,20 +445,44 @@ int64_t gemv_workspace(int M, int N, int K) {
     return (nfb * 4 + 255) / 256 * 256 + ks * nfb * mt * 256 * 4;
 }
 
+// Kernels already allowed more than the default 64 KiB of dynamic LDS.
+bool allow_lds(const void *kernel, int bytes) {
+    if (bytes <= 64 * 1024) return true;
+    static std::mutex mu;
+    static std::vector<const void *> allowed;
+    std::lock_guard<std::mutex> lock(mu);
+    if (std::find(allowed.begin(), allowed.end(), kernel) != allowed.end()) return true;
+    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxStage + kGemvRedBytes) != hipSuccess)
+        return false;
+    allowed.push_back(kernel);
+    return true;
+}
+
 template <int EP>
 hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     const int64_t need = gemv_workspace(a.M, a.N, a.K);
     const bool split = need > 0 && a.workspace && a.workspace_bytes >= need;
     const int nfb = (a.N + 15) / 16;
-    const dim3 grid(static_cast<unsigned>(nfb), static_cast<unsigned>(split ? gemv_split(a.N, a.K) : 1));
+    const int ks = split ? gemv_split(a.N, a.K) : 1;
+    const dim3 grid(static_cast<unsigned>(nfb), static_cast<unsigned>(ks));
     uint32_t *counters = split ? static_cast<uint32_t *>(a.workspace) : nullptr;
     float *slices = split ? reinterpret_cast<float *>(static_cast<char *>(a.workspace) + (nfb * 4 + 255) / 256 * 256)
                           : nullptr;
     const f16 *A = static_cast<const f16 *>(a.A);
     const f16 *W = static_cast<const f16 *>(a.W);
+    // Stage the activations when the slice's rows fit and their 16-byte
+    // pieces per row are a multiple of 16 (the swizzle's period).
+    const int mt = (a.M + 15) / 16, kw = a.K / ks;
+    const int stage = 16 * mt * kw * 2;
+    const bool staged = kw % 128 == 0 && stage <= kGemvMaxStage;
+    const int lds = staged ? std::max(stage, mt * kGemvRedBytes) : mt * kGemvRedBytes;
+    // ceil(2^32 / pieces): r = t / pieces as one multiply-high for every slot t
+    // of the stage (t * pieces < 2^32 since the stage is at most 128 KiB).
+    const uint32_t magic = staged ? static_cast<uint32_t>(((uint64_t{1} << 32) + kw / 8 - 1) / (kw / 8)) : 0;
     auto go = [&](auto kernel) {
-        hipLaunchKernelGGL(kernel, grid, dim3(kGemvThreads), 0, stream, A, a.lda, W, a.M, a.N, a.K, a.C, a.ldc, slices,
-                           counters);
+        if (!allow_lds(reinterpret_cast<const void *>(kernel), lds)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(kernel, grid, dim3(kGemvThreads), static_cast<unsigned>(lds), stream, A, a.lda, W, a.M, a.N,
+                           a.K, a.C, a.ldc, magic, slices, counters);
         return hipGetLastError();
     };
     if (!split && a.M <= 16 && nfb >= kWideMinTiles) {
@@ -372,23 +495,39 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
                                a.K, a.C, a.ldc);
         return hipGetLastError();
     }
-    switch ((a.M + 15) / 16 + (split ? 4 : 0) + (a.w_packed ? 8 : 0)) {
-        case 1: return go(gemv_kernel<1, EP, false, false>);
-        case 2: return go(gemv_kernel<2, EP, false, false>);
-        case 3: return go(gemv_kernel<3, EP, false, false>);
-        case 4: return go(gemv_kernel<4, EP, false, false>);
-        case 5: return go(gemv_kernel<1, EP, true, false>);
-        case 6: return go(gemv_kernel<2, EP, true, false>);
-        case 7: return go(gemv_kernel<3, EP, true, false>);
-        case 8: return go(gemv_kernel<4, EP, true, false>);
-        case 9: return go(gemv_kernel<1, EP, false, true>);
-        case 10: return go(gemv_kernel<2, EP, false, true>);
-        case 11: return go(gemv_kernel<3, EP, false, true>);
-        case 12: return go(gemv_kernel<4, EP, false, true>);
-        case 13: return go(gemv_kernel<1, EP, true, true>);
-        case 14: return go(gemv_kernel<2, EP, true, true>);
-        case 15: return go(gemv_kernel<3, EP, true, true>);
-        case 16: return go(gemv_kernel<4, EP, true, true>);
+    switch (mt + (split ? 4 : 0) + (a.w_packed ? 8 : 0) + (staged ? 16 : 0)) {
+        case 1: return go(gemv_kernel<1, EP, false, false, false>);
+        case 2: return go(gemv_kernel<2, EP, false, false, false>);
+        case 3: return go(gemv_kernel<3, EP, false, false, false>);
+        case 4: return go(gemv_kernel<4, EP, false, false, false>);
+        case 5: return go(gemv_kernel<1, EP, true, false, false>);
+        case 6: return go(gemv_kernel<2, EP, true, false, false>);
+        case 7: return go(gemv_kernel<3, EP, true, false, false>);
+        case 8: return go(gemv_kernel<4, EP, true, false, false>);
+        case 9: return go(gemv_kernel<1, EP, false, true, false>);
+        case 10: return go(gemv_kernel<2, EP, false, true, false>);
+        case 11: return go(gemv_kernel<3, EP, false, true, false>);
+        case 12: return go(gemv_kernel<4, EP, false, true, false>);
+        case 13: return go(gemv_kernel<1, EP, true, true, false>);
+        case 14: return go(gemv_kernel<2, EP, true, true, false>);
+        case 15: return go(gemv_kernel<3, EP, true, true, false>);
+        case 16: return go(gemv_kernel<4, EP, true, true, false>);
+        case 17: return go(gemv_kernel<1, EP, false, false, true>);
+        case 18: return go(gemv_kernel<2, EP, false, false, true>);
+        case 19: return go(gemv_kernel<3, EP, false, false, true>);
+        case 20: return go(gemv_kernel<4, EP, false, false, true>);
+        case 21: return go(gemv_kernel<1, EP, true, false, true>);
+        case 22: return go(gemv_kernel<2, EP, true, false, true>);
+        case 23: return go(gemv_kernel<3, EP, true, false, true>);
+        case 24: return go(gemv_kernel<4, EP, true, false, true>);
+        case 25: return go(gemv_kernel<1, EP, false, true, true>);
+        case 26: return go(gemv_kernel<2, EP, false, true, true>);
+        case 27: return go(gemv_kernel<3, EP, false, true, true>);
+        case 28: return go(gemv_kernel<4, EP, false, true, true>);
+        case 29: return go(gemv_kernel<1, EP, true, true, true>);
+        case 30: return go(gemv_kernel<2, EP, true, true, true>);
+        case 31: return go(gemv_kernel<3, EP, true, true, true>);
+        case 32: return go(gemv_kernel<4, EP, true, true, true>);
         default: return hipErrorInvalidValue;
     }
 }

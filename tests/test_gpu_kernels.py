@@ -563,6 +563,33 @@ def test_gemv_matches_oracle(device, M, N, KD, ep, split):
     assert _linear_err(got, want) < 2e-3
 
 
+@pytest.mark.parametrize("N,KD", [(4096, 2048), (2048, 4096), (1024, 3072)])
+@pytest.mark.parametrize("ep", [0, 2])
+def test_gemv_rows_do_not_depend_on_the_batch(device, N, KD, ep):
+    """A token's outputs are the same bits whatever the batch around it. The batches here take both activation
+    paths: up to 32 rows of a 2048-wide K slice (or 48 of 1024) are staged in LDS, 64 rows of one are read straight
+    from A. The split shapes (2048 x 4096 over 2 slices, 1024 x 3072 over 4) go through the merge too."""
+    from ember_amd import _lib
+    rng = np.random.default_rng(N + KD + ep)
+    a = torch.from_numpy(rng.standard_normal((64, KD)).astype(np.float16)).to(device)
+    w = torch.from_numpy((rng.standard_normal((N, KD)) * 0.05).astype(np.float16)).to(device)
+    start = torch.from_numpy(rng.standard_normal((64, N)).astype(np.float32)).to(device)
+    ws = K.gemv_workspace(64, N, KD, device)
+    outs = {}
+    for M in (64, 48, 32, 9, 1):
+        c = start[:M].clone() if ep == _lib.EPILOGUE_ADD_F32 else torch.empty((M, N), dtype=torch.float16,
+                                                                              device=device)
+        K.gemv(a[:M].contiguous(), w, c, ep, workspace=ws)
+        outs[M] = c
+    torch.cuda.synchronize()
+    view = torch.int32 if ep == _lib.EPILOGUE_ADD_F32 else torch.int16
+    for M in (48, 32, 9, 1):
+        assert torch.equal(outs[64][:M].view(view), outs[M].view(view)), f"M={M}"
+    want = oracle.linear(a.cpu().numpy(), w.cpu().numpy(), ep,
+                         start.cpu().numpy() if ep == _lib.EPILOGUE_ADD_F32 else None)
+    assert _linear_err(outs[64].float().cpu().numpy(), want) < 2e-3
+
+
 def test_gemv_split_is_deterministic_and_leaves_counters_zero(device):
     """The K-split merge: the o projection's shape (2048 features, 2 slices) gives the same bits on every launch
     (the slices are added in slice order, whichever work-group merges), agrees with the unsplit launch within
