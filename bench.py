@@ -472,7 +472,10 @@ def run_linear(args) -> dict:
     kv 8 x 128): the input RMSNorm, the qkv projection (N 4096, K 2048, f16 out) and the output projection
     (N 2048, K 2048, added into the f32 residual), in the reference's order (cuda_backend.cu:350-362). Each
     of the 28 layers has its own random weights (672 MB in all, more than the 256 MB last-level cache), so W
-    streams from HBM as in a real step. Kernels are timed with HIP events on the launching stream."""
+    streams from HBM as in a real step. The pass is timed as launched one by one; each kernel's time is a
+    hipGraph of its 28 launches replayed between two HIP events: a launch's share of back-to-back work on
+    the GPU, free of the host's launch rate. Consecutive launches overlap one's start with the other's end,
+    so it can read below a rocprof duration."""
     import torch
 
     from ember_amd import kernels as K
@@ -494,39 +497,44 @@ def run_linear(args) -> dict:
     p_o = [K.gemv_pack(w) for w in w_o]
     torch.cuda.synchronize()
     names = ["rmsnorm_rows", "gemv qkv (store_f16)", "gemv o (add_f32)"]
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in names]
-          for _ in range(N_LAYERS)]
 
-    def layer(l, timed):
-        ops = [lambda: K.rmsnorm_rows(h, norm_w[l], xn, 1e-6),
-               lambda: K.gemv(xn, w_qkv[l], qkv, 0, workspace=ws, packed=p_qkv[l]),
-               lambda: K.gemv(att, w_o[l], h, 2, workspace=ws, packed=p_o[l])]
-        for i, op in enumerate(ops):
-            if timed:
-                ev[l][i][0].record()
+    def ops(l):
+        return [lambda: K.rmsnorm_rows(h, norm_w[l], xn, 1e-6),
+                lambda: K.gemv(xn, w_qkv[l], qkv, 0, workspace=ws, packed=p_qkv[l]),
+                lambda: K.gemv(att, w_o[l], h, 2, workspace=ws, packed=p_o[l])]
+
+    def layer(l):
+        for op in ops(l):
             op()
-            if timed:
-                ev[l][i][1].record()
 
     for _ in range(args.warmup):
         for l in range(N_LAYERS):
-            layer(l, False)
+            layer(l)
     torch.cuda.synchronize()
     with collector_paused():
         t0 = time.perf_counter()
         for _ in range(args.steps):
             for l in range(N_LAYERS):
-                layer(l, False)
+                layer(l)
         torch.cuda.synchronize()
         step_s = (time.perf_counter() - t0) / args.steps
-    tot = [0.0] * len(names)
-    for _ in range(args.steps):
-        for l in range(N_LAYERS):
-            layer(l, True)
+    tot = []
+    for i in range(len(names)):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for l in range(N_LAYERS):
+                ops(l)[i]()
+        graph.replay()
         torch.cuda.synchronize()
-        for l in range(N_LAYERS):
-            for i in range(len(names)):
-                tot[i] += ev[l][i][0].elapsed_time(ev[l][i][1])
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with collector_paused():
+            start.record()
+            for _ in range(args.steps):
+                graph.replay()
+            stop.record()
+            torch.cuda.synchronize()
+        tot.append(start.elapsed_time(stop))
+        del graph
     us = [t / (args.steps * N_LAYERS) * 1e3 for t in tot]
     bytes_ = [M * HID * 4 + HID * 4 + M * HID * 2,
               NQKV * HID * 2 + M * HID * 2 + M * NQKV * 2,

@@ -214,6 +214,33 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
                 decode_cap_);
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
+    // Prefill tiles are dispatched longest first (keys read: the tile's last
+    // position + 1; ties keep list order): a launch of several rounds of
+    // work-groups, one per CU, then ends on its shortest tiles instead of on
+    // whichever long tile the list happened to put last. A tile's arithmetic
+    // does not depend on its place in the list.
+    if (tiles_ > 1) {
+        std::vector<int> order(static_cast<size_t>(tiles_));
+        std::vector<int> keys(static_cast<size_t>(tiles_));
+        for (int i = 0; i < tiles_; i++) {
+            order[static_cast<size_t>(i)] = i;
+            int k = 0;
+            for (int t = tile_start_[static_cast<size_t>(i)]; t < tile_end_[static_cast<size_t>(i)]; t++)
+                k = std::max(k, b.positions[static_cast<size_t>(t)] + 1);
+            keys[static_cast<size_t>(i)] = k;
+        }
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int x, int y) { return keys[static_cast<size_t>(x)] > keys[static_cast<size_t>(y)]; });
+        std::vector<int32_t> start(order.size()), end(order.size()), seq(order.size());
+        for (size_t i = 0; i < order.size(); i++) {
+            start[i] = tile_start_[static_cast<size_t>(order[i])];
+            end[i] = tile_end_[static_cast<size_t>(order[i])];
+            seq[i] = tile_seq_[static_cast<size_t>(order[i])];
+        }
+        tile_start_.swap(start);
+        tile_end_.swap(end);
+        tile_seq_.swap(seq);
+    }
     fused_ = fused_ && tiles_ == 0 && decode_count_ == T;
     splits_ = graph_splits > 0 ? graph_splits : std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
 
