@@ -3,13 +3,16 @@
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
 package, and only as the checker. The product (ember_amd/) never does.
 Every function restates a piece of the reference's CPU path; see oracle.h for
-the reference lines each follows and what pins it.
+the reference lines each follows and what pins it. ref_lib() loads the pieces of
+the reference itself that compile here (oracle/_ref, built by `make ref` where
+the reference tree is present), against which tests check the restatements.
 """
 from __future__ import annotations
 
 import ctypes
 import subprocess
-from ctypes import POINTER, c_char_p, c_double, c_float, c_int32, c_int64, c_uint8, c_uint16, c_uint64, c_void_p
+from ctypes import (POINTER, c_char_p, c_double, c_float, c_int32, c_int64, c_uint8, c_uint16, c_uint32, c_uint64,
+                    c_void_p)
 from pathlib import Path
 
 import numpy as np
@@ -66,10 +69,38 @@ _PROTOS = {
 _lib = None
 
 
+REF_TREE = Path("/root/reference/src")
+REF_LIB_PATH = HERE / "_ref" / "libember_ref.so"
+_REF_PROTOS = {
+    "ember_ref_rng_mix": (c_uint64, [c_uint64]),
+    "ember_ref_gumbel_noise": (c_float, [c_uint64, c_uint64, c_uint32]),
+    "ember_ref_sample_uniform": (c_double, [c_uint64, c_uint64]),
+    "ember_ref_sampling_distribution": (c_int32, [_F32P, c_int32, c_float, c_float, c_int32, c_float, _I32P, _F32P]),
+    "ember_ref_sample_host": (c_int32, [_F32P, c_int32, c_float, c_float, c_int32, c_float, c_uint64, c_uint64]),
+    "ember_ref_dot_avx2": (c_float, [_F32P, _F32P, c_int32]),
+}
+_ref_lib = None
+
+
 def build() -> Path:
-    """Compiles oracle/liboracle.so with the committed Makefile."""
+    """Compiles oracle/liboracle.so with the committed Makefile, and oracle/_ref from the reference's own sources
+    when the reference tree is present (not on a GPU box, which uses what was built)."""
     subprocess.run(["make", "-B", "-s", "-C", str(HERE)], check=True)
+    if REF_TREE.is_dir():
+        subprocess.run(["make", "-B", "-s", "-C", str(HERE), "ref"], check=True)
     return LIB_PATH
+
+
+def ref_lib():
+    """The reference's host sampler and AVX2 dot product as built into oracle/_ref, or None when not built."""
+    global _ref_lib
+    if _ref_lib is None and REF_LIB_PATH.exists():
+        h = ctypes.CDLL(str(REF_LIB_PATH))
+        for name, (res, args) in _REF_PROTOS.items():
+            fn = getattr(h, name)
+            fn.restype, fn.argtypes = res, args
+        _ref_lib = h
+    return _ref_lib
 
 
 def lib() -> ctypes.CDLL:

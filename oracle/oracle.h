@@ -49,14 +49,17 @@ void ember_oracle_linear_mt(const uint16_t *A, const uint16_t *W, int32_t M, int
                             float *C, int32_t ldc, int32_t threads);
 
 /* Sampling (src/backend/sampling_host.cpp:20-87, src/backend/sampling_rng.hpp:22-33).
- * rng_mix: SplitMix64's output step, pinned by its published first outputs.
- * gumbel: -log(-log(u)) of a 24-bit uniform from (seed, counter, id); pinned
- * by the Gumbel(0, 1) mean (Euler-Mascheroni) and variance (pi^2 / 6).
+ * Every function here is pinned bit for bit against the reference's own
+ * sampler, compiled from its sources into oracle/_ref (oracle/Makefile `ref`;
+ * tests/test_oracle_vs_reference.py), including tied logits at the cuts.
+ * rng_mix: SplitMix64's output step, also pinned by its published first outputs.
+ * gumbel: -log(-log(u)) of a 24-bit uniform from (seed, counter, id); also
+ * checked by the Gumbel(0, 1) mean (Euler-Mascheroni) and variance (pi^2 / 6).
  * sampling_distribution: the kept tokens, most likely first, with their
- * probabilities; pinned by numpy restatements of each filter on their own
- * (greedy argmax, top-k by sort, top-p cumulative, min-p ratio) and by the
+ * probabilities; also checked by numpy restatements of each filter on their
+ * own (greedy argmax, top-k by sort, top-p cumulative, min-p ratio) and by the
  * probabilities summing to 1. sample: argmax of logit / T + gumbel over the
- * kept set; pinned by its frequencies against the distribution. */
+ * kept set; also checked by its frequencies against the distribution. */
 uint64_t ember_oracle_rng_mix(uint64_t z);
 float ember_oracle_gumbel(uint64_t seed, uint64_t counter, uint32_t id);
 int32_t ember_oracle_sampling_distribution(const float *logits, int32_t vocab, float temperature, float top_p,
@@ -71,7 +74,11 @@ void ember_oracle_rope(float *x, int32_t head_dim, int32_t pos, const float *inv
 /* The f32 dot product of the CPU kernels: two 8-wide FMA accumulators over
  * 16-element strides, then a fixed horizontal sum (cpu_kernels_avx2.cpp:27-33,
  * :58-69); the scalar loop of cpu_kernels.cpp:74-79 without AVX2+FMA.
- * Pinned: float64 dot within f32 rounding. */
+ * Pinned: float64 dot within f32 rounding, and bit for bit against the
+ * reference's own AVX2 dot (oracle/_ref) at lengths that are multiples of 8.
+ * Other lengths end in a scalar tail whose rounding is the compiler's (the
+ * reference's GCC -O3 -mfma build vectorizes it, partly fused); the path never
+ * takes it (head_dim 128). */
 float ember_oracle_dot(const float *a, const float *b, int32_t n);
 
 /* Offset of (seq, layer, kv_head, pos) in a pool of num_blocks blocks per
