@@ -12,11 +12,16 @@
 // 4 drafts, one in four wrong (rollback). A page handed to the wrong sequence,
 // a stale slot or a wrong table shows up as logits far from the alone run's;
 // the different kernel paths (decode runs, prefill tiles, chunk boundaries)
-// only move them by rounding. Usage: hip_engine_test <model_dir>.
+// only move them by rounding. Usage: hip_engine_test <model_dir> [dump]: with a
+// dump path, the alone runs' sequences and logit rows are written there for the
+// Python side to check against the oracle (int32 requests, then per request
+// int32 prompt length, int32 length and its tokens; int32 rows, int32 vocab,
+// then per row int32 request, int32 position sampled, float logits[vocab]).
 #include <cmath>
 #include <cstdio>
 #include <map>
 #include <random>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -173,7 +178,7 @@ double compare(const Result &ref, const Result &got, const char *what, int &fail
 
 int main(int argc, char **argv) {
     if (argc < 2) {
-        std::fprintf(stderr, "usage: %s <model_dir>\n", argv[0]);
+        std::fprintf(stderr, "usage: %s <model_dir> [dump]\n", argv[0]);
         return 2;
     }
     int failures = 0;
@@ -214,6 +219,31 @@ int main(int argc, char **argv) {
             o.max_seqs = 1;
             Result one = run(*be, full, prompt_len, {id}, o, false, be->num_kv_blocks(), failures);
             ref.rec.insert(one.rec.begin(), one.rec.end());
+        }
+        if (argc > 2) {
+            std::FILE *f = std::fopen(argv[2], "wb");
+            if (!f) throw std::runtime_error(std::string("cannot write ") + argv[2]);
+            auto put = [&](const void *p, size_t bytes) {
+                if (std::fwrite(p, 1, bytes, f) != bytes) throw std::runtime_error("short write of the dump");
+            };
+            const int32_t nreq = static_cast<int32_t>(full.size());
+            put(&nreq, 4);
+            for (size_t i = 0; i < full.size(); i++) {
+                const int32_t pl = prompt_len[i], n = static_cast<int32_t>(full[i].size());
+                put(&pl, 4);
+                put(&n, 4);
+                put(full[i].data(), full[i].size() * 4);
+            }
+            const int32_t rows = static_cast<int32_t>(ref.rec.size()), vocab = V;
+            put(&rows, 4);
+            put(&vocab, 4);
+            for (const auto &[key, lg] : ref.rec) {
+                const int32_t id = key.first, pos = key.second;
+                put(&id, 4);
+                put(&pos, 4);
+                put(lg.data(), lg.size() * 4);
+            }
+            std::fclose(f);
         }
         // together on 24 pages (384 tokens for ~1,400 of context): preemption, 40-token chunks, the prefix cache
         testing::MiniOptions o;

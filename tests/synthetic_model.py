@@ -14,8 +14,11 @@ from pathlib import Path
 import numpy as np
 import torch
 
+import oracle
+
 H, I, NH, NKV, D = 1024, 3072, 16, 8, 128
 Q, KV = NH * D, NKV * D
+PAGE = 16
 
 
 def write_model(d: Path, layers: int = 4, vocab: int = 8192, seed: int = 20261005) -> dict:
@@ -58,3 +61,37 @@ def write_model(d: Path, layers: int = 4, vocab: int = 8192, seed: int = 2026100
             in_norm=f32(p + "input_layernorm.weight"), post_norm=f32(p + "post_attention_layernorm.weight"),
             q_norm=f32(p + "self_attn.q_norm.weight"), k_norm=f32(p + "self_attn.k_norm.weight")))
     return w
+
+
+class OracleModel:
+    """The forward pass composed from the oracle's pieces (rmsnorm, linear, append, attention) with the GPU path's f16
+    roundings (xn, qkv, attention output and the MLP activation stored as f16; cuda_backend.cu:350-366), f16 K/V
+    pages in the oracle's own pool. `w` is write_model's return value."""
+
+    def __init__(self, w, num_blocks=64):
+        self.w, self.NB = w, num_blocks
+        self.k = [np.zeros((num_blocks, NKV, PAGE, D), np.uint16) for _ in w["layers"]]
+        self.v = [np.zeros_like(self.k[0]) for _ in w["layers"]]
+        self.inv = oracle.inv_freq(1e6, D)
+
+    def _norm(self, h, wt):
+        return np.stack([oracle.rmsnorm(r, wt, 1e-6) for r in h]).astype(np.float16)
+
+    def forward(self, tokens, positions, table, logit_rows):
+        T = len(tokens)
+        h = self.w["embed"][np.asarray(tokens)].astype(np.float32)
+        qs = np.array([0, T], np.int32)
+        for layer, lw in enumerate(self.w["layers"]):
+            xn = self._norm(h, lw["in_norm"])
+            qkv = oracle.linear(xn, lw["qkv"], 0, threads=16).astype(np.float16).astype(np.float32)
+            q = oracle.append_layer(qkv, positions, qs, table, self.k[layer], self.v[layer], n_heads=NH, n_kv=NKV,
+                                    inv_freq_=self.inv, eps=1e-6, q_norm=lw["q_norm"], k_norm=lw["k_norm"],
+                                    num_blocks=self.NB, kv_f16=True)
+            att = oracle.attention_layer(q, positions, qs, table, self.k[layer], self.v[layer], n_heads=NH, n_kv=NKV,
+                                         num_blocks=self.NB, kv_f16=True, q_f16=True, threads=16)
+            h = oracle.linear(att.reshape(T, Q).astype(np.float16), lw["o"], 2, h, threads=16)
+            xn = self._norm(h, lw["post_norm"])
+            act = oracle.linear(xn, lw["gate_up"], 3, threads=16).astype(np.float16)
+            h = oracle.linear(act, lw["down"], 2, h, threads=16)
+        xn = self._norm(h[np.asarray(logit_rows)], self.w["norm"])
+        return oracle.linear(xn, self.w["embed"], 1, threads=16)
