@@ -25,9 +25,7 @@
 // Each stores its slice sum; the last to count in adds the KS sums in slice
 // order and applies the epilogue. KS depends on N and K only.
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
-#include <vector>
 
 #include "device.hpp"
 #include "kernels.hpp"
@@ -445,19 +443,6 @@ int64_t gemv_workspace(int M, int N, int K) {
     return (nfb * 4 + 255) / 256 * 256 + ks * nfb * mt * 256 * 4;
 }
 
-// Kernels already allowed more than the default 64 KiB of dynamic LDS.
-bool allow_lds(const void *kernel, int bytes) {
-    if (bytes <= 64 * 1024) return true;
-    static std::mutex mu;
-    static std::vector<const void *> allowed;
-    std::lock_guard<std::mutex> lock(mu);
-    if (std::find(allowed.begin(), allowed.end(), kernel) != allowed.end()) return true;
-    if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, kGemvMaxStage + kGemvRedBytes) != hipSuccess)
-        return false;
-    allowed.push_back(kernel);
-    return true;
-}
-
 template <int EP>
 hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     const int64_t need = gemv_workspace(a.M, a.N, a.K);
@@ -479,8 +464,9 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     // ceil(2^32 / pieces): r = t / pieces as one multiply-high for every slot t
     // of the stage (t * pieces < 2^32 since the stage is at most 128 KiB).
     const uint32_t magic = staged ? static_cast<uint32_t>(((uint64_t{1} << 32) + kw / 8 - 1) / (kw / 8)) : 0;
+    // Dynamic LDS up to the device's 160 KiB per work-group launches without
+    // raising a per-kernel limit on gfx950 (hipDeviceProp_t::sharedMemPerBlock).
     auto go = [&](auto kernel) {
-        if (!allow_lds(reinterpret_cast<const void *>(kernel), lds)) return hipErrorInvalidValue;
         hipLaunchKernelGGL(kernel, grid, dim3(kGemvThreads), static_cast<unsigned>(lds), stream, A, a.lda, W, a.M, a.N,
                            a.K, a.C, a.ldc, magic, slices, counters);
         return hipGetLastError();
