@@ -13,7 +13,7 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libember_hip.so"
 
 # Constants of include/ember_hip.h.
-ABI_VERSION = 6
+ABI_VERSION = 7
 BLOCK_SIZE = 16
 PREFILL_TILE = 64
 MAX_RUN = 8
@@ -63,6 +63,7 @@ class PrefillArgs(ctypes.Structure):
         ("positions", c_void_p), ("block_tables", c_void_p),
         ("num_tiles", c_int32), ("max_blocks", c_int32), ("n_heads", c_int32), ("n_kv", c_int32), ("head_dim", c_int32),
         ("scale", c_float), ("out", c_void_p), ("num_blocks", c_int32), ("dtype", c_int32),
+        ("heads_per_group", c_int32),
     ]
 
 

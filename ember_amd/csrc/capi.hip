@@ -119,6 +119,9 @@ int ember::hip::prefill_attn(const EmberPrefillArgs *a, hipStream_t stream, hipE
         return set_error(EMBER_ERR_INVALID, "prefill_attn: bad sizes");
     if (!(a->scale > 0.0f) || !std::isfinite(a->scale))  // the block max is taken before scaling
         return set_error(EMBER_ERR_INVALID, "prefill_attn: scale must be positive and finite");
+    if (a->heads_per_group < 0 || a->heads_per_group > 2 || (a->heads_per_group == 2 && G % 2 != 0))
+        return set_error(EMBER_ERR_INVALID, "prefill_attn: heads_per_group is 0, 1 or 2 (2 only for an even G; got %d)",
+                         a->heads_per_group);
     if (a->num_tiles == 0) return EMBER_OK;
     if (!a->q || !a->k_cache || !a->v_cache || !a->tile_start || !a->tile_end || !a->tile_seq || !a->positions ||
         !a->block_tables || !a->out)

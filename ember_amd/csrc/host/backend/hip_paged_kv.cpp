@@ -44,6 +44,12 @@ HipPagedKv::HipPagedKv(const ModelConfig &cfg, const PagedKvOptions &opt, hipStr
     EMBER_CHECK(opt_.num_blocks > 0, "the KV cache has no blocks");
     EMBER_CHECK(opt_.dtype == EMBER_DTYPE_F16 || opt_.dtype == EMBER_DTYPE_F32, "unknown dtype {}", opt_.dtype);
     if (opt_.split_len <= 0) opt_.split_len = 512;
+    {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && cus > 0)
+            cu_count_ = cus;
+    }
     EMBER_CHECK(opt_.split_len % kBlockSize == 0 && opt_.split_len <= EMBER_MAX_SPLIT_LEN,
                 "split_len {} is not a multiple of {} up to {}", opt_.split_len, kBlockSize, EMBER_MAX_SPLIT_LEN);
     EMBER_CHECK(opt_.max_batch_tokens > 0 && opt_.max_seqs > 0, "bad batch limits");
@@ -214,6 +220,13 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
                 decode_cap_);
     decode_runs_ = static_cast<int>(run_first_.size());
     tiles_ = static_cast<int>(tile_start_.size());
+    // A launch whose tiles fit one round of work-groups at one per CU (tiles x
+    // head pairs <= CUs) lasts as long as its longest tile. There each query
+    // head gets its own work-group instead (twice the work-groups, two per
+    // CU), and the list below pairs long tiles with short ones on a CU. A
+    // row's result is the same bits with one or two heads per work-group.
+    const int G = cfg_.group();
+    prefill_hg_ = G % 2 == 0 && static_cast<int64_t>(tiles_) * cfg_.n_heads <= 2LL * cu_count_ ? 1 : 0;
     // Prefill tiles are dispatched longest first (keys read: the tile's last
     // position + 1; ties keep list order): a launch of several rounds of
     // work-groups, one per CU, then ends on its shortest tiles instead of on
@@ -231,6 +244,14 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
         }
         std::stable_sort(order.begin(), order.end(),
                          [&](int x, int y) { return keys[static_cast<size_t>(x)] > keys[static_cast<size_t>(y)]; });
+        if (prefill_hg_ == 1) {
+            // Work-groups b and b + CUs share a CU (b = tile x heads + head), so
+            // tile i shares with tile i + CUs / heads: every other run of that
+            // many tiles is reversed, pairing the longest with the shortest.
+            const int per = cu_count_ / cfg_.n_heads;
+            for (int g0 = per; per > 0 && g0 < tiles_; g0 += 2 * per)
+                std::reverse(order.begin() + g0, order.begin() + std::min(tiles_, g0 + per));
+        }
         std::vector<int32_t> start(order.size()), end(order.size()), seq(order.size());
         for (size_t i = 0; i < order.size(); i++) {
             start[i] = tile_start_[static_cast<size_t>(order[i])];
@@ -455,6 +476,7 @@ void HipPagedKv::layer(int l, const void *qkv, const float *q_norm, const float 
         pa.out = out;
         pa.num_blocks = opt_.num_blocks + 1;
         pa.dtype = opt_.dtype;
+        pa.heads_per_group = prefill_hg_;
         hipEvent_t start = nullptr, stop = nullptr;
         if (timing_) prefill_timing_.next(&start, &stop);
         check_abi(hip::prefill_attn(&pa, stream_, start, stop), "prefill_attn");

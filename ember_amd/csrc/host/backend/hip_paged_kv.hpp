@@ -170,6 +170,8 @@ private:
 
     // The current plan (device addresses into dev_ints_[stage_]).
     int T_ = 0, decode_count_ = 0, decode_runs_ = 0, max_run_ = 1, tiles_ = 0, splits_ = 1, max_blocks_ = 0;
+    int prefill_hg_ = 0;   // EmberPrefillArgs::heads_per_group of the planned step
+    int cu_count_ = 256;   // the device's CUs (the constructor asks)
     bool fused_ = false;  // every sequence's new tokens form one run: append + attention in one launch
     const int32_t *d_positions_ = nullptr, *d_token_seq_ = nullptr, *d_tables_ = nullptr, *d_decode_ = nullptr,
                   *d_run_first_ = nullptr, *d_run_count_ = nullptr, *d_tile_start_ = nullptr, *d_tile_end_ = nullptr,

@@ -340,7 +340,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
 
 hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const int G = a.n_heads / a.n_kv;
-    const int hg = G % 2 == 0 ? 2 : 1;
+    const int hg = a.heads_per_group == 1 || G % 2 != 0 ? 1 : 2;
     const dim3 grid(static_cast<unsigned>(a.num_tiles * (a.n_heads / hg)));
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)

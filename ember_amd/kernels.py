@@ -293,12 +293,13 @@ def _attn_args(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, token_l
     return a, keep
 
 
-def prefill_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, tiles, stream=None):
+def prefill_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, tiles, stream=None,
+                      heads_per_group=0):
     """Causal prefill attention of query tiles on MFMA (≙ cuda::prefill_attention).
 
     tiles: (start, end, seq) triples, each up to PREFILL_TILE consecutive tokens start..end-1 of
     sequence seq; every token attends to its sequence's keys 0..its position, which must already be in
-    the pools. f16 only.
+    the pools. f16 only. heads_per_group: 0 (the launcher's choice), 1 or 2 (even G): the same bits.
     """
     if not tiles:
         return []
@@ -324,6 +325,7 @@ def prefill_attention(q, k_pool, v_pool, out, ints: StepInts, *, n_heads, n_kv, 
     a.scale = 1.0 / math.sqrt(HEAD_DIM)
     a.out = _dev(out, "out")
     a.num_blocks, a.dtype = ints.num_blocks, _dtype_code(q)
+    a.heads_per_group = heads_per_group
     check(_lib.lib().ember_hip_prefill_attn(a, _stream_handle(stream)), "prefill_attn")
     return [ts, te, tq]
 

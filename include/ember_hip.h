@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define EMBER_ABI_VERSION 6
+#define EMBER_ABI_VERSION 7
 #define EMBER_BLOCK_SIZE 16  /* tokens per page; kBlockSize, src/backend/backend.hpp:25 */
 #define EMBER_PREFILL_TILE 64 /* query tokens per prefill tile; kPrefillTile, kernels.cuh:108 */
 #define EMBER_MAX_RUN 8      /* query tokens one decode work-group reads a page for */
@@ -185,6 +185,11 @@ typedef struct EmberPrefillArgs {
     /* additions */
     int32_t num_blocks;
     int32_t dtype;                /* must be EMBER_DTYPE_F16 (MFMA path) */
+    /* Query heads per work-group (no counterpart in the reference): 0 lets
+     * the launcher choose (2 when G is even, else 1); 1 gives each query head
+     * its own work-group; 2 needs an even G. A row's result is the same bits
+     * either way, so a planner may pick per launch. */
+    int32_t heads_per_group;
 } EmberPrefillArgs;
 
 /* Causal attention of query tiles (up to 64 consecutive tokens of one

@@ -525,6 +525,28 @@ def test_prefill_tile_is_independent_of_its_neighbours(rng, device):
         assert np.isnan(one.float().cpu().numpy()[rest]).all(), "a tile wrote outside its tokens"
 
 
+@pytest.mark.parametrize("n_kv", [8, 4])
+def test_prefill_heads_per_group_gives_the_same_bits(rng, device, n_kv):
+    """One query head per work-group (heads_per_group 1) or two (2, the default at even G): every row's output
+    is the same bits, so a planner may pick per launch. Tiles of several lengths, some over long context."""
+    NB = 800
+    ctxs, new = [64, 200, 1100, 2100, 40], [64, 120, 100, 64, 40]
+    step = make_step(rng, ctxs, new, NB)
+    k, v = _random_pools(rng, step, NB, f16=True)
+    kp, vp = torch.from_numpy(np.nan_to_num(k)).to(device), torch.from_numpy(np.nan_to_num(v)).to(device)
+    q = torch.from_numpy(rng.standard_normal((step.T, H, D)).astype(np.float16)).to(device)
+    ints = K.StepInts(step.positions, step.token_seq, step.tables, NB)
+    outs = []
+    for hg in (0, 1, 2):
+        o = torch.full((step.T, H, D), float("nan"), dtype=torch.float16, device=device)
+        K.prefill_attention(q, kp, vp, o, ints, n_heads=H, n_kv=n_kv, tiles=_tiles_of(step), heads_per_group=hg)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0].float()).all()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16))
+
+
 # ---- the layer either side: decode-sized linear layers and the input RMSNorm ----
 
 def _linear_err(got, want):
