@@ -265,24 +265,55 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
     fused_ = fused_ && tiles_ == 0 && decode_count_ == T;
     splits_ = graph_splits > 0 ? graph_splits : std::max(1, (max_ctx + opt_.split_len - 1) / opt_.split_len);
 
-    // Decode work items (run, split), dispatched in list order: every full
-    // split first, then the partial last splits, longest first, so the short
-    // ones fill the tail of the launch.
+    // Decode work items (run, split), longest first (every full split, then
+    // the partial last splits), in an order that balances the keys each CU
+    // reads. The launch's first kDecodeWgPerCu x CUs work-groups start at
+    // once, work-group b on CU b mod CUs, so with the kv heads of an item
+    // side by side, item i lands on CU group i mod groups (groups = CUs /
+    // n_kv): those items are dealt to the group with the fewest keys so far,
+    // longest first, and later items follow longest first. Within a group
+    // the shortest item takes the first slot: a CU's earliest work-group wins
+    // the memory arbitration and finishes first, so the lightest CUs free a
+    // slot first and take the later items.
     work_.clear();
-    std::vector<std::pair<int, int>> partial;  // (keys, run)
-    for (int r = 0; r < decode_runs_; r++) {
-        const int ctx = run_ctx_[static_cast<size_t>(r)];
-        const int full = ctx / opt_.split_len;
-        for (int s = 0; s < full; s++) {
-            work_.push_back(r);
-            work_.push_back(s);
+    {
+        struct Item {
+            int keys, run, split;
+        };
+        std::vector<Item> items, partial;
+        for (int r = 0; r < decode_runs_; r++) {
+            const int ctx = run_ctx_[static_cast<size_t>(r)];
+            const int full = ctx / opt_.split_len;
+            for (int s = 0; s < full; s++) items.push_back({opt_.split_len, r, s});
+            if (ctx % opt_.split_len) partial.push_back({ctx % opt_.split_len, r, full});
         }
-        if (ctx % opt_.split_len) partial.emplace_back(ctx % opt_.split_len, r);
-    }
-    std::stable_sort(partial.begin(), partial.end(), [](const auto &a, const auto &b) { return a.first > b.first; });
-    for (const auto &[keys, r] : partial) {
-        work_.push_back(r);
-        work_.push_back(run_ctx_[static_cast<size_t>(r)] / opt_.split_len);
+        std::stable_sort(partial.begin(), partial.end(), [](const Item &a, const Item &b) { return a.keys > b.keys; });
+        items.insert(items.end(), partial.begin(), partial.end());
+        const int n = static_cast<int>(items.size());
+        const int groups = std::max(1, cu_count_ / cfg_.n_kv_heads);
+        std::vector<Item> order(items);
+        if (n >= groups * kDecodeWgPerCu) {
+            std::vector<int64_t> load(static_cast<size_t>(groups), 0);
+            std::vector<std::vector<Item>> dealt(static_cast<size_t>(groups));
+            for (int i = 0; i < groups * kDecodeWgPerCu; i++) {
+                int g = -1;
+                for (int h = 0; h < groups; h++)
+                    if (static_cast<int>(dealt[static_cast<size_t>(h)].size()) < kDecodeWgPerCu &&
+                        (g < 0 || load[static_cast<size_t>(h)] < load[static_cast<size_t>(g)]))
+                        g = h;
+                dealt[static_cast<size_t>(g)].push_back(items[static_cast<size_t>(i)]);
+                load[static_cast<size_t>(g)] += items[static_cast<size_t>(i)].keys;
+            }
+            for (int g = 0; g < groups; g++) {
+                std::reverse(dealt[static_cast<size_t>(g)].begin(), dealt[static_cast<size_t>(g)].end());
+                for (int k = 0; k < kDecodeWgPerCu; k++)
+                    order[static_cast<size_t>(k * groups + g)] = dealt[static_cast<size_t>(g)][static_cast<size_t>(k)];
+            }
+        }
+        for (const Item &it : order) {
+            work_.push_back(it.run);
+            work_.push_back(it.split);
+        }
     }
     if (graph_splits > 0) {  // the graph's fixed-length list: padding items name no run
         EMBER_CHECK(static_cast<int>(work_.size() / 2) <= decode_runs_ * graph_splits, "internal: graph work list");

@@ -59,6 +59,7 @@ public:
     };
     static constexpr int kGraphMaxTokens = 64;
     static constexpr int kDescInts = 16;  // ints per work descriptor (EmberAttnArgs::work_desc)
+    static constexpr int kDecodeWgPerCu = 4;  // decode work-groups a CU holds at once (f16, up to 10 rows)
     // A pure decode step (every sequence one new token, at most 64) as one
     // replayed hipGraph of all layers' launches (cuda_backend.cu:376-454): the
     // step is padded to a token bucket and a block-table width bucket, padding

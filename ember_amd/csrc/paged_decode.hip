@@ -353,6 +353,12 @@ __device__ __forceinline__ void put_partial(float *p, float v) {
 __device__ __forceinline__ float get_partial(const float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A split's (M, L), stored as two adjacent floats, with one 8-byte load.
+__device__ __forceinline__ float2 get_partial_pair(const float *p) {
+    const uint64_t v = __hip_atomic_load(reinterpret_cast<const uint64_t *>(p), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(float2, v);
+}
 
 // The split merge of one output element (token list entry li, head, dim d):
 // out = sum_s O_s 2^(M_s - M) / sum_s L_s 2^(M_s - M) over the ns splits that
@@ -473,6 +479,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     __shared__ __align__(16) T q_lds[(FUSED || Q_LDS) ? ROWS : 1][D];
     __shared__ __align__(16) T new_k[NEW][D], new_v[NEW][D];
     __shared__ int merge_here;
+    __shared__ int merge_ctx[ROWS];  // the keys each row sees, for the in-kernel merge
 
     // The run: list entries first .. first + nq - 1, one sequence. Its rows are
     // (token i, head kvh * G + g) for row = i * G + g < nrows; rows nrows ..
@@ -631,21 +638,38 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         if constexpr (Q_LDS) __syncthreads();
     } else {
         // q of every row and the new K/V in this split, one head vector per
-        // wave at a time; lane l holds dims l and l + 64 (a rotary pair). The
-        // wave's first q row and new token are loaded before its first pages,
-        // so their arithmetic overlaps those page loads, and the barrier after
+        // wave at a time; lane l holds dims l and l + 64 (a rotary pair). Wave
+        // w takes rows w, w + 4, ... and new tokens w, w + 4, ...; all of
+        // their loads are issued before the first is used, and before the
+        // wave's first pages, so the prologue costs one memory round trip (a
+        // verify run of 5 tokens gives a wave up to 3 rows and 2 tokens: one
+        // after another, under a full memory queue, they took about 4 round
+        // trips) and the arithmetic overlaps the page loads. The barrier after
         // it waits for LDS only, not for the pages.
         const int n_total = p.n_heads + 2 * p.n_kv;
         const T *qkv = static_cast<const T *>(p.qkv);
         auto vec = [&](int t, int head) { return qkv + (static_cast<int64_t>(t) * n_total + head) * D; };
         const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
 
-        const int row0 = min(wave, nrows - 1), i0 = min(wave, nq - 1);
-        const int qt0 = token_of(row0 / G), kt0 = token_of(i0);
-        const int qpos0 = pos_of(row0 / G), kpos0 = pos_of(i0);
-        const T *qs0 = vec(qt0, kvh * G + row0 % G), *ks0 = vec(kt0, kh), *vs0 = vec(kt0, vh);
-        const T q0a = qs0[lane], q0b = qs0[lane + D / 2];
-        const T k0a = ks0[lane], k0b = ks0[lane + D / 2], v0a = vs0[lane], v0b = vs0[lane + D / 2];
+        constexpr int RQ = (ROWS + kWaves - 1) / kWaves;                        // rows per wave, at most
+        constexpr int NT = ((NEW < ROWS ? NEW : ROWS) + kWaves - 1) / kWaves;  // new tokens per wave, at most
+        T qa[RQ], qb[RQ], ka[NT], kb[NT], va[NT], vb[NT];  // a row or token past the run loads the last again
+#pragma unroll
+        for (int k = 0; k < RQ; k++) {
+            const int row = min(wave + k * kWaves, nrows - 1);
+            const T *qs = vec(token_of(row / G), kvh * G + row % G);
+            qa[k] = qs[lane];
+            qb[k] = qs[lane + D / 2];
+        }
+#pragma unroll
+        for (int k = 0; k < NT; k++) {
+            const int t = token_of(min(wave + k * kWaves, nq - 1));
+            const T *ks = vec(t, kh), *vs = vec(t, vh);
+            ka[k] = ks[lane];
+            kb[k] = ks[lane + D / 2];
+            va[k] = vs[lane];
+            vb[k] = vs[lane + D / 2];
+        }
         const NormRopeLane qn = norm_rope_lane(p.q_norm, p.inv_freq, lane);
         const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
 
@@ -688,17 +712,17 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         // A new token is appended by the work-group whose split holds its position.
         auto in_split = [&](int pos) { return pos >= begin && pos < end; };
 
-        if (wave < nrows) put_q(row0, to_f32(q0a), to_f32(q0b), qpos0);
-        for (int row = wave + kWaves; row < nrows; row += kWaves) {
-            const T *s = vec(token_of(row / G), kvh * G + row % G);
-            put_q(row, to_f32(s[lane]), to_f32(s[lane + D / 2]), pos_of(row / G));
+#pragma unroll
+        for (int k = 0; k < RQ; k++) {
+            const int row = wave + k * kWaves;
+            if (row < nrows) put_q(row, to_f32(qa[k]), to_f32(qb[k]), pos_of(row / G));
         }
-        if (wave < nq && in_split(kpos0)) put_kv(i0, to_f32(k0a), to_f32(k0b), to_f32(v0a), to_f32(v0b), kpos0);
-        for (int i = wave + kWaves; i < nq; i += kWaves) {
-            const int t = token_of(i), pos = pos_of(i);
-            if (!in_split(pos)) continue;
-            const T *ks = vec(t, kh), *vs = vec(t, vh);
-            put_kv(i, to_f32(ks[lane]), to_f32(ks[lane + D / 2]), to_f32(vs[lane]), to_f32(vs[lane + D / 2]), pos);
+#pragma unroll
+        for (int k = 0; k < NT; k++) {
+            const int i = wave + k * kWaves;
+            if (i >= nq) continue;
+            const int pos = pos_of(i);
+            if (in_split(pos)) put_kv(i, to_f32(ka[k]), to_f32(kb[k]), to_f32(va[k]), to_f32(vb[k]), pos);
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
         __builtin_amdgcn_s_barrier();
@@ -1028,19 +1052,136 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
         uint32_t *counter = p.counters + static_cast<int64_t>(run) * p.n_kv + kvh;
         const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         merge_here = before + 1 == static_cast<uint32_t>(run_splits);
-        if (merge_here) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (merge_here) {
+            __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int row = 0; row < ROWS; row++) merge_ctx[row] = min(row_pos[row] + 1, p.max_blocks * kPage);
+        }
     }
     __syncthreads();
     if (!merge_here) return;
-    for (int idx = tid; idx < nrows * D; idx += kThreads) {
-        const int row = idx / D, d = idx % D;
+    auto ns_of = [&](int row) { return min(p.num_splits, max(1, (merge_ctx[row] + p.split_len - 1) / p.split_len)); };
+    auto out_of = [&](int row) {
         const int li = first + row / G, head = kvh * G + row % G;
-        int pos = row_pos[0];
-#pragma unroll
-        for (int k = 1; k < ROWS; k++) pos = row == k ? row_pos[k] : pos;
         const int t = counting ? desc[kDescTok] + row / G : p.token_index ? p.token_index[li] : li;
-        T *o = static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
-        merge_one<T>(p, li, head, d, min(pos + 1, p.max_blocks * kPage), o);
+        return static_cast<T *>(p.out) + (static_cast<int64_t>(t) * p.n_heads + head) * D;
+    };
+    constexpr int E = (ROWS * D + kThreads - 1) / kThreads;  // elements per thread
+    const int nsm = min(p.num_splits, run_splits);            // no row holds keys in more splits
+    // Element by element (merge_one) where that costs one round trip (one
+    // element per thread, the splits in one chunk), or where the splits are
+    // too many to stage in LDS; the batched merge below otherwise.
+    if ((E == 1 && nsm <= kMergeChunk) || 2 * nrows * nsm > kWaves * RW) {
+        for (int idx = tid; idx < nrows * D; idx += kThreads) {
+            const int row = idx / D;
+            merge_one<T>(p, first + row / G, kvh * G + row % G, idx % D, merge_ctx[row], out_of(row));
+        }
+        return;
+    }
+
+    // The run's merge with merge_one's arithmetic in merge_one's order (the
+    // same bits), its loads batched over the work-group: thread i < nrows * nsm
+    // brings (M, L) of (row i / nsm, split i % nsm) into LDS with one load,
+    // and every thread requests the O partials of all its elements for MS
+    // splits before the first wait. Up to MS splits then cost one memory round
+    // trip, where merge_one costs up to three per element and a thread merges
+    // ROWS / 2 elements one after another. One thread per row then turns its
+    // (M, L) pairs into weights (-1: a split without a key of the row) and L,
+    // and the elements' sums read the weights with no branch. red_acc is free:
+    // the partials are stored.
+    constexpr int MS = E >= 12 ? 4 : 48 / E < 16 ? 48 / E : 16;
+    constexpr int RC = 8;                     // splits per LDS batch of the row pass
+    float *const sm = red_acc;                // M per (row, split)
+    float *const sw = red_acc + nrows * nsm;  // L per (row, split), then its weight
+    auto slot_of = [&](int row, int s) {
+        const int li = first + row / G, head = kvh * G + row % G;
+        return (static_cast<int64_t>(li) * p.n_heads + head) * p.num_splits + s;
+    };
+    float O[E];
+    bool any[E];
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        O[e] = 0.0f;
+        any[e] = false;
+    }
+    for (int s0 = 0; s0 < nsm; s0 += MS) {
+        // Unconditional loads, one straight run and one wait: an element past
+        // the rows reads the last row, a split past the run's last reads that
+        // one again, and a split past a row's last reads that row's partial of
+        // the split (stored, holding no key of the row); none of them is used.
+        float ov[E][MS];
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const int row = min((tid + e * kThreads) / D, nrows - 1);
+#pragma unroll
+            for (int k = 0; k < MS; k++)
+                ov[e][k] = get_partial(p.part_acc + slot_of(row, min(s0 + k, nsm - 1)) * D + tid % D);
+        }
+        if (s0 == 0) {
+            for (int i = tid; i < nrows * nsm; i += kThreads) {
+                const float2 ml = get_partial_pair(p.part_ml + slot_of(i / nsm, i % nsm) * 2);
+                sm[i] = ml.x;
+                sw[i] = ml.y;
+            }
+            __syncthreads();
+            if (tid < nrows) {  // per row: M, then each split's weight and L in split order
+                const int row = tid, ns = ns_of(row);
+                const float *rm = sm + row * nsm;
+                float *rw = sw + row * nsm;
+                float M = -INFINITY;
+                for (int c0 = 0; c0 < ns; c0 += RC) {
+                    float mv[RC];
+#pragma unroll
+                    for (int k = 0; k < RC; k++) mv[k] = rm[min(c0 + k, ns - 1)];
+#pragma unroll
+                    for (int k = 0; k < RC; k++) M = fmaxf(M, mv[k]);  // repeats of the last split change nothing
+                }
+                float L = 0.0f;
+                bool seen = false;
+                for (int c0 = 0; c0 < ns; c0 += RC) {
+                    float mv[RC], lv[RC], w[RC];
+#pragma unroll
+                    for (int k = 0; k < RC; k++) {
+                        mv[k] = rm[min(c0 + k, ns - 1)];
+                        lv[k] = rw[min(c0 + k, ns - 1)];
+                    }
+#pragma unroll
+                    for (int k = 0; k < RC; k++) {
+                        const bool use = c0 + k < ns && mv[k] != -INFINITY;
+                        const float f = mv[k] == M ? 1.0f : exp2_hw(mv[k] - M);
+                        const float ls = lv[k] * f;
+                        L = use ? (seen ? L + ls : ls) : L;
+                        seen = seen || use;
+                        w[k] = use ? f : -1.0f;
+                    }
+#pragma unroll
+                    for (int k = 0; k < RC; k++)
+                        if (c0 + k < ns) rw[c0 + k] = w[k];
+                }
+                for (int s = ns; s < nsm; s++) rw[s] = -1.0f;
+                red_l[row][0] = L;
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int e = 0; e < E; e++) {
+            const int row = min((tid + e * kThreads) / D, nrows - 1);
+#pragma unroll
+            for (int k = 0; k < MS; k++) {
+                const float w = sw[row * nsm + min(s0 + k, nsm - 1)];
+                const bool use = s0 + k < nsm && w >= 0.0f;
+                const float os = ov[e][k] * w;
+                O[e] = use ? (any[e] ? O[e] + os : os) : O[e];
+                any[e] = any[e] || use;
+            }
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < E; e++) {
+        const int idx = tid + e * kThreads, row = idx / D;
+        if (idx >= nrows * D) continue;
+        const float L = red_l[row][0];
+        out_of(row)[idx % D] = from_f32<T>(L > 0.0f ? O[e] / L : 0.0f);
     }
 }
 

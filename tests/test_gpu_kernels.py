@@ -460,6 +460,36 @@ def test_in_kernel_merge_of_runs_across_a_split_boundary(rng, device, dtype):
         assert int(keep[-1].abs().sum()) == 0, "merge counters not reset"
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("new", [1, 5])
+def test_in_kernel_merge_of_many_splits(rng, device, dtype, new):
+    """Runs holding from 1 to 1,032 splits: one chunk, one batch or several batches of the in-kernel merge's
+    loads, and for the longest contexts at 16 keys a split more than its LDS stages (the element-by-element
+    merge). Bit for bit the
+    merge kernel's output, and at 512 keys a split within tolerance of the oracle up to 5k keys. (The
+    16.5k-key run, summed in f32 from 33 partials, is checked bit for bit against the merge kernel only: at 64
+    keys a split, from 258 partials, it lay 1.1e-5 from the oracle's single pass.)"""
+    f16 = dtype == torch.float16
+    NB = 2400
+    cached = [16500, 5000, 4100, 1100, 300, 20]
+    step = make_step(rng, [c + new for c in cached], [new] * len(cached), NB)
+    k, v = _random_pools(rng, step, NB, f16=f16)
+    kp, vp = torch.from_numpy(k).to(device), torch.from_numpy(v).to(device)
+    q = rng.standard_normal((step.T, H, D)).astype(np.float16 if f16 else np.float32)
+    runs = (step.query_start[:-1], np.diff(step.query_start)) if new > 1 else None
+    bits = lambda t: t.cpu().numpy().view(np.uint16 if f16 else np.uint32)  # noqa: E731
+    for split_len in (16, 64, 512):
+        kw = dict(runs=runs, split_len=split_len, use_work_list=True)
+        want = _run_decode(q, kp, vp, step, NB, device, merge_in_kernel=False, **kw)
+        for _ in range(2):
+            got = _run_decode(q, kp, vp, step, NB, device, merge_in_kernel=True, **kw)
+            assert np.array_equal(bits(got), bits(want)), split_len
+    ref = oracle.attention_layer(q, step.positions, step.query_start, step.tables, np.nan_to_num(k), np.nan_to_num(v),
+                                 n_heads=H, n_kv=KVH, num_blocks=NB, kv_f16=f16, threads=8)
+    rows = slice(int(step.query_start[1]), None)  # every run but the 16.5k-key one
+    assert rel_err(want.float().cpu().numpy()[rows], ref[rows]) < (2e-3 if f16 else 1e-5)
+
+
 # ---- MFMA prefill tiles ----
 
 def _tiles_of(step, tile=64):
