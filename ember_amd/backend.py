@@ -69,6 +69,8 @@ class Backend:
         c.kv_cache_bytes, c.kv_cache_tokens, c.memory_fraction, c.gpu = (o.kv_cache_bytes, o.kv_cache_tokens,
                                                                         o.memory_fraction, o.gpu)
         c.graphs = 1 if o.cuda_graphs else -1
+        # The destructor is bound here: at interpreter exit the module's globals may be gone before this object.
+        self._destroy = _lib.lib().ember_backend_destroy
         self._h = _lib.lib().ember_backend_create(str(model_dir).encode(), c)
         if not self._h:
             raise EmberError(last_error())
@@ -79,7 +81,7 @@ class Backend:
     def close(self) -> None:
         h, self._h = getattr(self, "_h", None), None
         if h:
-            _lib.lib().ember_backend_destroy(h)
+            self._destroy(h)
 
     def __del__(self):
         self.close()

@@ -27,6 +27,8 @@ def _ptr(a: np.ndarray):
 
 class BlockManager:
     def __init__(self, num_blocks: int, prefix_caching: bool):
+        # The destructor is bound here: at interpreter exit the module's globals may be gone before this object.
+        self._destroy = lib().ember_bm_destroy
         self._h = lib().ember_bm_create(int(num_blocks), 1 if prefix_caching else 0)
         if not self._h:
             raise EmberError(last_error())
@@ -34,7 +36,7 @@ class BlockManager:
     def __del__(self):
         h, self._h = getattr(self, "_h", None), None
         if h:
-            lib().ember_bm_destroy(h)
+            self._destroy(h)
 
     # -- sizes (block_manager.hpp:29-33) --
     def num_blocks(self) -> int:

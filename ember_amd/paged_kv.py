@@ -52,6 +52,8 @@ class PagedKv:
         c.qk_norm, c.split_len = 1 if qk_norm else 0, split_len
         self.cfg = c
         self.dtype = dtype
+        # The destructor is bound here: at interpreter exit the module's globals may be gone before this object.
+        self._destroy = _lib.lib().ember_kv_destroy
         self._h = _lib.lib().ember_kv_create(c, self.stream.cuda_stream)
         if not self._h:
             raise EmberError(last_error())
@@ -61,7 +63,7 @@ class PagedKv:
     def close(self):
         h, self._h = getattr(self, "_h", None), None
         if h:
-            _lib.lib().ember_kv_destroy(h)
+            self._destroy(h)
 
     def __del__(self):
         self.close()
