@@ -490,7 +490,7 @@ def run_linear(args) -> dict:
     xn = torch.empty((M, HID), device=dev, dtype=torch.float16)
     qkv = torch.empty((M, NQKV), device=dev, dtype=torch.float16)
     att = torch.randn((M, HID), generator=g, device=dev).half()
-    # One zeroed workspace for both projections (they never overlap): the o projection's 2048 features split K.
+    # One zeroed workspace for both projections (they never overlap); neither splits K at these shapes (None).
     ws = max((K.gemv_workspace(M, n, HID, dev) for n in (NQKV, HID)),
              key=lambda t: 0 if t is None else t.numel(), default=None)
     p_qkv = [K.gemv_pack(w) for w in w_qkv]  # W as a backend keeps it: the GEMV's packed layout

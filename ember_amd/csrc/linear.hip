@@ -38,6 +38,7 @@ constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kGemvUnroll = 8;  // k steps whose W loads are in flight together, per wave
 constexpr int kGemvTargetGroups = 256;  // work-groups a launch should reach: one per CU
 constexpr int kGemvMaxSplit = 4;
+constexpr int kGemvSplitAbove = 4096;  // K slices at most this wide are not split further
 // Packed W (ember_hip_gemv_pack): for each 16-feature tile and 32-wide k step,
 // the MFMA A operand as the 64 lanes take it, 8 halves per lane (lane 16 g + c:
 // row 16 tile + c, k 32 step + 8 g ..): one contiguous 1 KiB per load
@@ -424,11 +425,18 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_wide_kernel(const f16 *__re
 }
 
 // Work-groups per 16 features: doubled while the launch has fewer than
-// kGemvTargetGroups and each slice keeps at least one 32-wide k step per wave.
+// kGemvTargetGroups, the slice is wider than kGemvSplitAbove, and each slice
+// keeps at least one 32-wide k step per wave. A slice of 4096 or less runs in
+// at most two rounds of W loads per wave, and there the split's slice stores,
+// count-in and merge cost more than the spread over more CUs saves (per
+// launch, unsplit against split: 1024 x 2048 at 8 tokens 4.32 against 5.82 us
+// in 4 slices; 2048 x 2048 at 32 tokens 5.62 against 6.65 us in 2; 1024 x
+// 3072 at 8 tokens 5.78 against 6.14 in 4). At 2048 x 6144, 2 slices still
+// win (9.08 against 9.88 us).
 int gemv_split(int N, int K) {
     const int nfb = (N + 15) / 16;
     int ks = 1;
-    while (ks < kGemvMaxSplit && nfb * ks < kGemvTargetGroups && K % (2 * ks * 32) == 0 &&
+    while (ks < kGemvMaxSplit && nfb * ks < kGemvTargetGroups && K / ks > kGemvSplitAbove && K % (2 * ks * 32) == 0 &&
            K / (2 * ks) >= 32 * kGemvWaves)
         ks *= 2;
     return ks;

@@ -251,8 +251,8 @@ typedef struct EmberGemvArgs {
 
 /* C[M, N] = A[M, K] . W[N, K]^T, f16 in, f32 accumulation, then the epilogue
  * (silu_mul: N even, C has N / 2 columns). MFMA tiles of 16 features x 16
- * tokens, 8 waves splitting K; with a workspace and few features, 2 or 4
- * work-groups per 16 features each take a K slice, and the last to finish
+ * tokens, 8 waves splitting K; with a workspace, few features and K beyond
+ * 4096, 2 or 4 work-groups per 16 features each take a K slice, and the last to finish
  * adds the slices in slice order (deterministic; the split depends on N and
  * K only, so a token's result does not depend on the batch). Replaces
  * cuda::gemm with GemmKernel::gemv_tc (kernels.cuh:40-41; k_gemm.cu:302-425,

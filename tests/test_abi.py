@@ -93,16 +93,20 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
 
 
 def test_gemv_workspace_sizes():
-    """The K split is taken only when N / 16 gives fewer than 256 work-groups, in powers of two up to 4, with at
-    least 256 of K per slice; its workspace is the 16-feature counters (padded to 256 bytes) plus the slice sums."""
+    """The K split is taken only when N / 16 gives fewer than 256 work-groups and the slice would be wider than
+    4096, in powers of two up to 4, with at least 256 of K per slice; its workspace is the 16-feature counters
+    (padded to 256 bytes) plus the slice sums."""
     lib = _lib.lib()
     size = lib.ember_hip_gemv_workspace_bytes
     assert size(32, 4096, 2048) == 0  # 256 work-groups already: no split
-    assert size(32, 2048, 2048) == 512 + 2 * 128 * 2 * 1024  # the o projection: 2 slices of 1024
-    assert size(64, 1024, 2048) == 256 + 4 * 64 * 4 * 1024  # 4 slices of 512
-    assert size(1, 256, 512) == 256 + 2 * 16 * 1 * 1024  # 512 / 4 = 128 would leave a wave without a k step
+    assert size(32, 2048, 2048) == 0  # the o projection: K 2048 is not split
+    assert size(64, 1024, 3072) == 0  # nor 3072
+    assert size(32, 2048, 4096) == 0  # nor 4096
+    assert size(8, 2048, 6144) == 512 + 2 * 128 * 1 * 1024  # Qwen3-1.7B's down projection: 2 slices of 3072
+    assert size(16, 1024, 12288) == 256 + 4 * 64 * 1 * 1024  # 4 slices of 3072
+    assert size(32, 4096, 8192) == 0  # 256 work-groups already
     assert size(3, 130, 256) == 0  # K too short to split
-    assert size(65, 2048, 2048) == 0 and size(32, 2048, 40) == 0  # invalid shapes: no workspace
+    assert size(65, 2048, 6144) == 0 and size(32, 2048, 40) == 0  # invalid shapes: no workspace
 
 
 def test_gemv_pack_sizes_and_errors():

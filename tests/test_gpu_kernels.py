@@ -587,16 +587,17 @@ def _linear_err(got, want):
 @pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (8, 512, 1024), (13, 200, 128), (31, 384, 512),
                                    (64, 256, 1024), (32, 4096, 2048), (32, 2048, 2048), (17, 48, 32),
                                    (16, 1024, 2048), (8, 1024, 3072), (5, 4096, 1024),
+                                   (8, 2048, 6144), (16, 1024, 12288),
                                    (3, 70000, 256), (16, 66000, 1024)])
 @pytest.mark.parametrize("ep", [0, 1, 2, 3])
 @pytest.mark.parametrize("split", [False, True])
 def test_gemv_matches_oracle(device, M, N, KD, ep, split):
-    """Every epilogue on the reference test's decode-sized shapes (K a multiple of 32) and the Qwen3-1.7B
-    projections; ragged M and N exercise the clamped rows. With a workspace, the shapes with few features take
-    the K split: 2 or 4 slices, with 1 to 4 k steps per wave in a slice (16 x 1024 x 2048 and 8 x 1024 x 3072
-    are 4-way splits with 2 and 3), and 5 x 4096 x 1024 unsplit with 4 steps per wave. 70,000 and 66,000
-    features take the wide form (four tiles per work-group; the last block ragged). Bound 2e-3 as in the
-    reference's test."""
+    """Every epilogue on the reference test's decode-sized shapes (K a multiple of 32) and the Qwen3 projections;
+    ragged M and N exercise the clamped rows. With a workspace, the shapes with few features and K beyond 4096
+    take the K split: 8 x 2048 x 6144 in 2 slices and 16 x 1024 x 12288 in 4, each slice 12 k steps per wave (a
+    round of 8, then one of 4). Unsplit, 16 x 1024 x 2048 and 8 x 1024 x 3072 run 8 and 12 steps per wave, 5 x
+    4096 x 1024 4, and the short shapes 1 to 3. 70,000 and 66,000 features take the wide form (four tiles per
+    work-group; the last block ragged). Bound 2e-3 as in the reference's test."""
     from ember_amd import _lib
     rng = np.random.default_rng(M * 7919 + N * 31 + KD + ep)
     a = (rng.standard_normal((M, KD))).astype(np.float16)
@@ -615,12 +616,12 @@ def test_gemv_matches_oracle(device, M, N, KD, ep, split):
     assert _linear_err(got, want) < 2e-3
 
 
-@pytest.mark.parametrize("N,KD", [(4096, 2048), (2048, 4096), (1024, 3072)])
+@pytest.mark.parametrize("N,KD", [(4096, 2048), (2048, 6144), (1024, 3072)])
 @pytest.mark.parametrize("ep", [0, 2])
 def test_gemv_rows_do_not_depend_on_the_batch(device, N, KD, ep):
     """A token's outputs are the same bits whatever the batch around it. The batches here take both activation
-    paths: up to 32 rows of a 2048-wide K slice (or 48 of 1024) are staged in LDS, 64 rows of one are read straight
-    from A. The split shapes (2048 x 4096 over 2 slices, 1024 x 3072 over 4) go through the merge too."""
+    paths: up to 32 rows of a 2048-wide K slice (16 of a 3072-wide one) are staged in LDS, more rows are read
+    straight from A. The split shape (2048 x 6144 over 2 slices) goes through the merge too."""
     from ember_amd import _lib
     rng = np.random.default_rng(N + KD + ep)
     a = torch.from_numpy(rng.standard_normal((64, KD)).astype(np.float16)).to(device)
@@ -643,12 +644,13 @@ def test_gemv_rows_do_not_depend_on_the_batch(device, N, KD, ep):
 
 
 def test_gemv_split_is_deterministic_and_leaves_counters_zero(device):
-    """The K-split merge: the o projection's shape (2048 features, 2 slices) gives the same bits on every launch
-    (the slices are added in slice order, whichever work-group merges), agrees with the unsplit launch within
-    f32 reassociation, leaves its counters at zero, and a smaller batch right after reuses the workspace."""
+    """The K-split merge: Qwen3-1.7B's down projection shape (2048 features, K 6144 in 2 slices) gives the same
+    bits on every launch (the slices are added in slice order, whichever work-group merges), agrees with the
+    unsplit launch within f32 reassociation, leaves its counters at zero, and a smaller batch right after reuses
+    the workspace."""
     from ember_amd import _lib
     rng = np.random.default_rng(5)
-    M, N, KD = 32, 2048, 2048
+    M, N, KD = 32, 2048, 6144
     a = torch.from_numpy(rng.standard_normal((M, KD)).astype(np.float16)).to(device)
     w = torch.from_numpy((rng.standard_normal((N, KD)) * 0.05).astype(np.float16)).to(device)
     ws = K.gemv_workspace(M, N, KD, device)
@@ -690,7 +692,7 @@ def test_gemv_pack_layout(device):
 
 
 @pytest.mark.parametrize("M,N,KD", [(1, 256, 512), (3, 130, 256), (16, 1024, 2048), (32, 4096, 2048),
-                                   (8, 1024, 3072), (64, 256, 1024), (3, 70000, 256), (17, 48, 32)])
+                                   (8, 1024, 3072), (8, 2048, 6144), (64, 256, 1024), (3, 70000, 256), (17, 48, 32)])
 @pytest.mark.parametrize("ep", [0, 1, 2, 3])
 def test_gemv_packed_equals_row_major(device, M, N, KD, ep):
     """A packed W changes only where each lane's 16 bytes come from: the product is the same bits, with and without
