@@ -98,6 +98,16 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     const int fb = static_cast<int>(blockIdx.x), nfb = static_cast<int>(gridDim.x);
     const int ks = SPLIT ? static_cast<int>(blockIdx.y) : 0, KS = SPLIT ? static_cast<int>(gridDim.y) : 1;
     const int n0 = fb * 16;
+    // An unsplit launch may give its work-groups one group of MT token tiles
+    // each (blockIdx.z): rows 16 MT z ... of A and C. A row's arithmetic does
+    // not depend on the group, so the bits are those of one wider group.
+    if constexpr (!SPLIT) {
+        const int m0 = 16 * MT * static_cast<int>(blockIdx.z);
+        constexpr int out_bytes = EP == EMBER_EPILOGUE_STORE_F32 || EP == EMBER_EPILOGUE_ADD_F32 ? 4 : 2;
+        A += static_cast<int64_t>(m0) * lda;
+        C = static_cast<char *>(C) + static_cast<int64_t>(m0) * ldc * out_bytes;
+        M -= m0;
+    }
     const int kw = K / KS, k0 = ks * kw;  // this work-group's K slice, a multiple of 32 wide
     // Row-major W: this lane's row (rows past N repeat the last), k step s at
     // +32 s. Packed W: the tile's k steps are 1 KiB blocks in lane order.
@@ -457,7 +467,14 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     const bool split = need > 0 && a.workspace && a.workspace_bytes >= need;
     const int nfb = (a.N + 15) / 16;
     const int ks = split ? gemv_split(a.N, a.K) : 1;
-    const dim3 grid(static_cast<unsigned>(nfb), static_cast<unsigned>(ks));
+    // With fewer 16-feature blocks than kGemvTargetGroups and no K split, each
+    // work-group takes one 16-token tile (grid z): twice the work-groups at 17
+    // to 32 tokens, each staging half the activations. Blocks z and z + 1 of
+    // one feature block are nfb apart in launch order, on one XCD when nfb is
+    // a multiple of 8, so the second read of W can come from its L2.
+    const int tiles = (a.M + 15) / 16;
+    const int mt = !split && tiles > 1 && nfb < kGemvTargetGroups ? 1 : tiles;  // token tiles per work-group
+    const dim3 grid(static_cast<unsigned>(nfb), static_cast<unsigned>(ks), static_cast<unsigned>(tiles / mt));
     uint32_t *counters = split ? static_cast<uint32_t *>(a.workspace) : nullptr;
     float *slices = split ? reinterpret_cast<float *>(static_cast<char *>(a.workspace) + (nfb * 4 + 255) / 256 * 256)
                           : nullptr;
@@ -465,7 +482,7 @@ hipError_t launch_gemv_ep(const EmberGemvArgs &a, hipStream_t stream) {
     const f16 *W = static_cast<const f16 *>(a.W);
     // Stage the activations when the slice's rows fit and their 16-byte
     // pieces per row are a multiple of 16 (the swizzle's period).
-    const int mt = (a.M + 15) / 16, kw = a.K / ks;
+    const int kw = a.K / ks;
     const int stage = 16 * mt * kw * 2;
     const bool staged = kw % 128 == 0 && stage <= kGemvMaxStage;
     const int lds = staged ? std::max(stage, mt * kGemvRedBytes) : mt * kGemvRedBytes;

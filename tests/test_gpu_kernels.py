@@ -616,12 +616,13 @@ def test_gemv_matches_oracle(device, M, N, KD, ep, split):
     assert _linear_err(got, want) < 2e-3
 
 
-@pytest.mark.parametrize("N,KD", [(4096, 2048), (2048, 6144), (1024, 3072)])
+@pytest.mark.parametrize("N,KD", [(4096, 2048), (2048, 2048), (2048, 6144), (1024, 3072)])
 @pytest.mark.parametrize("ep", [0, 2])
 def test_gemv_rows_do_not_depend_on_the_batch(device, N, KD, ep):
     """A token's outputs are the same bits whatever the batch around it. The batches here take both activation
     paths: up to 32 rows of a 2048-wide K slice (16 of a 3072-wide one) are staged in LDS, more rows are read
-    straight from A. The split shape (2048 x 6144 over 2 slices) goes through the merge too."""
+    straight from A. With fewer than 256 feature blocks (2048 and 1024 features) a batch of more than 16 tokens
+    runs one 16-token tile per work-group. The split shape (2048 x 6144 over 2 slices) goes through the merge."""
     from ember_amd import _lib
     rng = np.random.default_rng(N + KD + ep)
     a = torch.from_numpy(rng.standard_normal((64, KD)).astype(np.float16)).to(device)
