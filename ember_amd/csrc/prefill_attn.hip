@@ -53,6 +53,7 @@ constexpr int kMergeSlots = 10;        // float4 slots per lane of a key group's
 constexpr int kKRow = kHeadDim + 16;
 constexpr int kVRow = kHeadDim + 16;              // LDS row of V (one key), halves: 72 dwords, rows 8 banks apart
 constexpr int kVAhead = 2;                        // V operand reads in flight ahead of their MFMAs
+constexpr int kDescWord3 = 0x00020000;            // gfx9 raw buffer: 32-bit data format, no swizzle
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 // The transposing LDS read's operand type. Its v4i16 form, with each element
@@ -153,31 +154,36 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     // Pages past the tile's last position or outside the pool give zeros, and
     // so do V slots past the last position (an unwritten slot may hold
     // anything, and P = 0 must not meet a NaN).
+    // Each load goes through a buffer descriptor of the kv head's page (built
+    // in scalar registers from the wave-uniform block id): a page past the
+    // tile's keys or outside the pool gets a descriptor with no records, and
+    // V's covers only the slots up to the last position, so those loads
+    // return zeros with no branch and no register cleared beforehand.
     constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kGroupThreads;
     const int wl_u = __builtin_amdgcn_readfirstlane(wl);
     const int64_t page_elems = static_cast<int64_t>(a.n_kv) * kPage * kHeadDim;
-    uint32_t koff[kChunks];
+    const int64_t head_elems = static_cast<int64_t>(kvh) * kPage * kHeadDim;
+    const int last_page = max_pos / kPage;
+    uint32_t koff[kChunks];  // bytes from the kv head's page start
 #pragma unroll
     for (int j = 0; j < kChunks; j++) {
         const int chunk = tg + j * kGroupThreads;
-        koff[j] = static_cast<uint32_t>((kvh * kPage + (chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8);
+        koff[j] = static_cast<uint32_t>((((chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8) * 2);
     }
     auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
-        const bool whole = kb * kKeyBlock + kKeyBlock - 1 <= max_pos;  // no slot past the last position
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
             const int pg = 2 * kb + (wl_u * kWave + j * kGroupThreads) / (kPage * 16);  // wave-uniform
-            kv4[j] = make_uint4(0, 0, 0, 0);
-            vq[j] = make_uint4(0, 0, 0, 0);
-            if (kb < n_blocks && pg * kPage <= max_pos) {
-                const int blk = table[pg];
-                if (blk >= 0 && blk < a.num_blocks) {
-                    const f16 *kp = kc + blk * page_elems, *vp = vc + blk * page_elems;
-                    kv4[j] = *reinterpret_cast<const uint4 *>(kp + koff[j]);
-                    vq[j] = *reinterpret_cast<const uint4 *>(vp + koff[j]);
-                    if (!whole && kb * kKeyBlock + (tg + j * kGroupThreads) / 16 > max_pos) vq[j] = make_uint4(0, 0, 0, 0);
-                }
-            }
+            const int blk = table[min(pg, last_page)];
+            const bool live = kb < n_blocks && pg <= last_page && blk >= 0 && blk < a.num_blocks;
+            const int64_t at = (live ? blk : 0) * page_elems + head_elems;
+            const int vslots = live ? min(kPage, max_pos - pg * kPage + 1) : 0;  // V slots up to the last position
+            const __amdgpu_buffer_rsrc_t kd = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<f16 *>(kc + at), 0, live ? kPage * kHeadDim * 2 : 0, kDescWord3);
+            const __amdgpu_buffer_rsrc_t vd =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<f16 *>(vc + at), 0, vslots * kHeadDim * 2, kDescWord3);
+            kv4[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kd, koff[j], 0, 0));
+            vq[j] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vd, koff[j], 0, 0));
         }
     };
     auto stage = [&](int buf, const uint4 (&kv4)[kChunks], const uint4 (&vq)[kChunks]) {
