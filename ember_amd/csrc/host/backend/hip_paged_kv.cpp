@@ -6,6 +6,9 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <functional>
+#include <queue>
+#include <utility>
 
 #include "common/error.hpp"
 #include "kernels.hpp"
@@ -293,16 +296,17 @@ void HipPagedKv::plan(const StepBatch &b, int graph_splits) {
         const int groups = std::max(1, cu_count_ / cfg_.n_kv_heads);
         std::vector<Item> order(items);
         if (n >= groups * kDecodeWgPerCu) {
-            std::vector<int64_t> load(static_cast<size_t>(groups), 0);
+            // (keys so far, group) of the groups with a free slot, least keys
+            // first, then the lowest group
+            std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>, std::greater<>> open;
+            for (int g = 0; g < groups; g++) open.emplace(0, g);
             std::vector<std::vector<Item>> dealt(static_cast<size_t>(groups));
             for (int i = 0; i < groups * kDecodeWgPerCu; i++) {
-                int g = -1;
-                for (int h = 0; h < groups; h++)
-                    if (static_cast<int>(dealt[static_cast<size_t>(h)].size()) < kDecodeWgPerCu &&
-                        (g < 0 || load[static_cast<size_t>(h)] < load[static_cast<size_t>(g)]))
-                        g = h;
+                const auto [load, g] = open.top();
+                open.pop();
                 dealt[static_cast<size_t>(g)].push_back(items[static_cast<size_t>(i)]);
-                load[static_cast<size_t>(g)] += items[static_cast<size_t>(i)].keys;
+                if (static_cast<int>(dealt[static_cast<size_t>(g)].size()) < kDecodeWgPerCu)
+                    open.emplace(load + items[static_cast<size_t>(i)].keys, g);
             }
             for (int g = 0; g < groups; g++) {
                 std::reverse(dealt[static_cast<size_t>(g)].begin(), dealt[static_cast<size_t>(g)].end());
