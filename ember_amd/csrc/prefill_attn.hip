@@ -69,7 +69,12 @@ constexpr float kLazyLog2 = 8.0f;
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int HG>  // query heads per work-group (1 or 2), all of one kv head
-__global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillArgs a, float scale_log2) {
+__global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillArgs a, float scale_log2_arg) {
+    // Kernel arguments used inside the key loop are taken into scalar registers once: left as they are, the
+    // compiler reloads them from the argument segment every step, and each reload is one more scalar round
+    // trip ahead of the step's LDS waits (lgkmcnt counts both).
+    const float scale_log2 = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, scale_log2_arg)));
+    const int pool_blocks = __builtin_amdgcn_readfirstlane(a.num_blocks);
     constexpr int kPThreads = kThreadsFor<HG>;
     constexpr int kGroupThreads = kPThreads / 2;       // one key group
     constexpr int kGroupWaves = kGroupThreads / kWave; // 4 x HG: wave w takes tokens 16 (w % 4).. and head w / 4
@@ -170,12 +175,22 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         const int chunk = tg + j * kGroupThreads;
         koff[j] = static_cast<uint32_t>((((chunk / 16) % kPage) * kHeadDim + (chunk % 16) * 8) * 2);
     }
-    auto fetch = [&](int kb, uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
+    // The block ids of block kb's pages for this wave's chunks (scalar loads), read one step before the
+    // fetch that uses them, next to the step's LDS stores: their round trip then ends inside the wait that
+    // precedes the barrier instead of at the top of the next step.
+    auto fetch_ids = [&](int kb, int (&ids)[kChunks]) {
+#pragma unroll
+        for (int j = 0; j < kChunks; j++)
+            ids[j] = table[min(2 * kb + (wl_u * kWave + j * kGroupThreads) / (kPage * 16), last_page)];
+    };
+    auto fetch = [&](int kb, const int (&ids)[kChunks], uint4 (&kv4)[kChunks], uint4 (&vq)[kChunks]) {
 #pragma unroll
         for (int j = 0; j < kChunks; j++) {
             const int pg = 2 * kb + (wl_u * kWave + j * kGroupThreads) / (kPage * 16);  // wave-uniform
-            const int blk = table[min(pg, last_page)];
-            const bool live = kb < n_blocks && pg <= last_page && blk >= 0 && blk < a.num_blocks;
+            const int blk = ids[j];
+            // Bitwise, not short-circuit: a branch here let the compiler sink the second id's load past the
+            // first chunk's loads, two scalar round trips per step instead of one.
+            const bool live = (kb < n_blocks) & (pg <= last_page) & (blk >= 0) & (blk < pool_blocks);
             const int64_t at = (live ? blk : 0) * page_elems + head_elems;
             const int vslots = live ? min(kPage, max_pos - pg * kPage + 1) : 0;  // V slots up to the last position
             const __amdgpu_buffer_rsrc_t kd = __builtin_amdgcn_make_buffer_rsrc(
@@ -205,20 +220,24 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     // during step s - 1 into one register set while the other set, staged at
     // the end of step s - 1, now takes block 2 (s + 2) + grp. The two sets
     // alternate, so the loop is unrolled by two to keep them in registers.
-    // Measured at config 3: 64.0 -> 61.9 us with two steps ahead (120 VGPRs);
-    // one query head per work-group stays at one step (132 VGPRs with two).
-    constexpr int kAhead = HG == 2 ? 2 : 1;
+    // Measured at config 3: 64.0 -> 61.9 us with two steps ahead (two query
+    // heads per work-group, 120 VGPRs). One query head per work-group runs
+    // two ahead as well at 128 VGPRs (four waves per SIMD still).
+    constexpr int kAhead = 2;
     const int n_steps = (n_blocks + 1) / 2;
     uint4 nk0[kChunks], nv0[kChunks], nk1[kChunks], nv1[kChunks];
-    fetch(grp, nk0, nv0);
-    if constexpr (kAhead == 2) fetch(grp + 2, nk1, nv1);
+    int idn[kChunks];
+    fetch_ids(grp, idn);
+    fetch(grp, idn, nk0, nv0);
+    fetch_ids(grp + 2, idn);
+    fetch(grp + 2, idn, nk1, nv1);
+    fetch_ids(grp + 2 * kAhead, idn);  // the first step's fetch
     stage(0, nk0, nv0);
     __syncthreads();
     auto step = [&](int st, uint4 (&nk_free)[kChunks], uint4 (&nv_free)[kChunks], uint4 (&nk_next)[kChunks],
                     uint4 (&nv_next)[kChunks]) {
         const int buf = st & 1, kb = 2 * st + grp;
-        if constexpr (kAhead == 2) fetch(kb + 4, nk_free, nv_free);  // in flight while this block
-        else fetch(kb + 2, nk_next, nv_next);                         // and the next compute
+        fetch(kb + 2 * kAhead, idn, nk_free, nv_free);  // in flight while this block and the next compute
         if (kb < n_blocks) {
             const f16 *kl = k_lds(buf), *vl = v_lds(buf);
             // S^T: lane l holds query ql and keys 16 h + 4g + r (h = half, r = 0..3).
@@ -299,6 +318,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        fetch_ids(kb + 2 * kAhead + 2, idn);  // the next step's fetch
         if (kb + 2 < n_blocks) stage(buf ^ 1, nk_next, nv_next);
         __syncthreads();
     };
