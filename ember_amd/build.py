@@ -70,9 +70,13 @@ def common_flags() -> list[str]:
 
 # Per-source additions. The decode kernel rescales its MFMA accumulators on the
 # VALU every page: they stay in VGPRs (the VGPR form of v_mfma) instead of
-# being copied out of and back into AGPRs around each rescale.
+# being copied out of and back into AGPRs around each rescale. Its first two
+# kernel arguments (the work descriptors' address and n_kv) are preloaded into
+# scalar registers at launch, so a work-group's descriptor load does not wait
+# for a kernel-argument load first (gfx950 supports the preload; the code
+# object carries a prologue that loads them itself where the firmware does not).
 EXTRA_FLAGS = {
-    "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=2"],
 }
 
 

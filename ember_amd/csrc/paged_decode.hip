@@ -87,7 +87,11 @@ constexpr int kThreads = kWaves * kWave;
 // the first entry's token when the run's tokens and positions both count up by
 // one (else -1), then the block ids of the split's first 8 pages (-1 past its
 // last page). One s_load_dwordx16 gives a work-group everything it needs to
-// issue its first page loads.
+// issue its first page loads. The descriptors' address and n_kv come as the
+// kernel's two leading arguments, which build.py has the compiler preload into
+// scalar registers at launch (-amdgpu-kernarg-preload-count=2): the descriptor
+// load then goes out at once, beside the first kernel-argument loads, instead
+// of after their round trip.
 typedef int32_t WorkDesc __attribute__((ext_vector_type(16)));
 constexpr int kDescTok = 7, kDescBlocks = 8;
 
@@ -425,7 +429,8 @@ __device__ __forceinline__ void phase_break() { __builtin_amdgcn_sched_barrier(0
 // entry `bid` of the work list (item bid / n_kv, kv head bid % n_kv). tid is
 // the thread's index in the work-group.
 template <typename T, int ROWS, bool FUSED>
-__device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid, const int tid) {
+__device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDesc *descs, const int n_kv_pre,
+                                            const int bid, const int tid) {
     constexpr int D = kHeadDim;
     constexpr int NEW = FUSED ? EMBER_MAX_RUN : 1;
     const int lane = tid % kWave;
@@ -437,20 +442,23 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
     // and a late work-group's first loads wait behind them for microseconds.
     __builtin_amdgcn_s_setprio(3);
 
+    // descs: the work list's descriptors (preloaded argument), or null when the
+    // launch has none; n_kv_pre = p.n_kv, preloaded too.
     int run, kvh, split;
     WorkDesc desc = {};
-    const bool have_desc = p.work && p.work_desc;
-    if (p.work) {
+    const bool have_desc = descs != nullptr;
+    if (have_desc) {
+        const int item = bid / n_kv_pre;
+        kvh = bid % n_kv_pre;
+        desc = uniform_load(descs + item);  // one s_load_dwordx16
+        run = desc[0];
+        split = desc[1];
+        if (run < 0 || run >= p.num_runs || split < 0 || split >= p.num_splits) return;  // whole work-group
+    } else if (p.work) {
         const int item = bid / p.n_kv;
         kvh = bid % p.n_kv;
-        if (have_desc) {
-            desc = uniform_load(reinterpret_cast<const WorkDesc *>(p.work_desc) + item);  // one s_load_dwordx16
-            run = desc[0];
-            split = desc[1];
-        } else {
-            run = uniform_load(p.work + 2 * item);
-            split = uniform_load(p.work + 2 * item + 1);
-        }
+        run = uniform_load(p.work + 2 * item);
+        split = uniform_load(p.work + 2 * item + 1);
         if (run < 0 || run >= p.num_runs || split < 0 || split >= p.num_splits) return;  // whole work-group
     } else {
         run = bid;
@@ -1186,8 +1194,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const int bid
 }
 
 template <typename T, int ROWS, bool FUSED>
-__global__ void __launch_bounds__(kThreads) paged_decode_kernel(DecodeParams p) {
-    decode_item<T, ROWS, FUSED>(p, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
+__global__ void __launch_bounds__(kThreads) paged_decode_kernel(const WorkDesc *descs, int n_kv, DecodeParams p) {
+    decode_item<T, ROWS, FUSED>(p, descs, n_kv, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
 }
 
 // The split merge as its own launch: one work-group per (token, head).
@@ -1206,10 +1214,13 @@ hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_
     const dim3 grid = p.work ? dim3(static_cast<unsigned>(num_work * p.n_kv))
                              : dim3(static_cast<unsigned>(runs), static_cast<unsigned>(p.n_kv),
                                     static_cast<unsigned>(p.num_splits));
+    // The descriptors go with the work list only (a launch without one indexes by grid position).
+    const WorkDesc *descs = p.work && p.work_desc ? reinterpret_cast<const WorkDesc *>(p.work_desc) : nullptr;
     if (start || stop)
-        hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, start, stop, 0, p);
+        hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, start, stop, 0,
+                              descs, p.n_kv, p);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, descs, p.n_kv, p);
     return hipGetLastError();
 }
 
