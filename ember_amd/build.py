@@ -75,8 +75,12 @@ def common_flags() -> list[str]:
 # scalar registers at launch, so a work-group's descriptor load does not wait
 # for a kernel-argument load first (gfx950 supports the preload; the code
 # object carries a prologue that loads them itself where the firmware does not).
+# The linear layers' kernels take plain arguments: their first nine (the
+# GEMV's operands, shapes and staging constant; all of RMSNorm's) are
+# preloaded, so their first loads issue at once.
 EXTRA_FLAGS = {
     "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=2"],
+    "linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 
