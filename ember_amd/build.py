@@ -81,6 +81,7 @@ def common_flags() -> list[str]:
 EXTRA_FLAGS = {
     "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=2"],
     "linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+    "kv_append.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
 }
 
 
