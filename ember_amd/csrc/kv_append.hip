@@ -103,7 +103,11 @@ __global__ void __launch_bounds__(kWavesPerBlock * kWave)
     const bool is_q = head < n_heads, is_k = !is_q && head < n_heads + n_kv;
     const int page = pos / kPage;
     const bool slot_ok = pos >= 0 && page < max_blocks;
-    const int block = block_tables[static_cast<int64_t>(seq) * max_blocks + min(max(page, 0), max_blocks - 1)];
+    // The index is clamped into the row (a position outside the table stores nothing) and a negative
+    // sequence reads row 0, so the load needs no branch: a select here made the compiler load the
+    // sequence inside a branch, one more round trip.
+    const int block =
+        block_tables[static_cast<int64_t>(max(seq, 0)) * max_blocks + min(max(page, 0), max_blocks - 1)];
     // Taken here, while the head's elements are still in flight: left to itself the
     // compiler issued this load after the sine and cosine, where the shuffles' LDS
     // waits (lgkmcnt, which counts scalar loads too) then waited for it.
