@@ -69,7 +69,13 @@ constexpr float kLazyLog2 = 8.0f;
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int HG>  // query heads per work-group (1 or 2), all of one kv head
-__global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillArgs a, float scale_log2_arg) {
+__global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(const int32_t *tile_start, const int32_t *tile_end,
+                                                                  const int32_t *tile_seq, const int32_t *positions,
+                                                                  const int32_t *block_tables, int n_heads,
+                                                                  int n_kv, int max_blocks, EmberPrefillArgs a,
+                                                                  float scale_log2_arg) {
+    // The leading arguments (what the first loads need) are preloaded into scalar registers at launch
+    // (build.py: -amdgpu-kernarg-preload-count=8); `a` carries the rest.
     // Kernel arguments used inside the key loop are taken into scalar registers once: left as they are, the
     // compiler reloads them from the argument segment every step, and each reload is one more scalar round
     // trip ahead of the step's LDS waits (lgkmcnt counts both).
@@ -93,15 +99,15 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     // Work-group id -> (tile, head pair), head pairs fastest: ids that differ by
     // a multiple of 8 run on one XCD, so with 8 head pairs every tile of one
     // (sequence, kv head) shares that XCD's L2 for the keys they all read.
-    const int n_pairs = a.n_heads / HG;
+    const int n_pairs = n_heads / HG;
     const int tile = static_cast<int>(blockIdx.x) / n_pairs;
     const int pair = static_cast<int>(blockIdx.x) % n_pairs;
     const int head = pair * HG + wl / 4;
-    const int G = a.n_heads / a.n_kv;
+    const int G = n_heads / n_kv;
     const int kvh = pair * HG / G;
-    const int t0 = a.tile_start[tile];
-    const int nt = min(a.tile_end[tile] - t0, kTileTokens);
-    const int32_t *table = a.block_tables + static_cast<int64_t>(a.tile_seq[tile]) * a.max_blocks;
+    const int t0 = tile_start[tile], t_end = tile_end[tile], seq = tile_seq[tile];
+    const int nt = min(t_end - t0, kTileTokens);
+    const int32_t *table = block_tables + static_cast<int64_t>(seq) * max_blocks;
     const f16 *q = static_cast<const f16 *>(a.q);
     const f16 *kc = static_cast<const f16 *>(a.k_cache);
     const f16 *vc = static_cast<const f16 *>(a.v_cache);
@@ -111,7 +117,36 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     // This lane's query (token 16 (wl % 4) + ql of the tile) and the tile's key range.
     const int my_i = 16 * (wl % 4) + ql;
     const bool my_ok = my_i < nt;
-    const int my_pos = my_ok ? a.positions[t0 + my_i] : -1;
+    // One query head per work-group (launches of one round, where every work-group's prologue is on the
+    // launch's critical path): every load the first blocks need goes out here, before the positions'
+    // reduction and its barrier, unguarded: this lane's position and Q (a row past the tile reads the
+    // tile's last token; its position still counts as -1 and its Q as 0), and the block ids of the first
+    // three fetches, clamped into the table's row (the fetches test the page against the last one
+    // later). Config 3: 55.4-55.6 against 56.3-56.4 us per launch. Two heads per work-group keep their
+    // loads after the barrier: early, they cost config 4's many-round launches 1.7%.
+    constexpr bool kEarly = HG == 1;
+    const int my_row = t0 + min(my_i, nt - 1);
+    const int wl_pre = __builtin_amdgcn_readfirstlane(wl);
+    constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kGroupThreads;  // 16-byte chunks per thread and tensor
+    f16x8 qb[4];  // Q^T operands: for 32-dim chunk c, dims 32c + 8g .. + 8 of this lane's query
+    int ids_pre[3][kChunks];
+    int my_pos;
+    if constexpr (kEarly) {
+        const int pos_raw = positions[my_row];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            qb[c] = *reinterpret_cast<const f16x8 *>(q + (static_cast<int64_t>(my_row) * n_heads + head) * kHeadDim +
+                                                     32 * c + 8 * g);
+#pragma unroll
+        for (int b = 0; b < 3; b++)
+#pragma unroll
+            for (int j = 0; j < kChunks; j++)
+                ids_pre[b][j] = table[min(2 * (grp + 2 * b) + (wl_pre * kWave + j * kGroupThreads) / (kPage * 16),
+                                          max_blocks - 1)];
+        my_pos = my_ok ? pos_raw : -1;
+    } else {
+        my_pos = my_ok ? positions[t0 + my_i] : -1;
+    }
     int mx = my_pos, mn_pos = my_pos;
     for (int o = 32; o > 0; o >>= 1) {
         mx = max(mx, __shfl_xor(mx, o, kWave));
@@ -124,18 +159,21 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     __syncthreads();
     int max_pos = wave_max[0];
     for (int w = 1; w < kWavesP; w++) max_pos = max(max_pos, wave_max[w]);
-    max_pos = __builtin_amdgcn_readfirstlane(min(max_pos, a.max_blocks * kPage - 1));
+    max_pos = __builtin_amdgcn_readfirstlane(min(max_pos, max_blocks * kPage - 1));
     const int n_blocks = (max_pos + kKeyBlock) / kKeyBlock;
 
-    // Q^T operands: for 32-dim chunk c, dims 32c + 8g .. + 8 of this lane's query.
-    f16x8 qb[4];
+    if constexpr (kEarly) {
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        f16x8 v = {};
-        if (my_ok)
-            v = *reinterpret_cast<const f16x8 *>(q + (static_cast<int64_t>(t0 + my_i) * a.n_heads + head) * kHeadDim +
-                                                 32 * c + 8 * g);
-        qb[c] = v;
+        for (int c = 0; c < 4; c++) qb[c] = my_ok ? qb[c] : f16x8{};
+    } else {
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            f16x8 v = {};
+            if (my_ok)
+                v = *reinterpret_cast<const f16x8 *>(q + (static_cast<int64_t>(t0 + my_i) * n_heads + head) * kHeadDim +
+                                                     32 * c + 8 * g);
+            qb[c] = v;
+        }
     }
 
     float m = -INFINITY;  // the reference max of this lane's query (base 2, scaled)
@@ -164,9 +202,8 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     // tile's keys or outside the pool gets a descriptor with no records, and
     // V's covers only the slots up to the last position, so those loads
     // return zeros with no branch and no register cleared beforehand.
-    constexpr int kChunks = kKeyBlock * kHeadDim / 8 / kGroupThreads;
-    const int wl_u = __builtin_amdgcn_readfirstlane(wl);
-    const int64_t page_elems = static_cast<int64_t>(a.n_kv) * kPage * kHeadDim;
+    const int wl_u = wl_pre;
+    const int64_t page_elems = static_cast<int64_t>(n_kv) * kPage * kHeadDim;
     const int64_t head_elems = static_cast<int64_t>(kvh) * kPage * kHeadDim;
     const int last_page = max_pos / kPage;
     uint32_t koff[kChunks];  // bytes from the kv head's page start
@@ -227,11 +264,18 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
     const int n_steps = (n_blocks + 1) / 2;
     uint4 nk0[kChunks], nv0[kChunks], nk1[kChunks], nv1[kChunks];
     int idn[kChunks];
-    fetch_ids(grp, idn);
-    fetch(grp, idn, nk0, nv0);
-    fetch_ids(grp + 2, idn);
-    fetch(grp + 2, idn, nk1, nv1);
-    fetch_ids(grp + 2 * kAhead, idn);  // the first step's fetch
+    if constexpr (kEarly) {
+        fetch(grp, ids_pre[0], nk0, nv0);
+        fetch(grp + 2, ids_pre[1], nk1, nv1);
+#pragma unroll
+        for (int j = 0; j < kChunks; j++) idn[j] = ids_pre[2][j];  // the first step's fetch
+    } else {
+        fetch_ids(grp, idn);
+        fetch(grp, idn, nk0, nv0);
+        fetch_ids(grp + 2, idn);
+        fetch(grp + 2, idn, nk1, nv1);
+        fetch_ids(grp + 2 * kAhead, idn);  // the first step's fetch
+    }
     stage(0, nk0, nv0);
     __syncthreads();
     auto step = [&](int st, uint4 (&nk_free)[kChunks], uint4 (&nv_free)[kChunks], uint4 (&nk_next)[kChunks],
@@ -354,7 +398,7 @@ __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(EmberPrefillAr
         const float l = l_acc[r] * c0[r] + l1[r] * c1[r];
         const float inv = l > 0.0f ? 1.0f / l : 0.0f;
         if (i >= nt) continue;
-        f16 *row = out + (static_cast<int64_t>(t0 + i) * a.n_heads + head) * kHeadDim;
+        f16 *row = out + (static_cast<int64_t>(t0 + i) * n_heads + head) * kHeadDim;
 #pragma unroll
         for (int dt = 0; dt < 8; dt++) {
             const float o = o_acc[dt][r] * c0[r] + slot[dt * kWave][r] * c1[r];
@@ -370,9 +414,13 @@ hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEven
     const dim3 grid(static_cast<unsigned>(a.num_tiles * (a.n_heads / hg)));
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)
-        hipExtLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, start, stop, 0, a, scale_log2);
+        hipExtLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, start, stop, 0, a.tile_start,
+                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks, a,
+                              scale_log2);
     else
-        hipExtLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, start, stop, 0, a, scale_log2);
+        hipExtLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, start, stop, 0, a.tile_start,
+                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks, a,
+                              scale_log2);
     return hipGetLastError();
 }
 
