@@ -70,16 +70,17 @@ def common_flags() -> list[str]:
 
 # Per-source additions. The decode kernel rescales its MFMA accumulators on the
 # VALU every page: they stay in VGPRs (the VGPR form of v_mfma) instead of
-# being copied out of and back into AGPRs around each rescale. Its first two
-# kernel arguments (the work descriptors' address and n_kv) are preloaded into
-# scalar registers at launch, so a work-group's descriptor load does not wait
-# for a kernel-argument load first (gfx950 supports the preload; the code
-# object carries a prologue that loads them itself where the firmware does not).
+# being copied out of and back into AGPRs around each rescale. Its first seven
+# kernel arguments (the work descriptors' address, n_kv, the pools, the block
+# tables, qkv and the rotary frequencies) are preloaded into scalar registers at
+# launch, so a work-group's descriptor load does not wait for a kernel-argument
+# load first (gfx950 supports the preload; the code object carries a prologue
+# that loads them itself where the firmware does not).
 # The linear layers' kernels take plain arguments: their first nine (the
 # GEMV's operands, shapes and staging constant; all of RMSNorm's) are
 # preloaded, so their first loads issue at once.
 EXTRA_FLAGS = {
-    "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=2"],
+    "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=7"],
     "linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "kv_append.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "prefill_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],

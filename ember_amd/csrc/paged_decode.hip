@@ -87,11 +87,13 @@ constexpr int kThreads = kWaves * kWave;
 // the first entry's token when the run's tokens and positions both count up by
 // one (else -1), then the block ids of the split's first 8 pages (-1 past its
 // last page). One s_load_dwordx16 gives a work-group everything it needs to
-// issue its first page loads. The descriptors' address and n_kv come as the
-// kernel's two leading arguments, which build.py has the compiler preload into
-// scalar registers at launch (-amdgpu-kernarg-preload-count=2): the descriptor
-// load then goes out at once, beside the first kernel-argument loads, instead
-// of after their round trip.
+// issue its first page loads. The descriptors' address and n_kv, and the
+// pools, block tables, qkv and rotary frequencies that the first page and
+// query loads need, come as the kernel's leading arguments, which build.py has
+// the compiler preload into scalar registers at launch
+// (-amdgpu-kernarg-preload-count=7): the descriptor load then goes out at
+// once, beside the first kernel-argument loads, instead of after their round
+// trip.
 typedef int32_t WorkDesc __attribute__((ext_vector_type(16)));
 constexpr int kDescTok = 7, kDescBlocks = 8;
 
@@ -428,9 +430,19 @@ __device__ __forceinline__ void phase_break() { __builtin_amdgcn_sched_barrier(0
 // One work item: (run, kv head, split) = work-group `bid` of the dense grid or
 // entry `bid` of the work list (item bid / n_kv, kv head bid % n_kv). tid is
 // the thread's index in the work-group.
+struct Preloaded {  // the kernel's leading arguments, in scalar registers from launch on
+    const WorkDesc *descs;
+    int n_kv;
+    const void *k, *v;
+    const int32_t *tables;
+    const void *qkv;
+    const float *inv_freq;
+};
+
 template <typename T, int ROWS, bool FUSED>
-__device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDesc *descs, const int n_kv_pre,
-                                            const int bid, const int tid) {
+__device__ __forceinline__ void decode_item(const DecodeParams &p, const Preloaded &pre, const int bid, const int tid) {
+    const WorkDesc *descs = pre.descs;
+    const int n_kv_pre = pre.n_kv;
     constexpr int D = kHeadDim;
     constexpr int NEW = FUSED ? EMBER_MAX_RUN : 1;
     const int lane = tid % kWave;
@@ -507,7 +519,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDes
     };
     auto pos_of = [&](int i) { return counting ? desc[5] + i : uniform_load(p.positions + token_of(i)); };
     const int seq = have_desc ? desc[4] : uniform_load(p.token_seq + token_of(0));
-    const int32_t *table = p.tables + static_cast<int64_t>(seq) * p.max_blocks;
+    const int32_t *table = pre.tables + static_cast<int64_t>(seq) * p.max_blocks;
 
     // Per-row positions (for masking and RoPE); the page range needs only the
     // lowest and highest, which the descriptor already holds.
@@ -529,8 +541,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDes
     const int end = min(ctx_max, begin + p.split_len);
     const int run_splits = (ctx_max + p.split_len - 1) / p.split_len;
 
-    const T *kbase = static_cast<const T *>(p.k);
-    const T *vbase = static_cast<const T *>(p.v);
+    const T *kbase = static_cast<const T *>(pre.k);
+    const T *vbase = static_cast<const T *>(pre.v);
     const int64_t head_off = static_cast<int64_t>(kvh) * (kPage * kHeadDim);
     const int64_t block_stride = static_cast<int64_t>(p.n_kv) * (kPage * kHeadDim);
 
@@ -655,7 +667,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDes
         // trips) and the arithmetic overlaps the page loads. The barrier after
         // it waits for LDS only, not for the pages.
         const int n_total = p.n_heads + 2 * p.n_kv;
-        const T *qkv = static_cast<const T *>(p.qkv);
+        const T *qkv = static_cast<const T *>(pre.qkv);
         auto vec = [&](int t, int head) { return qkv + (static_cast<int64_t>(t) * n_total + head) * D; };
         const int kh = p.n_heads + kvh, vh = p.n_heads + p.n_kv + kvh;
 
@@ -678,8 +690,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDes
             va[k] = vs[lane];
             vb[k] = vs[lane + D / 2];
         }
-        const NormRopeLane qn = norm_rope_lane(p.q_norm, p.inv_freq, lane);
-        const NormRopeLane kn = norm_rope_lane(p.k_norm, p.inv_freq, lane);
+        const NormRopeLane qn = norm_rope_lane(p.q_norm, pre.inv_freq, lane);
+        const NormRopeLane kn = norm_rope_lane(p.k_norm, pre.inv_freq, lane);
 
         fetch_first(A);
 
@@ -1194,8 +1206,11 @@ __device__ __forceinline__ void decode_item(const DecodeParams &p, const WorkDes
 }
 
 template <typename T, int ROWS, bool FUSED>
-__global__ void __launch_bounds__(kThreads) paged_decode_kernel(const WorkDesc *descs, int n_kv, DecodeParams p) {
-    decode_item<T, ROWS, FUSED>(p, descs, n_kv, static_cast<int>(blockIdx.x), static_cast<int>(threadIdx.x));
+__global__ void __launch_bounds__(kThreads)
+    paged_decode_kernel(const WorkDesc *descs, int n_kv, const void *k, const void *v, const int32_t *tables,
+                        const void *qkv, const float *inv_freq, DecodeParams p) {
+    decode_item<T, ROWS, FUSED>(p, Preloaded{descs, n_kv, k, v, tables, qkv, inv_freq}, static_cast<int>(blockIdx.x),
+                                static_cast<int>(threadIdx.x));
 }
 
 // The split merge as its own launch: one work-group per (token, head).
@@ -1218,9 +1233,10 @@ hipError_t launch_rows(const DecodeParams &p, int runs, int num_work, hipStream_
     const WorkDesc *descs = p.work && p.work_desc ? reinterpret_cast<const WorkDesc *>(p.work_desc) : nullptr;
     if (start || stop)
         hipExtLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, start, stop, 0,
-                              descs, p.n_kv, p);
+                              descs, p.n_kv, p.k, p.v, p.tables, p.qkv, p.inv_freq, p);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, descs, p.n_kv, p);
+        hipLaunchKernelGGL((paged_decode_kernel<T, ROWS, FUSED>), grid, dim3(kThreads), 0, stream, descs, p.n_kv, p.k,
+                           p.v, p.tables, p.qkv, p.inv_freq, p);
     return hipGetLastError();
 }
 
