@@ -170,6 +170,52 @@ def test_append_far_positions_and_clamp(rng, device):
     assert row.tolist() == [65504.0, -65504.0, 65504.0, 65504.0]
 
 
+
+def test_append_writes_nothing_for_a_slot_outside_the_table(device):
+    """Through the C ABI (the Python wrapper refuses such steps), a token whose position lies past its block
+    table, and one at position -1 with sequence -1, store nothing; a valid token in the same launch stores the
+    same bits, and gets the same q, as when it is appended alone. The kernel looks up every token's block id
+    unguarded, its index clamped into the row (row 0 for a negative sequence)."""
+    import ctypes
+
+    from ember_amd import _lib
+
+    NB, MB = 8, 2
+    rng = np.random.default_rng(11)
+    tables = torch.tensor([[3, 5]], dtype=torch.int32, device=device)
+    inv = torch.from_numpy(oracle.inv_freq(THETA, D)).to(device)
+    ones = torch.ones(D, device=device)
+
+    def run(positions, seqs):
+        T = len(positions)
+        qkv = torch.from_numpy(rng_qkv[:T]).to(device)
+        q_out = torch.zeros((T, H, D), dtype=torch.float16, device=device)
+        kp, vp = _pools(NB, torch.float16, 7.0, device)
+        pos = torch.tensor(positions, dtype=torch.int32, device=device)
+        seq = torch.tensor(seqs, dtype=torch.int32, device=device)
+        a = _lib.QkvArgs()
+        a.qkv, a.q_out, a.k_cache, a.v_cache = qkv.data_ptr(), q_out.data_ptr(), kp.data_ptr(), vp.data_ptr()
+        a.q_norm, a.k_norm, a.bias, a.inv_freq = ones.data_ptr(), ones.data_ptr(), None, inv.data_ptr()
+        a.positions, a.token_seq, a.block_tables = pos.data_ptr(), seq.data_ptr(), tables.data_ptr()
+        a.max_blocks, a.T, a.n_heads, a.n_kv, a.head_dim = MB, T, H, KVH, D
+        a.eps, a.num_blocks, a.dtype = 1e-6, NB, _lib.DTYPE_F16
+        _lib.check(_lib.lib().ember_hip_kv_append(ctypes.byref(a), None), "kv_append")
+        torch.cuda.synchronize()
+        return _host(q_out), _host(kp), _host(vp)
+
+    rng_qkv = (rng.standard_normal((3, W)) * 0.5).astype(np.float16)
+    q3, k3, v3 = run([5, MB * PAGE, -1], [0, 0, -1])
+    q1, k1, v1 = run([5], [0])
+    sentinel = np.full((NB, KVH, PAGE, D), 7.0, np.float16).view(np.uint16)
+    written = np.zeros((NB, KVH, PAGE, D), bool)
+    written[3, :, 5, :] = True
+    for pool3, pool1 in ((k3, k1), (v3, v1)):
+        assert np.array_equal(pool3[~written], sentinel[~written])  # nothing else was written
+        assert np.array_equal(pool3, pool1)                         # the valid token's slot, same bits
+        assert not np.array_equal(pool3[written], sentinel[written])
+    assert np.array_equal(q3[0], q1[0])
+
+
 # ---- paged decode attention ----
 
 def _run_decode(q, kp, vp, step, NB, device, **kw):
