@@ -83,7 +83,7 @@ EXTRA_FLAGS = {
     "paged_decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-mllvm", "-amdgpu-kernarg-preload-count=7"],
     "linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "kv_append.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
-    "prefill_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "prefill_attn.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 

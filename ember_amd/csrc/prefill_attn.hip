@@ -72,10 +72,12 @@ template <int HG>  // query heads per work-group (1 or 2), all of one kv head
 __global__ void __launch_bounds__(kThreadsFor<HG>) prefill_kernel(const int32_t *tile_start, const int32_t *tile_end,
                                                                   const int32_t *tile_seq, const int32_t *positions,
                                                                   const int32_t *block_tables, int n_heads,
-                                                                  int n_kv, int max_blocks, EmberPrefillArgs a,
-                                                                  float scale_log2_arg) {
-    // The leading arguments (what the first loads need) are preloaded into scalar registers at launch
-    // (build.py: -amdgpu-kernarg-preload-count=8); `a` carries the rest.
+                                                                  int n_kv, int max_blocks, float scale_log2_arg,
+                                                                  EmberPrefillArgs a) {
+    // The leading arguments (what the first loads need, and the softmax scale) are preloaded into scalar
+    // registers at launch (build.py: -amdgpu-kernarg-preload-count=9); `a` carries the rest. The scale
+    // loaded from the argument segment instead went out just before the key loop, and its pending scalar
+    // load made the compiler wait for all of a step's first LDS reads (lgkmcnt(0)) at the loop's head.
     // Kernel arguments used inside the key loop are taken into scalar registers once: left as they are, the
     // compiler reloads them from the argument segment every step, and each reload is one more scalar round
     // trip ahead of the step's LDS waits (lgkmcnt counts both).
@@ -415,12 +417,12 @@ hipError_t launch_prefill(const EmberPrefillArgs &a, hipStream_t stream, hipEven
     const float scale_log2 = a.scale * kLog2e;
     if (hg == 2)
         hipExtLaunchKernelGGL(prefill_kernel<2>, grid, dim3(kThreadsFor<2>), 0, stream, start, stop, 0, a.tile_start,
-                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks, a,
-                              scale_log2);
+                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks,
+                              scale_log2, a);
     else
         hipExtLaunchKernelGGL(prefill_kernel<1>, grid, dim3(kThreadsFor<1>), 0, stream, start, stop, 0, a.tile_start,
-                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks, a,
-                              scale_log2);
+                              a.tile_end, a.tile_seq, a.positions, a.block_tables, a.n_heads, a.n_kv, a.max_blocks,
+                              scale_log2, a);
     return hipGetLastError();
 }
 
