@@ -125,14 +125,23 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     const uint32_t pieces = kw / 8;  // 16-byte pieces per staged row
     // The f32 residual this work-group's epilogue adds to, read now so that
     // its latency hides behind the W loads (wave mt ends with token tile mt).
-    float prev[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    // A lane's four outputs (features n0 + 4 g .. + 3 of one token) are
+    // adjacent: with a 16-byte aligned C, ldc a multiple of 4 and the whole
+    // tile inside N, they go out as one store (and come in as one load).
+    const bool vec_out = ((reinterpret_cast<uintptr_t>(C) & 15) | (ldc & 3)) == 0 && n0 + 16 <= N;
+    f32x4 prev = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (EP == EMBER_EPILOGUE_ADD_F32) {
         const int tok = 16 * wave + c;
         if (wave < MT && tok < M) {
+            const float *row = static_cast<const float *>(C) + static_cast<int64_t>(tok) * ldc;
+            if (vec_out) {
+                prev = *reinterpret_cast<const f32x4 *>(row + n0 + 4 * g);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int n = n0 + 4 * g + i;
-                if (n < N) prev[i] = static_cast<const float *>(C)[static_cast<int64_t>(tok) * ldc + n];
+                for (int i = 0; i < 4; i++) {
+                    const int n = n0 + 4 * g + i;
+                    if (n < N) prev[i] = row[n];
+                }
             }
         }
     }
@@ -325,6 +334,18 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
             if (n + 1 < N)
                 static_cast<f16 *>(C)[static_cast<int64_t>(tok) * ldc + n / 2] =
                     static_cast<f16>(clamp_half(silu(sum[i]) * sum[i + 1]));
+        }
+    } else if (vec_out) {
+        const int64_t at = static_cast<int64_t>(tok) * ldc + n0 + 4 * g;
+        if constexpr (EP == EMBER_EPILOGUE_STORE_F16) {
+            f16x4 h;
+#pragma unroll
+            for (int i = 0; i < 4; i++) h[i] = static_cast<f16>(clamp_half(sum[i]));
+            *reinterpret_cast<f16x4 *>(static_cast<f16 *>(C) + at) = h;
+        } else if constexpr (EP == EMBER_EPILOGUE_STORE_F32) {
+            *reinterpret_cast<f32x4 *>(static_cast<float *>(C) + at) = sum;
+        } else {
+            *reinterpret_cast<f32x4 *>(static_cast<float *>(C) + at) = prev + sum;
         }
     } else {
 #pragma unroll

@@ -775,6 +775,26 @@ def test_gemv_saturates_f16_outputs(device):
     assert c.float().cpu().numpy()[0, :2].tolist() == [65504.0, -65504.0]
 
 
+@pytest.mark.parametrize("ep", [0, 1, 2])
+def test_gemv_vector_and_scalar_stores_agree(device, ep):
+    """A 16-byte aligned output whose row length is a multiple of 4 takes each lane's four outputs in one store
+    (and, adding into f32, one load); 130 features (rows of 130) take them one at a time. The first 128
+    features are the same bits either way."""
+    rng = np.random.default_rng(130 + ep)
+    a = torch.from_numpy(rng.standard_normal((20, 256)).astype(np.float16)).to(device)
+    w = torch.from_numpy((rng.standard_normal((132, 256)) * 0.05).astype(np.float16)).to(device)
+    f32 = ep != 0
+    start = torch.from_numpy(rng.standard_normal((20, 132)).astype(np.float32)).to(device)
+    outs = []
+    for n in (132, 130):
+        c = start[:, :n].clone(memory_format=torch.contiguous_format) if f32 else torch.empty((20, n), dtype=torch.float16, device=device)
+        K.gemv(a, w[:n].contiguous(), c, ep)
+        outs.append(c[:, :128])
+    torch.cuda.synchronize()
+    view = torch.int32 if f32 else torch.int16
+    assert torch.equal(outs[0].view(view), outs[1].view(view))
+
+
 @pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (3, 4096), (2, 5120)])
 def test_rmsnorm_rows_matches_oracle(device, R, hidden):
     """f16 outputs within one f16 ulp of the oracle's f32 rows (cpu_backend.cpp:34-39; the GPU's double sum of
