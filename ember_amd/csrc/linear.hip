@@ -582,11 +582,18 @@ constexpr int kNormThreads = 256;
 constexpr int kNormPer = 16;  // elements of a row per thread held in registers (hidden <= 4096)
 
 // One work-group per row: the sum of squares in double, reduced in a fixed
-// order (each thread's elements t, t + 256, ..., then the wave, then the
-// waves in order). Rows up to kNormThreads * kNormPer wide keep the thread's
-// elements of x and w in registers, all loaded up front: one memory round
-// trip per row instead of one for x and another for w and x again.
-template <bool HELD>
+// order (each thread's elements in the order it holds them, then the wave,
+// then the waves in order). Rows up to kNormThreads * kNormPer wide keep the
+// thread's elements of x and w in registers, all loaded up front: one memory
+// round trip per row instead of one for x and another for w and x again.
+// FORM: kNormLoop (any width: elements t, t + 256, ... re-read for the
+// output), kNormHeld (held, elements t, t + 256, ...), kNormHeld4 (held, a
+// width that is a multiple of 4 with 16-byte aligned rows: runs of 4
+// adjacent elements 4 (t + 256 j) .. + 3, each one load of x, one of w and
+// one 8-byte store).
+constexpr int kNormLoop = 0, kNormHeld = 1, kNormHeld4 = 2;
+
+template <int FORM>
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float *__restrict__ x,
                                                                     const int32_t *__restrict__ rows, int hidden,
                                                                     const float *__restrict__ w, float eps,
@@ -595,9 +602,24 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float 
     const int r = static_cast<int>(blockIdx.x), t = static_cast<int>(threadIdx.x);
     const float *xr = x + static_cast<int64_t>(rows ? rows[r] : r) * hidden;
     f16 *o = out + static_cast<int64_t>(r) * hidden;
+    constexpr bool HELD = FORM != kNormLoop;
     float xv[HELD ? kNormPer : 1], wv[HELD ? kNormPer : 1];
     double ss = 0.0;
-    if constexpr (HELD) {
+    if constexpr (FORM == kNormHeld4) {
+#pragma unroll
+        for (int j = 0; j < kNormPer / 4; j++) {
+            const int i = 4 * (t + j * kNormThreads);
+            const f32x4 xq = i < hidden ? *reinterpret_cast<const f32x4 *>(xr + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            const f32x4 wq = i < hidden ? *reinterpret_cast<const f32x4 *>(w + i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                xv[4 * j + e] = xq[e];
+                wv[4 * j + e] = wq[e];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kNormPer; j++) ss += static_cast<double>(xv[j]) * xv[j];  // + 0.0 past the row: exact
+    } else if constexpr (FORM == kNormHeld) {
 #pragma unroll
         for (int j = 0; j < kNormPer; j++) {
             const int i = t + j * kNormThreads;
@@ -615,7 +637,17 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_rows_kernel(const float 
     double total = part[0];
     for (int v = 1; v < kNormThreads / kWave; v++) total += part[v];
     const float scale = static_cast<float>(1.0 / sqrt(total / hidden + static_cast<double>(eps)));
-    if constexpr (HELD) {
+    if constexpr (FORM == kNormHeld4) {
+#pragma unroll
+        for (int j = 0; j < kNormPer / 4; j++) {
+            const int i = 4 * (t + j * kNormThreads);
+            if (i >= hidden) continue;
+            f16x4 h;
+#pragma unroll
+            for (int e = 0; e < 4; e++) h[e] = static_cast<f16>(clamp_half(wv[4 * j + e] * (xv[4 * j + e] * scale)));
+            *reinterpret_cast<f16x4 *>(o + i) = h;
+        }
+    } else if constexpr (FORM == kNormHeld) {
 #pragma unroll
         for (int j = 0; j < kNormPer; j++) {
             const int i = t + j * kNormThreads;
@@ -650,12 +682,13 @@ hipError_t launch_gemv(const EmberGemvArgs &a, hipStream_t stream) {
 }
 
 hipError_t launch_rmsnorm_rows(const EmberNormArgs &a, hipStream_t stream) {
-    if (a.hidden <= kNormThreads * kNormPer)
-        hipLaunchKernelGGL(rmsnorm_rows_kernel<true>, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream,
-                           a.x, a.rows, a.hidden, a.w, a.eps, static_cast<f16 *>(a.out));
-    else
-        hipLaunchKernelGGL(rmsnorm_rows_kernel<false>, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream,
-                           a.x, a.rows, a.hidden, a.w, a.eps, static_cast<f16 *>(a.out));
+    const bool aligned = a.hidden % 4 == 0 && ((reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.w)) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.out) & 7) == 0;
+    const auto kernel = a.hidden > kNormThreads * kNormPer ? rmsnorm_rows_kernel<kNormLoop>
+                        : aligned                          ? rmsnorm_rows_kernel<kNormHeld4>
+                                                           : rmsnorm_rows_kernel<kNormHeld>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(a.R)), dim3(kNormThreads), 0, stream, a.x, a.rows, a.hidden,
+                       a.w, a.eps, static_cast<f16 *>(a.out));
     return hipGetLastError();
 }
 

@@ -795,10 +795,11 @@ def test_gemv_vector_and_scalar_stores_agree(device, ep):
     assert torch.equal(outs[0].view(view), outs[1].view(view))
 
 
-@pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (3, 4096), (2, 5120)])
+@pytest.mark.parametrize("R,hidden", [(1, 2048), (32, 2048), (5, 1000), (4, 1002), (3, 4096), (2, 5120)])
 def test_rmsnorm_rows_matches_oracle(device, R, hidden):
     """f16 outputs within one f16 ulp of the oracle's f32 rows (cpu_backend.cpp:34-39; the GPU's double sum of
-    squares runs in another order), through a row list."""
+    squares runs in another order), through a row list. Widths that are a multiple of 4 take runs of 4 adjacent
+    elements per load and store, 1002 one element at a time, 5120 the form that re-reads its row."""
     rng = np.random.default_rng(R * 100 + hidden)
     x = rng.standard_normal((R + 2, hidden)).astype(np.float32) * 3
     w = (1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32)
