@@ -327,7 +327,14 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     const int tok = 16 * mt + c;
     if (tok >= M) return;
     if constexpr (EP == EMBER_EPILOGUE_SILU_MUL) {
-        // gate rows even, up rows odd: this lane holds the pairs (4g, 4g+1), (4g+2, 4g+3)
+        // gate rows even, up rows odd: this lane holds the pairs (4g, 4g+1), (4g+2, 4g+3),
+        // whose outputs are adjacent: one 4-byte store when vec_out holds
+        if (vec_out) {
+            const f16x2 h = {static_cast<f16>(clamp_half(silu(sum[0]) * sum[1])),
+                             static_cast<f16>(clamp_half(silu(sum[2]) * sum[3]))};
+            *reinterpret_cast<f16x2 *>(static_cast<f16 *>(C) + static_cast<int64_t>(tok) * ldc + (n0 + 4 * g) / 2) = h;
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
             const int n = n0 + 4 * g + i;

@@ -775,21 +775,25 @@ def test_gemv_saturates_f16_outputs(device):
     assert c.float().cpu().numpy()[0, :2].tolist() == [65504.0, -65504.0]
 
 
-@pytest.mark.parametrize("ep", [0, 1, 2])
+@pytest.mark.parametrize("ep", [0, 1, 2, 3])
 def test_gemv_vector_and_scalar_stores_agree(device, ep):
-    """A 16-byte aligned output whose row length is a multiple of 4 takes each lane's four outputs in one store
-    (and, adding into f32, one load); 130 features (rows of 130) take them one at a time. The first 128
-    features are the same bits either way."""
+    """A 16-byte aligned output whose row length is a multiple of 4 takes each lane's outputs in one store (and,
+    adding into f32, one load); 130 features (rows of 130, or 65 after the SiLU pairs) take them one at a time.
+    The first 128 features (64 SiLU outputs) are the same bits either way."""
+    from ember_amd import _lib
     rng = np.random.default_rng(130 + ep)
+    silu = ep == _lib.EPILOGUE_SILU_MUL
     a = torch.from_numpy(rng.standard_normal((20, 256)).astype(np.float16)).to(device)
-    w = torch.from_numpy((rng.standard_normal((132, 256)) * 0.05).astype(np.float16)).to(device)
-    f32 = ep != 0
-    start = torch.from_numpy(rng.standard_normal((20, 132)).astype(np.float32)).to(device)
+    w = torch.from_numpy((rng.standard_normal((136, 256)) * 0.05).astype(np.float16)).to(device)
+    f32 = ep in (_lib.EPILOGUE_STORE_F32, _lib.EPILOGUE_ADD_F32)
+    start = torch.from_numpy(rng.standard_normal((20, 136)).astype(np.float32)).to(device)
     outs = []
-    for n in (132, 130):
-        c = start[:, :n].clone(memory_format=torch.contiguous_format) if f32 else torch.empty((20, n), dtype=torch.float16, device=device)
+    for n in ((136, 130) if silu else (132, 130)):
+        cols = n // 2 if silu else n
+        c = start[:, :cols].clone(memory_format=torch.contiguous_format) if f32 else \
+            torch.empty((20, cols), dtype=torch.float16, device=device)
         K.gemv(a, w[:n].contiguous(), c, ep)
-        outs.append(c[:, :128])
+        outs.append(c[:, :64 if silu else 128])
     torch.cuda.synchronize()
     view = torch.int32 if f32 else torch.int16
     assert torch.equal(outs[0].view(view), outs[1].view(view))
