@@ -88,6 +88,19 @@ def test_token_probs_match_the_host_distribution(logits):
     assert got[3] == 0.0 and got[4] == 1.0 and got[5] == 0.0 and got[6] == 0.0 and got[7] == 0.0
 
 
+@pytest.mark.parametrize("V", [4999, 5000])
+def test_rows_of_any_length_and_ties_across_threads(logits, V):
+    """Rows of 4999 and 5000 logits: the draws are the host sampler's, and greedy takes the first largest of a tie
+    whose tokens lie in different threads' elements."""
+    x = logits[:V].copy()
+    x[[6, 9, 4000]] = x.max() + 1.0
+    host = [oracle.sample(x, 0.8, 0.9, 40, 0.0, seed=5, counter=c) for c in range(64)]
+    rows = [(0.8, 0.9, 40, 0.0, 5, c) for c in range(64)] + [(0.0, 1.0, 0, 0.0, 0, 0)]
+    got = gpu_sample(np.tile(x, (65, 1)), rows)
+    assert got[:64] == host
+    assert got[64] == 6
+
+
 def test_full_vocabulary_rows_and_batch_invariance():
     """Qwen3's 151,936-token vocabulary: each row's token does not depend on the other rows of the launch."""
     rng = np.random.default_rng(11)
