@@ -39,6 +39,7 @@ constexpr int kGemvUnroll = 8;  // k steps whose W loads are in flight together,
 constexpr int kGemvTargetGroups = 256;  // work-groups a launch should reach: one per CU
 constexpr int kGemvMaxSplit = 4;
 constexpr int kGemvSplitAbove = 4096;  // K slices at most this wide are not split further
+constexpr int kGemvEarlyW = 2;  // a staged first round's W loads issued before its activation copies
 // Packed W (ember_hip_gemv_pack): for each 16-feature tile and 32-wide k step,
 // the MFMA A operand as the 64 lanes take it, 8 halves per lane (lane 16 g + c:
 // row 16 tile + c, k 32 step + 8 g ..): one contiguous 1 KiB per load
@@ -234,16 +235,20 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     };
     auto first_round = [&](auto unroll) {
         constexpr int U = decltype(unroll)::value;
-        if constexpr (staged) issue_stage();
-        __builtin_amdgcn_sched_barrier(0);
+        constexpr int E = staged ? (U < kGemvEarlyW ? U : kGemvEarlyW) : 0;  // W loads ahead of the copies
         f16x8 wv[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) wv[u] = load_w(w + wstep * (s + u * stride));
+        for (int u = 0; u < E; u++) wv[u] = load_w(w + wstep * (s + u * stride));
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (staged) issue_stage();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = E; u < U; u++) wv[u] = load_w(w + wstep * (s + u * stride));
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (staged) {
-            // s_waitcnt vmcnt(U), expcnt and lgkmcnt left alone: every copy
-            // (issued before the U W loads) has landed
-            __builtin_amdgcn_s_waitcnt(0x0F70 | U);
+            // s_waitcnt vmcnt(U - E), expcnt and lgkmcnt left alone: every
+            // copy (issued before the last U - E W loads) has landed
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (U - E));
             stage_barrier();
         }
         compute(unroll, wv, s, stride);
