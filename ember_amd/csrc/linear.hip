@@ -39,7 +39,12 @@ constexpr int kGemvUnroll = 8;  // k steps whose W loads are in flight together,
 constexpr int kGemvTargetGroups = 256;  // work-groups a launch should reach: one per CU
 constexpr int kGemvMaxSplit = 4;
 constexpr int kGemvSplitAbove = 4096;  // K slices at most this wide are not split further
-constexpr int kGemvEarlyW = 2;  // a staged first round's W loads issued before its activation copies
+// A staged first round's W loads issued before its activation copies: one
+// for a single 16-token tile (8 KiB of copies per wave at K 2048), two for
+// more (16 KiB at two tiles). Measured at K 2048: qkv (two tiles) 6.32 us
+// with none, 6.14 with one, 5.96 with two, 6.02 with three, 6.20 with four;
+// o (one tile) 4.70, 4.65, 4.71, 4.77, 4.83.
+constexpr int gemv_early_w(int mt) { return mt == 1 ? 1 : 2; }
 // Packed W (ember_hip_gemv_pack): for each 16-feature tile and 32-wide k step,
 // the MFMA A operand as the 64 lanes take it, 8 halves per lane (lane 16 g + c:
 // row 16 tile + c, k 32 step + 8 g ..): one contiguous 1 KiB per load
@@ -235,7 +240,7 @@ __global__ void __launch_bounds__(kGemvThreads) gemv_kernel(const f16 *__restric
     };
     auto first_round = [&](auto unroll) {
         constexpr int U = decltype(unroll)::value;
-        constexpr int E = staged ? (U < kGemvEarlyW ? U : kGemvEarlyW) : 0;  // W loads ahead of the copies
+        constexpr int E = staged ? (U < gemv_early_w(MT) ? U : gemv_early_w(MT)) : 0;  // W loads ahead of the copies
         f16x8 wv[U];
 #pragma unroll
         for (int u = 0; u < E; u++) wv[u] = load_w(w + wstep * (s + u * stride));
